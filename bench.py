@@ -1,0 +1,278 @@
+#!/usr/bin/env python
+"""Benchmark of the tensorjit hip backend on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Prints ONE JSON line.  The headline (``value``) is BASELINE.json's fused
+elementwise/broadcast chain (config 2): ``y = gelu(x*a+b) * sigmoid(c) + x`` over
+fp32 x, c [16384, 4096] and a, b [4096], compiled by ``tj.jit`` into one kernel;
+a step is one call of the compiled function on inputs already resident in HBM,
+and ``value`` is algorithmic HBM bytes per step / wall time per step (GB/s).
+
+``roofline`` is that kernel's achieved bandwidth (algorithmic bytes / average
+kernel duration from hipEvents on the stream the kernel runs on) against the
+8 TB/s HBM3E peak; ``traffic`` is the measured HBM bytes per launch from the
+committed rocprofv3 counter summary when one exists for this workload.
+``cpu_baseline`` is the CPU oracle (the C/OpenMP restatement of the reference
+``c`` backend) on the same workload.  ``secondary`` carries the other
+BASELINE.json configurations (row kernels, GEMMs, MLP block per-call time).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "mlir-gpu-kernel-compiler_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+METRIC = "HBM GB/s (eltwise/row) + bf16 GEMM TFLOPS, % of peak; MLP block us/call"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _fn_c2(x, a, b, c):
+    import tensorjit as tj
+
+    return tj.gelu(x * a + b) * tj.sigmoid(c) + x
+
+
+def _fn_ln(x, g):
+    import tensorjit as tj
+
+    return tj.layer_norm(x, g)
+
+
+def _fn_rms(x, g):
+    import tensorjit as tj
+
+    return tj.rms_norm(x, g)
+
+
+def _fn_softmax(s):
+    import tensorjit as tj
+
+    return tj.softmax(s)
+
+
+def _fn_gemm(x, w, b):
+    import tensorjit as tj
+
+    return tj.gelu(tj.linear(x, w, b))
+
+
+def _fn_mlp(x, g, w1, b1, w2, b2):
+    import tensorjit as tj
+
+    return x + tj.linear(tj.gelu(tj.linear(tj.layer_norm(x, g), w1, b1)), w2, b2)
+
+
+def c2_inputs(torch, dt, dev):
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(16384, 4096, device=dev, generator=g)
+    a = torch.randn(4096, device=dev, generator=g)
+    b = torch.randn(4096, device=dev, generator=g)
+    c = torch.rand(16384, 4096, device=dev, generator=g) * 8 - 4
+    return [t.to(dt) for t in (x, a, b, c)]
+
+
+def timed_steps(torch, fn, args, steps, warmup):
+    for _ in range(warmup):
+        fn(*args)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn(*args)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+def kernel_ms(f, args, k=0, iters=20):
+    cp = f.compiled(*args)
+    return cp.kernel_time_ms(k, *args, warmup=3, iters=iters)
+
+
+def load_traffic(workload: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+    p = ROOT / "profiles" / "hbm_traffic.json"
+    try:
+        data = json.loads(p.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get(workload)
+    return None if entry is None else entry.get("traffic_bytes")
+
+
+def cpu_baseline(torch, args_gpu, nbytes, seconds):
+    import oracle
+
+    host = [t.float().cpu() for t in args_gpu]
+    prog = oracle.compile_program(oracle.lower_f32(_fn_c2, *[t.shape for t in host]))
+    prog(*host)                               # warm (page-in, OpenMP pool)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        prog(*host)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 200:
+            break
+    per = el / n
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    return {"value": round(nbytes / per / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full config-2 fp32 workload [16384,4096] x {n} calls ({el:.1f} s), "
+                      f"oracle C/OpenMP restatement of the reference c backend, {cores} threads",
+            "ms_per_call": round(per * 1e3, 3)}
+
+
+def secondary(torch, dev, quick):
+    import tensorjit as tj
+
+    out = {}
+
+    def row(name, fn, args, nbytes):
+        f = tj.jit(fn)
+        f(*args)
+        ms = kernel_ms(f, args)
+        wall = timed_steps(torch, f, args, 20, 3)
+        out[name] = {"GB/s": round(nbytes / ms / 1e6, 1), "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                     "kernel_us": round(ms * 1e3, 2), "us_per_call": round(wall * 1e3, 2), "bytes": nbytes}
+        log(f"{name}: {out[name]}")
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    # config 2 in bf16
+    args = c2_inputs(torch, bf, dev)
+    row("c2_eltwise_bf16", _fn_c2, args, 3 * 16384 * 4096 * 2 + 2 * 4096 * 2)
+    del args
+    # config 3: rows
+    x = torch.randn(65536, 4096, device=dev, generator=gen).to(bf)
+    gn = (1 + 0.1 * torch.randn(4096, device=dev, generator=gen)).to(bf)
+    nb = 2 * 65536 * 4096 * 2 + 4096 * 2
+    row("c3_layernorm_bf16", _fn_ln, [x, gn], nb)
+    row("c3_rmsnorm_bf16", _fn_rms, [x, gn], nb)
+    del x
+    s = torch.randn(65536, 2048, device=dev, generator=gen) * 3
+    row("c3_softmax_f32", _fn_softmax, [s], 2 * 65536 * 2048 * 4)
+    del s
+    if quick:
+        return out
+    # config 4: GEMMs
+
+    def gemm(name, M, N, K, dt, peak):
+        xg = torch.randn(M, K, device=dev, generator=gen).to(dt)
+        wg = (0.02 * torch.randn(N, K, device=dev, generator=gen)).to(dt)
+        bg = (0.02 * torch.randn(N, device=dev, generator=gen)).to(dt)
+        f = tj.jit(_fn_gemm)
+        f(xg, wg, bg)
+        ms = kernel_ms(f, [xg, wg, bg], iters=10)
+        wall = timed_steps(torch, f, [xg, wg, bg], 10, 2)
+        flops = 2.0 * M * N * K
+        esz = 2 if dt == bf else 4
+        nbytes = (M * K + N * K + N + M * N) * esz
+        cfg = f.compiled(xg, wg, bg).matmul_configs[0].as_dict()
+        out[name] = {"TFLOP/s": round(flops / ms / 1e9, 1), "frac_peak": round(flops / ms / 1e9 / peak, 4),
+                     "GB/s": round(nbytes / ms / 1e6, 1), "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                     "kernel_us": round(ms * 1e3, 2), "us_per_call": round(wall * 1e3, 2), "tile": cfg}
+        log(f"{name}: {out[name]}")
+
+    gemm("c4_gemm_bf16_8192", 8192, 8192, 8192, bf, BF16_PEAK_TFLOPS)
+    gemm("c4_gemm_f32_4096", 4096, 4096, 4096, torch.float32, FP32_PEAK_TFLOPS)
+    gemm("c4_skinny_bf16_m16", 16, 8192, 8192, bf, BF16_PEAK_TFLOPS)
+    # config 1: MLP block per-call time (hip eager launches and hipGraph replay)
+    shapes = [(512, 768), (768,), (3072, 768), (3072,), (768, 3072), (768,)]
+    margs = [torch.randn(s, device=dev, generator=gen) * (1 if i < 2 else 0.02) for i, s in enumerate(shapes)]
+    res = {}
+    for mode in ("0", "1"):
+        os.environ["TENSORJIT_HIP_GRAPH"] = mode
+        f = tj.jit(_fn_mlp)
+        f(*margs)
+        res["graph" if mode == "1" else "eager"] = round(timed_steps(torch, f, margs, 200, 20) * 1e3, 2)
+    os.environ["TENSORJIT_HIP_GRAPH"] = "1"
+    out["c1_mlp_f32_us_per_call"] = res
+    log(f"c1_mlp: {res}")
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="skip the GEMM / MLP secondaries")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every box has one MI355X); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import tensorjit as tj
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"device {torch.cuda.get_device_name(0)}")
+
+    args = c2_inputs(torch, torch.float32, dev)
+    nbytes = 3 * 16384 * 4096 * 4 + 2 * 4096 * 4       # read x, c, a, b; write y
+    f = tj.jit(_fn_c2)
+    f(*args)
+    cp = f.compiled(*args)
+    assert cp.num_kernels == 1 and cp.backend == "hip"
+    torch.cuda.synchronize()
+    ms_step = timed_steps(torch, f, args, a.steps, a.warmup)
+    kms = kernel_ms(f, args, iters=max(20, a.steps))
+    value = nbytes / (ms_step / 1e3) / 1e9
+    achieved = nbytes / (kms / 1e3) / 1e9
+    log(f"c2 fp32: {value:.1f} GB/s per step ({ms_step * 1e3:.1f} us), kernel {kms * 1e3:.1f} us = {achieved:.1f} GB/s")
+    workload = "c2_eltwise_f32"
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch.randn / rand, BASELINE.json config 2 distributions)",
+        "config": {"workload": "config 2: y = gelu(x*a+b)*sigmoid(c)+x, fp32 x,c[16384,4096], a,b[4096]; "
+                               "one fused hip kernel via tj.jit", "numel": 16384 * 4096,
+                   "algorithmic_bytes": nbytes, "kernels": cp.num_kernels,
+                   "hip_graph": cp.use_graph},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(workload),
+                     "kernel_us": round(kms * 1e3, 2), "kernel": cp.launches[0].name},
+    }
+    if not a.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(torch, args, nbytes, a.cpu_seconds)
+        log(f"cpu baseline: {line['cpu_baseline']}")
+    else:
+        line["cpu_baseline"] = None
+    del args
+    if not a.no_secondary:
+        line["secondary"] = secondary(torch, dev, a.quick)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,308 @@
+"""hip backend: fused kernel program -> gfx950 HIP C++ -> hipRTC -> C-ABI executor.
+
+``compile_program(program, device, tune)`` is the backend entry point that
+``tensorjit.compiler.compile_graph`` dispatches to for ``backend="hip"``,
+in the place of the reference's ``cuda_backend.compile_program``
+(``tensorjit/backends/cuda_backend.py:556-557``).  It returns a
+``HipProgram`` with the executor protocol of the reference's
+``CudaProgram`` (``tensorjit/backends/cuda_backend.py:459-553``): callable on
+torch tensors, ``num_kernels``, ``source`` (HIP), ``launches``, ``plan``,
+``stats`` (``calls`` / ``graph_replays``), ``matmul_configs``.
+
+Everything below ``HipProgram.__call__`` is native: the pointer tables go to
+``libtjhip.so`` (``tj_hip_program_run`` / ``tj_hip_program_replay``), which
+launches the kernels on torch's current HIP stream.  There is no other
+execution path; a missing library or GPU raises.
+"""
+from __future__ import annotations
+
+import logging
+import math
+import os
+import threading
+
+import torch
+
+from ..ir import DType, Node
+from ..passes import Kernel, Program
+from ..passes.memory_planner import MemoryPlan, plan_memory
+from ..runtime import hip as rt
+from ..runtime.autotune import HIP_CANDIDATES, HIP_F32_CANDIDATES, MatmulConfig, autotune, cost_model
+from ..runtime.cache import AutotuneStore, CodeObjectCache
+from ..runtime.dtypes import TORCH_DTYPE
+from ..runtime.pool import BufferPool
+from .hip_gemm import compute_dtype, config_ok, gen_matmul, matmul_dims
+from .hip_kernels import KernelGen, Launch, gen_copy, gen_elementwise, gen_row
+from .hip_prelude import PRELUDE
+
+log = logging.getLogger("tensorjit")
+
+DEFAULT_ARCH = "gfx950"
+NO_PACKED_FP32 = ("-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops")
+COMPILE_OPTS = ("-O3", "-std=c++17", *NO_PACKED_FP32)
+
+
+# ---------------------------------------------------------------------------
+# tile selection
+# ---------------------------------------------------------------------------
+
+
+def _candidates(dt: DType) -> list[MatmulConfig]:
+    return [c for c in (HIP_F32_CANDIDATES if dt == DType.f32 else HIP_CANDIDATES) if config_ok(c, dt)]
+
+
+def matmul_key(k: Kernel, arch: str) -> str:
+    mm = k.anchor
+    M, N, K, tb = matmul_dims(mm)
+    batch = math.prod(mm.shape[:-2]) if len(mm.shape) > 2 else 1
+    dt = compute_dtype(mm)
+    return f"hip|{arch}|matmul|{batch}x{M}x{N}x{K}|{dt.value}|tb{int(tb)}|epi{len(k.nodes) - 1}"
+
+
+def analytic_config(k: Kernel) -> MatmulConfig:
+    mm = k.anchor
+    M, N, K, _ = matmul_dims(mm)
+    batch = math.prod(mm.shape[:-2]) if len(mm.shape) > 2 else 1
+    dt = compute_dtype(mm)
+    kind = "hip_f32" if dt == DType.f32 else "hip"
+    return min(_candidates(dt), key=lambda c: cost_model(c, M, N, K, kind, batch))
+
+
+# ---------------------------------------------------------------------------
+# code generation
+# ---------------------------------------------------------------------------
+
+
+def generate_kernel(k: Kernel, idx: int, cfg: MatmulConfig | None = None) -> tuple[str, Launch]:
+    g = KernelGen.of(k, idx)
+    if k.kind == "elementwise":
+        return gen_elementwise(g)
+    if k.kind == "copy":
+        return gen_copy(g)
+    if k.kind == "row":
+        return gen_row(g, k.stages, tuple(k.rows), k.n)  # type: ignore[attr-defined]
+    if k.kind == "reduce":
+        x = k.anchor.inputs[0]
+        return gen_row(g, [k], tuple(x.shape[:-1]), x.shape[-1])
+    if k.kind == "matmul":
+        return gen_matmul(g, cfg or analytic_config(k))
+    raise NotImplementedError(k.kind)
+
+
+def generate(program: Program, configs: dict[int, MatmulConfig] | None = None) -> tuple[str, list[Launch]]:
+    """HIP source of the whole program (prelude + one ``extern "C"`` kernel per fused kernel)."""
+    configs = configs or {}
+    sources, launches = [PRELUDE], []
+    for idx, k in enumerate(program.kernels):
+        src, launch = generate_kernel(k, idx, configs.get(idx))
+        sources.append(src)
+        launches.append(launch)
+    return "\n\n".join(sources), launches
+
+
+# ---------------------------------------------------------------------------
+# compilation
+# ---------------------------------------------------------------------------
+
+_compile_lock = threading.Lock()
+
+
+def arch_of(device_index: int | None) -> str:
+    forced = os.environ.get("TENSORJIT_HIP_ARCH")
+    if forced:
+        return forced
+    if device_index is None:
+        return DEFAULT_ARCH
+    return rt.device_info(device_index).arch.decode().split(":")[0]
+
+
+def compile_source(source: str, arch: str, name: str = "tensorjit.hip") -> bytes:
+    """hipRTC compile with an on-disk code-object cache (source hash, target, ABI)."""
+    opts = (f"--offload-arch={arch}", *COMPILE_OPTS)
+    cache = CodeObjectCache(arch, f"hiprtc-abi{rt.ABI_VERSION}")
+    code = cache.get(source, opts)
+    if code is not None:
+        return code
+    with _compile_lock:
+        code = rt.compile_source(source, name, opts)
+    cache.put(source, opts, code)
+    return code
+
+
+# ---------------------------------------------------------------------------
+# executor
+# ---------------------------------------------------------------------------
+
+
+class HipProgram:
+    """A compiled program bound to one GPU (see module docstring for the protocol)."""
+
+    def __init__(self, program: Program, device: str | torch.device = "cuda", use_graph: bool | None = None,
+                 tune: bool = True):
+        self.program = program
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError(f"the hip backend runs on ROCm GPU tensors (device 'cuda'), got {self.device}")
+        if not torch.cuda.is_available():
+            raise rt.HipError("the hip backend needs a ROCm GPU; torch.cuda.is_available() is False")
+        self.device_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        self.backend = "hip"
+        self.arch = arch_of(self.device_index)
+        self.plan: MemoryPlan = plan_memory(program)
+        self.matmul_configs: dict[int, MatmulConfig] = {}
+        self._tuned_ms: dict[int, float] = {}
+        self._native: rt.NativeHipProgram | None = None
+        g = program.graph
+        self._input_index = {id(n): i for i, n in enumerate(g.inputs)}
+        returned = {id(program.resolve(o)) for o in g.outputs}
+        self._out_nodes: list[Node] = []
+        for k in program.kernels:
+            for o in k.outputs:
+                if id(o) in returned and all(o is not x for x in self._out_nodes):
+                    self._out_nodes.append(o)
+        self._out_index = {id(o): j for j, o in enumerate(self._out_nodes)}
+        self._args = [[self._ref(i) for i in k.inputs] + [self._ref(o) for o in k.outputs] for k in program.kernels]
+        self._out_specs = [(tuple(o.shape), TORCH_DTYPE[o.dtype]) for o in self._out_nodes]
+
+        for idx, k in enumerate(program.kernels):
+            if k.kind == "matmul":
+                self.matmul_configs[idx] = self._pick_config(k, idx, tune)
+        self.source, self.launches = generate(program, self.matmul_configs)
+        self.code = compile_source(self.source, self.arch)
+        self._native = self._load(self.code, self.launches, self._args)
+
+        self.pool = BufferPool()
+        env = os.environ.get("TENSORJIT_HIP_GRAPH", "1") == "1"
+        self.use_graph = env if use_graph is None else use_graph
+        self.stats = {"calls": 0, "graph_replays": 0}
+
+    # -- construction helpers -------------------------------------------------------
+    def _ref(self, n: Node) -> tuple[int, int]:
+        src = self.program.resolve(n)
+        if id(src) in self._input_index:
+            return rt.INPUT, self._input_index[id(src)]
+        if id(src) in self._out_index:
+            return rt.OUTPUT, self._out_index[id(src)]
+        off = self.plan.offset(src)
+        if off is None:
+            raise RuntimeError(f"{n.name} has no storage (not an input, output or planned intermediate)")
+        return rt.ARENA, off
+
+    def _load(self, code: bytes, launches: list[Launch], args) -> rt.NativeHipProgram:
+        return rt.NativeHipProgram(self.device_index, code, [l.name for l in launches],
+                                   [(l.grid, l.block, l.shared) for l in launches], args,
+                                   self.plan.arena_bytes, len(self.program.graph.inputs), len(self._out_nodes))
+
+    def _pick_config(self, k: Kernel, idx: int, tune: bool) -> MatmulConfig:
+        store = AutotuneStore()
+        key = matmul_key(k, self.arch)
+        cached = store.get(key)
+        if cached is not None:
+            cfg = MatmulConfig.from_dict(cached["config"])
+            if config_ok(cfg, compute_dtype(k.anchor)):
+                return cfg
+        if not tune or os.environ.get("TENSORJIT_NO_AUTOTUNE") == "1":
+            return analytic_config(k)
+        return self._autotune(k, idx, key, store)
+
+    def _autotune(self, k: Kernel, idx: int, key: str, store: AutotuneStore) -> MatmulConfig:
+        """Time the cost model's best candidates on random buffers of the kernel's shapes."""
+        mm = k.anchor
+        M, N, K, _ = matmul_dims(mm)
+        batch = math.prod(mm.shape[:-2]) if len(mm.shape) > 2 else 1
+        dt = compute_dtype(mm)
+        kind = "hip_f32" if dt == DType.f32 else "hip"
+        dev = self.device
+        ins = [torch.randn(i.shape, device=dev).to(TORCH_DTYPE[i.dtype]) for i in k.inputs]
+        outs = [torch.empty(o.shape, device=dev, dtype=TORCH_DTYPE[o.dtype]) for o in k.outputs]
+        single = Program(self.program.graph, [k], {})
+        args = [[(rt.INPUT, j) for j in range(len(k.inputs))] + [(rt.OUTPUT, j) for j in range(len(k.outputs))]]
+        stream = torch.cuda.current_stream(dev).cuda_stream
+
+        def build(cfg: MatmulConfig):
+            src, launch = generate(single, {0: cfg})
+            code = compile_source(src, self.arch)
+            prog = rt.NativeHipProgram(self.device_index, code, ["kernel_0"], [(launch[0].grid, launch[0].block, 0)],
+                                       args, 0, len(ins), len(outs))
+            ip, op = [t.data_ptr() for t in ins], [t.data_ptr() for t in outs]
+            return lambda warmup, iters: prog.kernel_time(0, ip, op, stream, warmup, iters)
+
+        def timer(run, warmup, iters):
+            return run(warmup, iters)
+
+        return autotune(key, _candidates(dt), build, (M, N, K), kind, store=store, timer=timer)
+
+    # -- protocol ---------------------------------------------------------------
+    @property
+    def num_kernels(self) -> int:
+        return len(self.launches)
+
+    @property
+    def native(self) -> rt.NativeHipProgram:
+        return self._native
+
+    def _prepare(self, inputs) -> list[torch.Tensor]:
+        g = self.program.graph
+        if len(inputs) != len(g.inputs):
+            raise TypeError(f"expected {len(g.inputs)} inputs, got {len(inputs)}")
+        ins = []
+        for node, t in zip(g.inputs, inputs):
+            if not isinstance(t, torch.Tensor):
+                raise TypeError(f"{node.name}: expected a torch.Tensor, got {type(t)}")
+            if tuple(t.shape) != tuple(node.shape) or t.dtype != TORCH_DTYPE[node.dtype]:
+                raise ValueError(f"{node.name}: expected {tuple(node.shape)} {TORCH_DTYPE[node.dtype]}, "
+                                 f"got {tuple(t.shape)} {t.dtype}")
+            if t.device != self.device and not (t.is_cuda and t.device.index == self.device_index):
+                raise ValueError(f"{node.name}: tensor on {t.device}, program compiled for {self.device}")
+            t = t.contiguous()
+            if t.data_ptr() % 16:
+                t = t.clone()   # 16-byte vector loads need 16-byte aligned bases
+            ins.append(t)
+        return ins
+
+    def __call__(self, *inputs: torch.Tensor) -> list[torch.Tensor]:
+        ins = self._prepare(inputs)
+        outs = [self.pool.take_output(shape, dtype, self.device) for shape, dtype in self._out_specs]
+        ip = [t.data_ptr() for t in ins]
+        op = [t.data_ptr() for t in outs]
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self.stats["calls"] += 1
+        if self.use_graph and self.launches:
+            self._native.replay(ip, op, stream)
+            self.stats["graph_replays"] += 1
+        elif self.launches:
+            self._native.run(ip, op, stream)
+        return self._results(ins, outs)
+
+    def _results(self, ins: list[torch.Tensor], outs: list[torch.Tensor]) -> list[torch.Tensor]:
+        g = self.program.graph
+        env = {id(o): t for o, t in zip(self._out_nodes, outs)}
+        env.update({id(n): t for n, t in zip(g.inputs, ins)})
+        result = []
+        for o in g.outputs:
+            src = self.program.resolve(o)
+            if id(src) in env:
+                t = env[id(src)]
+            elif src.op == "const":
+                t = torch.full(src.shape, src.attrs["value"], dtype=TORCH_DTYPE[src.dtype], device=self.device)
+            else:
+                raise RuntimeError(f"output {o.name} was not produced")
+            result.append(t.reshape(o.shape) if tuple(t.shape) != tuple(o.shape) else t)
+        return result
+
+    # -- measurement helpers --------------------------------------------------------
+    def kernel_time_ms(self, k: int, *inputs: torch.Tensor, warmup: int = 3, iters: int = 20,
+                       outputs: list[torch.Tensor] | None = None) -> float:
+        """Average device time of kernel ``k`` (hipEvents on torch's current stream)."""
+        ins = self._prepare(inputs)
+        outs = outputs or [torch.empty(s, dtype=d, device=self.device) for s, d in self._out_specs]
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        return self._native.kernel_time(k, [t.data_ptr() for t in ins], [t.data_ptr() for t in outs], stream,
+                                        warmup, iters)
+
+    def native_stats(self) -> dict:
+        return self._native.stats()
+
+
+def compile_program(program: Program, device: str = "cuda", tune: bool = True) -> HipProgram:
+    return HipProgram(program, device=device, tune=tune)

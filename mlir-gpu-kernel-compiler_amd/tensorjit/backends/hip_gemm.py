@@ -1,0 +1,367 @@
+"""Kernel family 3 of the hip backend: tiled MFMA GEMM with a fused epilogue.
+
+``out = epilogue(A @ op(B))`` where ``op(B) = B^T`` when the fusion passes
+folded a transpose into the matmul (``trans_b``; the ``nn.Linear`` layout),
+with broadcast batch dims.  Reference template:
+``tensorjit/backends/cuda_backend.py:296-429`` (64x64x16 SIMT / WMMA tiles,
+single-buffered, epilogue in the store loop).
+
+gfx950 design:
+
+* Matrix cores: bf16 / fp16 use ``v_mfma_f32_32x32x16_{bf16,f16}`` (MI=32) or
+  ``v_mfma_f32_16x16x32_{bf16,f16}`` (MI=16); fp32 uses
+  ``v_mfma_f32_32x32x2f32`` / ``v_mfma_f32_16x16x4f32``.  fp32 accumulate.
+* Workgroup = ``WM x WN`` waves of 64 lanes; each wave owns a
+  ``(TM/WM) x (TN/WN)`` sub-tile as a grid of MI x MI accumulator blocks.
+* LDS holds A as ``[TM][TK+pad]`` and B as ``[TN][TK+pad]`` (both K
+  contiguous, 16-byte row padding so the 16-byte fragment reads of a wave hit
+  distinct banks), double buffered: while the waves run the MFMAs of K step
+  ``t`` from one buffer, the global loads of step ``t+1`` are already in
+  flight into registers and are written to the other buffer afterwards; one
+  barrier per K step.
+* ``trans_b`` (NT): both operands are K contiguous and load as 16-byte
+  vectors straight into the LDS layout.  Plain B (NN, ``[K][N]``) loads 16
+  bytes along N and is transposed on its way into LDS.
+* The epilogue runs on the accumulator registers: every fused pointwise op
+  (bias, gelu, residual, scale ...) is applied in fp32 and each escaping value
+  is stored once, with its extra inputs read at their broadcast strides.
+* Bounds checks are generated only for the edges the shape actually has.
+"""
+from __future__ import annotations
+
+import math
+
+from ..ir import DType, Node
+from ..runtime.autotune import MatmulConfig
+from .common import access_strides, contiguous_strides, emit_expr
+from .hip_kernels import KernelGen, Launch
+from .hip_prelude import CTYPE
+
+# (dtype, MI) -> (builtin, KI = K per instruction, KPL = K elements per lane, acc regs, operand vector type)
+MFMA = {
+    (DType.bf16, 32): ("__builtin_amdgcn_mfma_f32_32x32x16_bf16", 16, 8, 16, "tj_bf16x8"),
+    (DType.bf16, 16): ("__builtin_amdgcn_mfma_f32_16x16x32_bf16", 32, 8, 4, "tj_bf16x8"),
+    (DType.f16, 32): ("__builtin_amdgcn_mfma_f32_32x32x16_f16", 16, 8, 16, "tj_f16x8"),
+    (DType.f16, 16): ("__builtin_amdgcn_mfma_f32_16x16x32_f16", 32, 8, 4, "tj_f16x8"),
+    (DType.f32, 32): ("__builtin_amdgcn_mfma_f32_32x32x2f32", 2, 1, 16, "float"),
+    (DType.f32, 16): ("__builtin_amdgcn_mfma_f32_16x16x4f32", 4, 1, 4, "float"),
+}
+
+
+def matmul_dims(mm: Node) -> tuple[int, int, int, bool]:
+    a, b = mm.inputs
+    tb = bool(mm.attrs.get("trans_b"))
+    M, K = a.shape[-2], a.shape[-1]
+    N = b.shape[-2] if tb else b.shape[-1]
+    return M, N, K, tb
+
+
+def compute_dtype(mm: Node) -> DType:
+    """Operand type of the MFMA path: bf16/fp16 when both operands share it, else fp32."""
+    a, b = mm.inputs
+    if a.dtype == b.dtype and a.dtype in (DType.bf16, DType.f16):
+        return a.dtype
+    return DType.f32
+
+
+def config_ok(cfg: MatmulConfig, dt: DType) -> bool:
+    if (dt, cfg.MI) not in MFMA or cfg.SPLIT_K != 1:
+        return False
+    _, ki, _, _, _ = MFMA[(dt, cfg.MI)]
+    return (cfg.WM * cfg.WN == cfg.num_warps and cfg.TM % (cfg.WM * cfg.MI) == 0
+            and cfg.TN % (cfg.WN * cfg.MI) == 0 and cfg.TK % ki == 0 and cfg.TK > 0)
+
+
+def _batch_strides(t: Node, batch_shape: tuple) -> tuple[int, ...]:
+    """Strides of t's leading (batch) dims over the output's batch shape (0 = broadcast)."""
+    cs = contiguous_strides(t.shape)
+    lead = len(batch_shape) - (len(t.shape) - 2)
+    st = [0] * lead
+    for d in range(len(t.shape) - 2):
+        st.append(0 if t.shape[d] == 1 and batch_shape[lead + d] != 1 else cs[d])
+    return tuple(st)
+
+
+def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, Launch]:
+    k = g.k
+    mm = k.anchor
+    a, b = mm.inputs
+    M, N, K, tb = matmul_dims(mm)
+    out_shape = tuple(mm.shape)
+    batch_shape = out_shape[:-2]
+    batch = math.prod(batch_shape) if batch_shape else 1
+    dt = compute_dtype(mm)
+    if not config_ok(cfg, dt):
+        raise ValueError(f"matmul config {cfg} is not valid for {dt.value}")
+    builtin, KI, KPL, NACC, opvec = MFMA[(dt, cfg.MI)]
+    BM, BN, BK, MI = cfg.TM, cfg.TN, cfg.TK, cfg.MI
+    WM, WN = cfg.WM, cfg.WN
+    THREADS = 64 * cfg.num_warps
+    TMW, TNW = BM // WM // MI, BN // WN // MI
+    lds_t = CTYPE[dt] if dt != DType.f32 else "float"
+    esz = dt.itemsize
+    VK = 16 // esz                 # elements per 16-byte global load
+    PAD = VK                       # 16 bytes of row padding
+    LDK = BK + PAD
+    fname = g.fname + suffix
+
+    a_vec = a.dtype == dt and K % VK == 0
+    if tb:
+        b_vec = b.dtype == dt and K % VK == 0
+    else:
+        b_vec = b.dtype == dt and N % VK == 0
+    guard_m, guard_n, guard_k = M % BM != 0, N % BN != 0, K % BK != 0
+    KT = -(-K // BK)
+
+    A, B = g.names[id(a)], g.names[id(b)]
+    epilogue = [n for n in k.nodes if n is not mm]
+    idx_t = "unsigned long" if batch * M * N >= 2**31 or batch * max(M, N) * K >= 2**31 else "unsigned int"
+
+    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {fname}({g.params()}) {{']
+    L.append(f"  __shared__ __attribute__((aligned(16))) {lds_t} As[2][{BM}][{LDK}];")
+    L.append(f"  __shared__ __attribute__((aligned(16))) {lds_t} Bs[2][{BN}][{LDK}];")
+    L.append("  const unsigned int tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;")
+    L.append(f"  const unsigned int wm = wave / {WN}u, wn = wave % {WN}u;")
+    L.append(f"  const unsigned int m0 = blockIdx.y * {BM}u, n0 = blockIdx.x * {BN}u;")
+    # batch offsets
+    if batch_shape:
+        L.append(f"  const {idx_t} bi = blockIdx.z;")
+        bst = contiguous_strides(batch_shape)
+        bidx = []
+        rem = "bi"
+        for d, (s, cst) in enumerate(zip(batch_shape, bst)):
+            v = f"b{d}"
+            if d == len(batch_shape) - 1:
+                L.append(f"  const {idx_t} {v} = {rem};")
+            else:
+                L.append(f"  const {idx_t} {v} = {rem} / {cst}u;")
+                L.append(f"  const {idx_t} br{d} = {rem} % {cst}u;")
+                rem = f"br{d}"
+            bidx.append(v)
+
+        def boff(t: Node) -> str:
+            st = _batch_strides(t, batch_shape)
+            terms = [f"{v} * {s}u" for v, s in zip(bidx, st) if s]
+            return " + ".join(terms) if terms else "0u"
+
+        L.append(f"  const {CTYPE[a.dtype]}* __restrict__ Ab = {A}_p + ({boff(a)});")
+        L.append(f"  const {CTYPE[b.dtype]}* __restrict__ Bb = {B}_p + ({boff(b)});")
+    else:
+        bidx = []
+        L.append(f"  const {CTYPE[a.dtype]}* __restrict__ Ab = {A}_p;")
+        L.append(f"  const {CTYPE[b.dtype]}* __restrict__ Bb = {B}_p;")
+
+    # ---- global -> register staging ------------------------------------------------
+    def plan_k_major(rows: int, vec: bool):
+        """Chunks of a [rows][BK] tile read along K: (per-lane count, elems per chunk)."""
+        ve = VK if vec else 1
+        total = rows * BK // ve
+        return -(-total // THREADS), ve, total
+
+    a_cnt, a_ve, a_tot = plan_k_major(BM, a_vec)
+    if tb:
+        b_cnt, b_ve, b_tot = plan_k_major(BN, b_vec)
+    else:
+        b_ve = VK if b_vec else 1
+        b_tot = BK * BN // b_ve
+        b_cnt = -(-b_tot // THREADS)
+
+    def stage_type(ve: int, src_dt: DType) -> str:
+        if ve > 1:
+            return "tj_u32x4"
+        return lds_t
+
+    a_st_t, b_st_t = stage_type(a_ve, a.dtype), stage_type(b_ve, b.dtype)
+    L.append(f"  {a_st_t} ra[{a_cnt}];")
+    L.append(f"  {b_st_t} rb[{b_cnt}];")
+
+    def conv(src_dt: DType, expr: str) -> str:
+        """Scalar global element -> LDS element type."""
+        if src_dt == dt:
+            return expr
+        return f"tj_ld({expr})"   # fp32 LDS path for mixed / integer operands
+
+    def load_lines() -> list[str]:
+        out = ["#pragma unroll", f"  for (int i = 0; i < {a_cnt}; ++i) {{",
+               f"    const unsigned int c = i * {THREADS}u + tid;"]
+        if a_tot % THREADS:
+            out.append(f"    if (c >= {a_tot}u) break;")
+        per_row = BK // a_ve
+        out.append(f"    const unsigned int row = c / {per_row}u, kk = (c % {per_row}u) * {a_ve}u;")
+        out.append(f"    const {idx_t} gm = m0 + row, gk = k0 + kk;")
+        conds = []
+        if guard_m:
+            conds.append(f"gm < {M}u")
+        if guard_k:
+            conds.append(f"gk < {K}u")
+        cond = " && ".join(conds)
+        src = f"Ab[gm * {K}u + gk]"
+        if a_ve > 1:
+            ld = f"*(const tj_u32x4*)&{src}"
+            zero = "(tj_u32x4){0u, 0u, 0u, 0u}"
+        else:
+            ld = conv(a.dtype, src)
+            zero = f"({lds_t})0"
+        out.append(f"    ra[i] = ({cond}) ? {ld} : {zero};" if cond else f"    ra[i] = {ld};")
+        out.append("  }")
+        # B
+        out += ["#pragma unroll", f"  for (int i = 0; i < {b_cnt}; ++i) {{",
+                f"    const unsigned int c = i * {THREADS}u + tid;"]
+        if b_tot % THREADS:
+            out.append(f"    if (c >= {b_tot}u) break;")
+        if tb:
+            per_row = BK // b_ve
+            out.append(f"    const unsigned int row = c / {per_row}u, kk = (c % {per_row}u) * {b_ve}u;")
+            out.append(f"    const {idx_t} gn = n0 + row, gk = k0 + kk;")
+            conds = ([f"gn < {N}u"] if guard_n else []) + ([f"gk < {K}u"] if guard_k else [])
+            src = f"Bb[gn * {K}u + gk]"
+        else:
+            per_row = BN // b_ve
+            out.append(f"    const unsigned int krow = c / {per_row}u, nn = (c % {per_row}u) * {b_ve}u;")
+            out.append(f"    const {idx_t} gn = n0 + nn, gk = k0 + krow;")
+            conds = ([f"gn < {N}u"] if guard_n else []) + ([f"gk < {K}u"] if guard_k else [])
+            src = f"Bb[gk * {N}u + gn]"
+        cond = " && ".join(conds)
+        if b_ve > 1:
+            ld = f"*(const tj_u32x4*)&{src}"
+            zero = "(tj_u32x4){0u, 0u, 0u, 0u}"
+        else:
+            ld = conv(b.dtype, src)
+            zero = f"({lds_t})0"
+        out.append(f"    rb[i] = ({cond}) ? {ld} : {zero};" if cond else f"    rb[i] = {ld};")
+        out.append("  }")
+        return out
+
+    def store_lines(buf: str) -> list[str]:
+        out = ["#pragma unroll", f"  for (int i = 0; i < {a_cnt}; ++i) {{",
+               f"    const unsigned int c = i * {THREADS}u + tid;"]
+        if a_tot % THREADS:
+            out.append(f"    if (c >= {a_tot}u) break;")
+        per_row = BK // a_ve
+        out.append(f"    const unsigned int row = c / {per_row}u, kk = (c % {per_row}u) * {a_ve}u;")
+        if a_ve > 1:
+            out.append(f"    *(tj_u32x4*)&As[{buf}][row][kk] = ra[i];")
+        else:
+            out.append(f"    As[{buf}][row][kk] = ra[i];")
+        out.append("  }")
+        out += ["#pragma unroll", f"  for (int i = 0; i < {b_cnt}; ++i) {{",
+                f"    const unsigned int c = i * {THREADS}u + tid;"]
+        if b_tot % THREADS:
+            out.append(f"    if (c >= {b_tot}u) break;")
+        if tb:
+            per_row = BK // b_ve
+            out.append(f"    const unsigned int row = c / {per_row}u, kk = (c % {per_row}u) * {b_ve}u;")
+            if b_ve > 1:
+                out.append(f"    *(tj_u32x4*)&Bs[{buf}][row][kk] = rb[i];")
+            else:
+                out.append(f"    Bs[{buf}][row][kk] = rb[i];")
+        else:
+            per_row = BN // b_ve
+            out.append(f"    const unsigned int krow = c / {per_row}u, nn = (c % {per_row}u) * {b_ve}u;")
+            if b_ve > 1:
+                out.append("#pragma unroll")
+                out.append("    for (int w = 0; w < 4; ++w) {")
+                out.append("      const unsigned int x_ = rb[i][w];")
+                if esz == 4:
+                    out.append(f"      Bs[{buf}][nn + w][krow] = __builtin_bit_cast(float, x_);")
+                else:
+                    lo, hi = "(unsigned short)(x_ & 0xffffu)", "(unsigned short)(x_ >> 16)"
+                    if dt == DType.f16:
+                        lo, hi = f"__builtin_bit_cast(_Float16, {lo})", f"__builtin_bit_cast(_Float16, {hi})"
+                    out.append(f"      Bs[{buf}][nn + 2 * w][krow] = {lo};")
+                    out.append(f"      Bs[{buf}][nn + 2 * w + 1][krow] = {hi};")
+                out.append("    }")
+            else:
+                out.append(f"    Bs[{buf}][nn][krow] = rb[i];")
+        out.append("  }")
+        return out
+
+    # ---- MFMA compute on one LDS buffer ----------------------------------------------
+    groups = 64 // MI
+    acc_t = "tj_f32x16" if NACC == 16 else "tj_f32x4"
+    L.append(f"  {acc_t} acc[{TMW}][{TNW}];")
+    L.append("#pragma unroll")
+    L.append(f"  for (int x = 0; x < {TMW}; ++x)")
+    L.append("#pragma unroll")
+    L.append(f"    for (int y = 0; y < {TNW}; ++y) acc[x][y] = ({acc_t})(0.0f);")
+    L.append(f"  const unsigned int arow = wm * {BM // WM}u + (lane % {MI}u);")
+    L.append(f"  const unsigned int brow = wn * {BN // WN}u + (lane % {MI}u);")
+    L.append(f"  const unsigned int kofs = (lane / {MI}u) * {KPL}u;")
+
+    def compute_lines(buf: str) -> list[str]:
+        out = ["#pragma unroll", f"  for (int ks = 0; ks < {BK // KI}; ++ks) {{"]
+        out.append(f"    {opvec} fa[{TMW}], fb[{TNW}];")
+        out.append("#pragma unroll")
+        out.append(f"    for (int x = 0; x < {TMW}; ++x) fa[x] = *(const {opvec}*)&As[{buf}][arow + x * {MI}u][ks * {KI} + kofs];")
+        out.append("#pragma unroll")
+        out.append(f"    for (int y = 0; y < {TNW}; ++y) fb[y] = *(const {opvec}*)&Bs[{buf}][brow + y * {MI}u][ks * {KI} + kofs];")
+        out.append("#pragma unroll")
+        out.append(f"    for (int x = 0; x < {TMW}; ++x)")
+        out.append("#pragma unroll")
+        out.append(f"      for (int y = 0; y < {TNW}; ++y) acc[x][y] = {builtin}(fa[x], fb[y], acc[x][y], 0, 0, 0);")
+        out.append("  }")
+        return out
+
+    L.append("  unsigned int k0 = 0;")
+    L += load_lines()
+    L += store_lines("0")
+    L.append("  __syncthreads();")
+    L.append(f"  for (int kt = 0; kt < {KT}; ++kt) {{")
+    L.append("    const int cur = kt & 1;")
+    L.append(f"    k0 = (kt + 1) * {BK}u;")
+    L.append(f"    if (kt + 1 < {KT}) {{")
+    L += ["    " + s for s in load_lines()]
+    L.append("    }")
+    L += ["  " + s for s in compute_lines("cur")]
+    L.append(f"    if (kt + 1 < {KT}) {{")
+    L += ["    " + s for s in store_lines("cur ^ 1")]
+    L.append("    }")
+    L.append("    __syncthreads();")
+    L.append("  }")
+
+    # ---- epilogue on accumulators ------------------------------------------------------
+    epi_inputs = [i for i in k.inputs if i is not a and i is not b]
+    nrow_regs = NACC
+    if MI == 32:
+        row_of = "(r / 4) * 8 + (lane / 32u) * 4 + (r % 4)"
+        col_of = "lane % 32u"
+    else:
+        row_of = "(lane / 16u) * 4 + r"
+        col_of = "lane % 16u"
+    L.append("#pragma unroll")
+    L.append(f"  for (int x = 0; x < {TMW}; ++x)")
+    L.append("#pragma unroll")
+    L.append(f"  for (int y = 0; y < {TNW}; ++y)")
+    L.append("#pragma unroll")
+    L.append(f"  for (int r = 0; r < {nrow_regs}; ++r) {{")
+    L.append(f"    const {idx_t} i = m0 + wm * {BM // WM}u + x * {MI}u + {row_of};")
+    L.append(f"    const {idx_t} j = n0 + wn * {BN // WN}u + y * {MI}u + {col_of};")
+    conds = ([f"i < {M}u"] if guard_m else []) + ([f"j < {N}u"] if guard_n else [])
+    if conds:
+        L.append(f"    if ({' && '.join(conds)}) {{")
+    L.append(f"    const float {g.names[id(mm)]} = acc[x][y][r];")
+    local = {id(mm): g.names[id(mm)]}
+    full_idx = list(bidx) + ["i", "j"]
+    for n in epi_inputs:
+        consumer = next((c for c in epilogue if n in c.inputs), epilogue[0] if epilogue else mm)
+        st = access_strides(n, consumer, out_shape)
+        terms = [v if s == 1 else f"{v} * {s}u" for v, s in zip(full_idx, st) if s]
+        off = " + ".join(terms) if terms else "0u"
+        L.append(f"    const float {g.names[id(n)]}_e = tj_ld({g.names[id(n)]}_p[{off}]);")
+        local[id(n)] = f"{g.names[id(n)]}_e"
+    for n in epilogue:
+        L.append(f"    const float {g.names[id(n)]} = {emit_expr(n, local)};")
+        local[id(n)] = g.names[id(n)]
+    obase = f"bi * {M * N}u + " if batch_shape else ""
+    for jj, o in enumerate(k.outputs):
+        L.append(f"    tj_st(out{jj}_p + {obase}i * {N}u + j, {local[id(o)]});")
+    if conds:
+        L.append("    }")
+    L.append("  }")
+    L.append("}")
+
+    grid = (-(-N // BN), -(-M // BM), batch)
+    lds = 2 * (BM + BN) * LDK * esz
+    meta = {"family": "matmul", "config": cfg.as_dict(), "dtype": dt.value, "M": M, "N": N, "K": K, "batch": batch,
+            "trans_b": tb, "lds_bytes": lds, "flops": 2.0 * M * N * K * batch}
+    return "\n".join(L), Launch(fname, grid, (THREADS, 1, 1), 0, meta)

@@ -1,0 +1,458 @@
+"""Kernel families 1 and 2 of the hip backend: pointwise loop nests and row kernels.
+
+Both take a fused ``Kernel`` from the fusion passes and return HIP C++ text
+plus the launch geometry.  Every size and stride is a literal; all compute
+is fp32.
+
+Family 1 (``elementwise`` / ``copy``; reference template
+``tensorjit/backends/cuda_backend.py:142-160``): each lane owns 16-byte
+vectors of the contiguous output.  A vector never crosses a row of the last
+dim, so every input is read with one offset per vector: a 16-byte load when
+its innermost stride is 1, one broadcast scalar when it is 0, a gather
+otherwise.  ``U`` vectors per lane are loaded before any is computed so
+several loads per lane are in flight.  Grid = one workgroup of 256 lanes per
+``256*U`` vectors (no grid-stride loop; HIP's dispatcher spreads workgroups
+over all XCDs round-robin).
+
+Family 2 (``row`` and stand-alone ``reduce``; reference template
+``tensorjit/backends/cuda_backend.py:168-289``): one workgroup per row.  A
+lane owns ``NCH`` 16-byte chunks of the row, chunk ``c`` at element
+``(c*T + tid)*VEC``, so each chunk load is coalesced across the workgroup.
+External row inputs are loaded once into VGPRs at kernel entry (the
+reference reloads them in every stage) and values needed by later stages
+stay in VGPRs.  A reduction is a per-lane partial, a wave64 xor butterfly and
+one LDS exchange between the waves (one barrier, its own LDS slots per
+reduction so consecutive reductions never race).  A row group without any
+reduction is emitted as a flat family-1 loop nest over ``rows x N``.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+from ..ir import DType, Node
+from ..passes import Kernel
+from .common import access_strides, emit_expr, inner_stride, offset_expr
+from .hip_prelude import CTYPE, vec_width
+
+THREADS = 256
+
+
+@dataclass
+class Launch:
+    name: str
+    grid: tuple[int, int, int]
+    block: tuple[int, int, int]
+    shared: int = 0           # dynamic LDS bytes
+    meta: dict = field(default_factory=dict)
+
+
+@dataclass
+class KernelGen:
+    """Names for one kernel: external inputs ``in{j}``, nodes ``v{j}``, outputs ``out{j}``."""
+
+    k: Kernel
+    idx: int
+    names: dict[int, str]
+
+    @classmethod
+    def of(cls, k: Kernel, idx: int) -> "KernelGen":
+        names = {id(n): f"in{j}" for j, n in enumerate(k.inputs)}
+        names.update({id(n): f"v{j}" for j, n in enumerate(k.nodes)})
+        return cls(k, idx, names)
+
+    @property
+    def fname(self) -> str:
+        return f"kernel_{self.idx}"
+
+    def params(self) -> str:
+        ps = [f"const {CTYPE[n.dtype]}* __restrict__ {self.names[id(n)]}_p" for n in self.k.inputs]
+        ps += [f"{CTYPE[o.dtype]}* __restrict__ out{j}_p" for j, o in enumerate(self.k.outputs)]
+        return ", ".join(ps)
+
+    def consumer(self, n: Node, nodes: list[Node]) -> Node:
+        return next((c for c in nodes if n in c.inputs), nodes[0])
+
+
+def _index_type(count: int) -> str:
+    return "unsigned int" if count < 2**31 else "unsigned long"
+
+
+def _kernel_dtype(k: Kernel) -> DType:
+    """The storage dtype that sets the vector width (widest item wins)."""
+    dts = [n.dtype for n in k.outputs] + [n.dtype for n in k.inputs]
+    return max(dts, key=lambda d: d.itemsize) if dts else DType.f32
+
+
+def _vec_for(row_len: int, numel: int, dtype: DType) -> int:
+    w = vec_width(dtype)
+    return w if row_len % w == 0 and numel % w == 0 else 1
+
+
+# ---------------------------------------------------------------------------
+# family 1: pointwise loop nest
+# ---------------------------------------------------------------------------
+
+
+def _load_lines(src: str, ctype_ptr: str, off: str, inner: int, vec: int, dst: str) -> list[str]:
+    """Lines that fill ``dst[0..vec)`` with fp32 values of one vector of input ``src``."""
+    if vec == 1:
+        return [f"{dst}[0] = tj_ld({src}_p[{off}]);"]
+    if inner == 1:
+        return [f"tj_ldv({src}_p + ({off}), {dst});"]
+    if inner == 0:
+        return [f"{{ const float s_ = tj_ld({src}_p[{off}]);",
+                f"  for (int j = 0; j < {vec}; ++j) {dst}[j] = s_; }}"]
+    return [f"for (int j = 0; j < {vec}; ++j) {dst}[j] = tj_ld({src}_p[({off}) + j * {inner}u]);"]
+
+
+def gen_pointwise(g: KernelGen, nodes: list[Node], iter_shape: tuple[int, ...]) -> tuple[str, Launch]:
+    """Fused pointwise DAG ``nodes`` over ``iter_shape`` (elementwise kernels and
+    reduction-free row groups)."""
+    k = g.k
+    numel = math.prod(iter_shape) if iter_shape else 1
+    row_len = iter_shape[-1] if iter_shape else 1
+    vec = _vec_for(row_len, numel, _kernel_dtype(k))
+    nvec = numel // vec
+    unroll = 4 if nvec >= THREADS * 4 * 512 else (2 if nvec >= THREADS * 2 * 256 else 1)
+    per_block = THREADS * unroll
+    grid = max(1, -(-nvec // per_block))
+    idx_t = _index_type(numel)
+    guard = nvec % per_block != 0
+    inside = {id(n) for n in nodes}
+
+    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {g.fname}({g.params()}) {{',
+         f"  const {idx_t} vbase = ({idx_t})blockIdx.x * {per_block}u + threadIdx.x;"]
+    for n in k.inputs:
+        L.append(f"  float {g.names[id(n)]}_v[{unroll}][{vec}];")
+    # phase 1: issue every load of this lane
+    L.append("#pragma unroll")
+    L.append(f"  for (int u = 0; u < {unroll}; ++u) {{")
+    L.append(f"    const {idx_t} vi = vbase + u * {THREADS}u;")
+    if guard:
+        L.append(f"    if (vi >= {nvec}u) break;")
+    L.append(f"    const {idx_t} e = vi * {vec}u;")
+    for n in k.inputs:
+        st = access_strides(n, g.consumer(n, nodes), iter_shape)
+        nm = g.names[id(n)]
+        L += ["    " + s for s in _load_lines(nm, CTYPE[n.dtype], offset_expr("e", iter_shape, st),
+                                             inner_stride(iter_shape, st), vec, f"{nm}_v[u]")]
+    L.append("  }")
+    # phase 2: compute and store
+    L.append("#pragma unroll")
+    L.append(f"  for (int u = 0; u < {unroll}; ++u) {{")
+    L.append(f"    const {idx_t} vi = vbase + u * {THREADS}u;")
+    if guard:
+        L.append(f"    if (vi >= {nvec}u) break;")
+    L.append(f"    const {idx_t} e = vi * {vec}u;")
+    for j, o in enumerate(k.outputs):
+        L.append(f"    float o{j}_v[{vec}];")
+    L.append("#pragma unroll")
+    L.append(f"    for (int j = 0; j < {vec}; ++j) {{")
+    local = {id(n): f"{g.names[id(n)]}_v[u][j]" for n in k.inputs}
+    for n in nodes:
+        if n.op in ("transpose", "broadcast_to"):
+            expr = local[id(n.inputs[0])]
+        else:
+            expr = emit_expr(n, local)
+        L.append(f"      const float {g.names[id(n)]} = {expr};")
+        local[id(n)] = g.names[id(n)]
+    for j, o in enumerate(k.outputs):
+        if id(o) not in inside:
+            raise AssertionError(f"output {o.name} not computed by {g.fname}")
+        L.append(f"      o{j}_v[j] = {g.names[id(o)]};")
+    L.append("    }")
+    for j, o in enumerate(k.outputs):
+        if vec == 1:
+            L.append(f"    tj_st(out{j}_p + e, o{j}_v[0]);")
+        else:
+            L.append(f"    tj_stv(out{j}_p + e, o{j}_v);")
+    L.append("  }")
+    L.append("}")
+    meta = {"family": "pointwise", "vec": vec, "unroll": unroll, "numel": numel}
+    return "\n".join(L), Launch(g.fname, (grid, 1, 1), (THREADS, 1, 1), 0, meta)
+
+
+def gen_elementwise(g: KernelGen) -> tuple[str, Launch]:
+    return gen_pointwise(g, g.k.nodes, tuple(g.k.iter_shape))
+
+
+def gen_copy(g: KernelGen) -> tuple[str, Launch]:
+    """Materialised transpose / broadcast_to: a bit-exact move of storage elements."""
+    k = g.k
+    node = k.anchor
+    (src,) = k.inputs if k.inputs else (node.inputs[0],)
+    shape = tuple(node.shape)
+    numel = math.prod(shape) if shape else 1
+    ct = CTYPE[node.dtype]
+    st = access_strides(src, node, shape)
+    inner = inner_stride(shape, st)
+    row_len = shape[-1] if shape else 1
+    vec = _vec_for(row_len, numel, node.dtype)
+    nvec = numel // vec
+    unroll = 4 if nvec >= THREADS * 4 * 512 else 1
+    per_block = THREADS * unroll
+    grid = max(1, -(-nvec // per_block))
+    idx_t = _index_type(numel)
+    sname = g.names[id(src)]
+    off = offset_expr("e", shape, st)
+    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {g.fname}({g.params()}) {{',
+         f"  const {idx_t} vbase = ({idx_t})blockIdx.x * {per_block}u + threadIdx.x;",
+         "#pragma unroll",
+         f"  for (int u = 0; u < {unroll}; ++u) {{",
+         f"    const {idx_t} vi = vbase + u * {THREADS}u;"]
+    if nvec % per_block:
+        L.append(f"    if (vi >= {nvec}u) break;")
+    L.append(f"    const {idx_t} e = vi * {vec}u;")
+    if vec > 1 and inner == 1:
+        L.append(f"    *(tj_u32x4*)(out0_p + e) = *(const tj_u32x4*)({sname}_p + ({off}));")
+    elif vec > 1 and inner == 0:
+        L.append(f"    const {ct} s_ = {sname}_p[{off}];")
+        L.append(f"    for (int j = 0; j < {vec}; ++j) out0_p[e + j] = s_;")
+    elif vec > 1:
+        L.append(f"    {ct} t_[{vec}];")
+        L.append(f"    for (int j = 0; j < {vec}; ++j) t_[j] = {sname}_p[({off}) + j * {inner}u];")
+        L.append("    *(tj_u32x4*)(out0_p + e) = *(const tj_u32x4*)t_;")
+    else:
+        L.append(f"    out0_p[e] = {sname}_p[{off}];")
+    L += ["  }", "}"]
+    if len(k.outputs) != 1 or k.outputs[0] is not node:
+        raise AssertionError("copy kernels have exactly one output, the moved value")
+    if node.dtype != src.dtype:
+        raise AssertionError("copy kernels do not convert dtypes")
+    meta = {"family": "copy", "vec": vec, "unroll": unroll, "numel": numel}
+    return "\n".join(L), Launch(g.fname, (grid, 1, 1), (THREADS, 1, 1), 0, meta)
+
+
+# ---------------------------------------------------------------------------
+# family 2: row kernels
+# ---------------------------------------------------------------------------
+
+
+def row_geometry(N: int, vec: int, streaming_ok: bool) -> tuple[int, int, bool]:
+    """(threads T, chunks per lane NCH, streaming).  Aims at <= 256 lanes x a few
+    16-byte chunks; rows longer than 1024 lanes x 16 chunks stream through a
+    rolled loop (single-stage reductions only)."""
+    nv = -(-N // vec)
+    nch = max(1, -(-nv // 256))
+    t = 64 * -(-(-(-nv // nch)) // 64)
+    while t > 1024:
+        nch += 1
+        t = 64 * -(-(-(-nv // nch)) // 64)
+    if nch > 16:
+        if not streaming_ok:
+            raise NotImplementedError(f"row length {N} needs {nch} chunks per lane")
+        t = 1024
+        nch = -(-nv // t)
+        return t, nch, True
+    return t, nch, False
+
+
+def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[str, Launch]:
+    k = g.k
+    nrows = math.prod(rows) if rows else 1
+    vec_shape = tuple(rows) + (N,)
+    has_reduce = any(st.kind == "reduce" for st in stages)
+    if not has_reduce and all(tuple(st.iter_shape) == vec_shape for st in stages):
+        return gen_pointwise(g, k.nodes, vec_shape)
+
+    dt = _kernel_dtype(k)
+    vec = _vec_for(N, N, dt)
+    T, NCH, streaming = row_geometry(N, vec, streaming_ok=len(stages) == 1)
+    nwaves = T // 64
+    full = N % (T * vec) == 0
+    inside = {id(n) for n in k.nodes}
+    escaping = {id(o): j for j, o in enumerate(k.outputs)}
+    stage_of = {id(n): si for si, st in enumerate(stages) for n in st.nodes}
+    # per-row scalars: reduction results, their epilogues and scalar stages (classified by
+    # position, not shape: with N == 1 a keepdim reduction has the row shape too)
+    scalar_ids = set()
+    for st in stages:
+        if st.kind == "reduce":
+            scalar_ids |= {id(n) for n in st.nodes[st.nodes.index(st.anchor):]}
+        elif tuple(st.iter_shape) != vec_shape:
+            scalar_ids |= {id(n) for n in st.nodes}
+    is_vec = lambda n: id(n) not in scalar_ids  # noqa: E731
+    # vec values read by a later stage stay in registers
+    kept = [n for si, st in enumerate(stages) for n in st.nodes
+            if is_vec(n) and any(stage_of.get(id(u), si) != si for u in n.users if id(u) in inside)]
+    kept_ids = {id(n) for n in kept}
+    scalars = [n for n in k.nodes if not is_vec(n)]
+    nred = sum(st.kind == "reduce" for st in stages)
+    idx_t = _index_type(nrows * N)
+
+    # external inputs read per element (vec context) and per row (scalar context)
+    vec_ext: dict[int, tuple[Node, tuple[int, ...]]] = {}
+    for st in stages:
+        if st.kind == "reduce":
+            red = st.anchor
+            pos = st.nodes.index(red)
+            elem_nodes = st.nodes[:pos + 1]
+        elif tuple(st.iter_shape) == vec_shape:
+            elem_nodes = st.nodes
+        else:
+            continue
+        for n in st.inputs:
+            if id(n) in inside or id(n) in vec_ext:
+                continue
+            if not any(n in m.inputs for m in elem_nodes):
+                continue
+            strides = access_strides(n, g.consumer(n, [m for m in elem_nodes if n in m.inputs] or elem_nodes),
+                                     vec_shape)
+            vec_ext[id(n)] = (n, strides)
+
+    L = [f'extern "C" __global__ __launch_bounds__({T}) void {g.fname}({g.params()}) {{']
+    if nred:
+        L.append(f"  __shared__ float tj_red[{nred}][{nwaves}];")
+    L.append(f"  const {idx_t} r = blockIdx.x;")
+    L.append("  const unsigned int tid = threadIdx.x;")
+    if scalars:
+        L.append("  float " + ", ".join(g.names[id(n)] for n in scalars) + ";")
+
+    def chunk_open(c: str, body_indent: str = "    ") -> list[str]:
+        out = [f"  {{ const unsigned int n0 = ({c} * {T}u + tid) * {vec}u;"]
+        if not full:
+            out.append(f"  if (n0 < {N}u) {{")
+        return out
+
+    def chunk_close() -> list[str]:
+        return ["  }"] + ([] if full else ["  }"])
+
+    def ext_load(n: Node, strides, dst: str) -> list[str]:
+        off = offset_expr(f"(r * {N}u + n0)", vec_shape, strides)
+        return _load_lines(g.names[id(n)], CTYPE[n.dtype], off, inner_stride(vec_shape, strides), vec, dst)
+
+    # register arrays: preloaded external inputs and kept values
+    preload = not streaming
+    if preload:
+        for n, strides in vec_ext.values():
+            nm = g.names[id(n)]
+            L.append(f"  float {nm}_r[{NCH}][{vec}];")
+        for n in kept:
+            L.append(f"  float {g.names[id(n)]}_r[{NCH}][{vec}];")
+        if vec_ext:
+            L.append("#pragma unroll")
+            L.append(f"  for (int c = 0; c < {NCH}; ++c) {{")
+            L += ["  " + s for s in chunk_open("c")]
+            for n, strides in vec_ext.values():
+                L += ["      " + s for s in ext_load(n, strides, f"{g.names[id(n)]}_r[c]")]
+            L += ["  " + s for s in chunk_close()]
+            L.append("  }")
+
+    def elem_value(n: Node) -> str:
+        """fp32 value of input/earlier-stage node ``n`` at (chunk c, lane element j)."""
+        if id(n) in vec_ext:
+            return f"{g.names[id(n)]}_r[c][j]" if preload else f"{g.names[id(n)]}_l[j]"
+        if id(n) in kept_ids:
+            return f"{g.names[id(n)]}_r[c][j]"
+        if id(n) in inside and not is_vec(n):
+            return g.names[id(n)]
+        raise AssertionError(f"row kernel {g.fname}: no value for {n.name}")
+
+    def elem_block(nodes: list[Node], inputs: list[Node], extra: list[str]) -> list[str]:
+        """Per-element body for chunk c: loads (streaming), compute, stores, keeps."""
+        out = []
+        if not preload:
+            for n in inputs:
+                if id(n) in vec_ext:
+                    out.append(f"float {g.names[id(n)]}_l[{vec}];")
+                    out += ext_load(n, vec_ext[id(n)][1], f"{g.names[id(n)]}_l")
+        stores = [n for n in nodes if id(n) in escaping and is_vec(n)]
+        for n in stores:
+            out.append(f"float {g.names[id(n)]}_o[{vec}];")
+        out.append("#pragma unroll")
+        out.append(f"for (int j = 0; j < {vec}; ++j) {{")
+        own = {id(m) for m in nodes}
+        local = {id(n): elem_value(n) for n in inputs if id(n) not in own}
+        for n in nodes:
+            out.append(f"  const float {g.names[id(n)]}_e = {emit_expr(n, local)};")
+            local[id(n)] = f"{g.names[id(n)]}_e"
+            if id(n) in kept_ids:
+                out.append(f"  {g.names[id(n)]}_r[c][j] = {g.names[id(n)]}_e;")
+            if n in stores:
+                out.append(f"  {g.names[id(n)]}_o[j] = {g.names[id(n)]}_e;")
+        out += ["  " + s for s in extra]
+        out.append("}")
+        for n in stores:
+            j = escaping[id(n)]
+            dst = f"out{j}_p + r * {N}u + n0"
+            out.append(f"tj_stv({dst}, {g.names[id(n)]}_o);" if vec > 1 else f"tj_st({dst}, {g.names[id(n)]}_o[0]);")
+        return out
+
+    def chunk_loop(body: list[str]) -> list[str]:
+        out = []
+        if streaming:
+            out.append(f"  for (int c = 0; c < {NCH}; ++c) {{")
+        else:
+            out.append("#pragma unroll")
+            out.append(f"  for (int c = 0; c < {NCH}; ++c) {{")
+        out += ["  " + s for s in chunk_open("c")]
+        out += ["      " + s for s in body]
+        out += ["  " + s for s in chunk_close()]
+        out.append("  }")
+        return out
+
+    def scalar_store(n: Node) -> list[str]:
+        if id(n) not in escaping:
+            return []
+        return [f"  if (tid == 0) tj_st(out{escaping[id(n)]}_p + r, {g.names[id(n)]});"]
+
+    def scalar_lines(nodes: list[Node], st: Kernel, shape: tuple, idx_vars_expr: str,
+                     anchor: Node | None = None) -> list[str]:
+        """Per-row scalar nodes (uniform across the workgroup)."""
+        out = []
+        local: dict[int, str] = {id(anchor): g.names[id(anchor)]} if anchor is not None else {}
+        for n in st.inputs:
+            if id(n) in inside:
+                local[id(n)] = g.names[id(n)]
+            elif any(n in m.inputs for m in nodes):
+                strides = access_strides(n, g.consumer(n, [m for m in nodes if n in m.inputs]), shape)
+                off = offset_expr(idx_vars_expr, shape, strides)
+                out.append(f"  const float {g.names[id(n)]}_s{st_i} = tj_ld({g.names[id(n)]}_p[{off}]);")
+                local[id(n)] = f"{g.names[id(n)]}_s{st_i}"
+        for n in nodes:
+            local[id(n)] = g.names[id(n)]
+            out.append(f"  {g.names[id(n)]} = {emit_expr(n, local)};")
+            out += scalar_store(n)
+        return out
+
+    red_slot = 0
+    for st_i, st in enumerate(stages):
+        L.append(f"  // stage {st_i}: {st.kind} {[n.op for n in st.nodes]}")
+        if st.kind == "reduce":
+            red = st.anchor
+            pos = st.nodes.index(red)
+            prologue, epilogue = st.nodes[:pos], st.nodes[pos + 1:]
+            x = red.inputs[0]
+            is_max = red.op == "max"
+            init = "(-__builtin_inff())" if is_max else "0.0f"
+            xv = f"{g.names[id(x)]}_e" if x in prologue else elem_value(x)
+            upd = f"acc{st_i} = fmaxf(acc{st_i}, {xv});" if is_max else f"acc{st_i} += {xv};"
+            L.append(f"  float acc{st_i} = {init};")
+            used = [n for n in st.inputs if any(n in m.inputs for m in prologue + [red])]
+            L += chunk_loop(elem_block(prologue, used, [upd]))
+            wave = "tj_wave_max" if is_max else "tj_wave_sum"
+            L.append(f"  acc{st_i} = {wave}(acc{st_i});")
+            if nwaves > 1:
+                L.append(f"  if ((tid & 63u) == 0u) tj_red[{red_slot}][tid >> 6] = acc{st_i};")
+                L.append("  __syncthreads();")
+                L.append(f"  acc{st_i} = tj_red[{red_slot}][0];")
+                for w in range(1, nwaves):
+                    comb = f"fmaxf(acc{st_i}, tj_red[{red_slot}][{w}])" if is_max else f"acc{st_i} + tj_red[{red_slot}][{w}]"
+                    L.append(f"  acc{st_i} = {comb};")
+            red_slot += 1
+            if red.op == "mean":
+                L.append(f"  {g.names[id(red)]} = acc{st_i} / {float(N)!r}f;")
+            else:
+                L.append(f"  {g.names[id(red)]} = acc{st_i};")
+            L += scalar_store(red)
+            L += scalar_lines(epilogue, st, tuple(red.shape), "r", anchor=red)
+        elif tuple(st.iter_shape) == vec_shape:
+            used = [n for n in st.inputs if any(n in m.inputs for m in st.nodes)]
+            L += chunk_loop(elem_block(st.nodes, used, []))
+        else:
+            # per-row scalar stage over [rows] or [rows, 1]: linear index r addresses both
+            L += scalar_lines(st.nodes, st, tuple(st.iter_shape), "r")
+    L.append("}")
+    meta = {"family": "row", "vec": vec, "threads": T, "chunks": NCH, "streaming": streaming, "rows": nrows, "n": N}
+    return "\n".join(L), Launch(g.fname, (nrows, 1, 1), (T, 1, 1), 0, meta)

@@ -1,0 +1,118 @@
+"""Pipeline: trace -> optimise -> fuse -> row-fuse -> hip codegen -> cached callable.
+
+Same API and dispatch structure as the reference ``tensorjit/compiler.py``
+(``BACKENDS``, ``pick_backend``, ``ROW_FUSION_MAX_N``, ``lower``,
+``compile_graph``, ``CompileStats``, ``JitFunction``, ``jit``), with the
+``hip`` backend registered in it.  On PyTorch-ROCm the device type of GPU
+tensors is ``"cuda"``, and ``pick_backend`` routes it to ``hip``.
+"""
+from __future__ import annotations
+
+import functools
+import logging
+import os
+import threading
+import time
+from dataclasses import dataclass, field
+from typing import Callable, Sequence
+
+import torch
+
+from .frontend.tracer import tensor_type_of, trace
+from .ir import Graph
+from .passes import Program, fuse, optimize, row_fuse
+
+log = logging.getLogger("tensorjit")
+
+BACKENDS = ("hip",)
+
+# Longest row that row fusion may keep resident in one workgroup (same limit as the
+# reference's GPU backends: 8192 elements = 32 fp32 values per lane at 256 lanes).
+ROW_FUSION_MAX_N = {"hip": 8192}
+
+
+def pick_backend(device: str, requested: str | None = None) -> str:
+    requested = requested or os.environ.get("TENSORJIT_BACKEND")
+    if requested:
+        if requested not in BACKENDS:
+            raise AssertionError(f"unknown backend {requested} (this build provides {BACKENDS})")
+        return requested
+    if device == "cuda" and torch.version.hip is not None:
+        return "hip"
+    raise NotImplementedError(f"no tensorjit backend for device '{device}' in this build (hip backend: ROCm GPUs)")
+
+
+def lower(graph: Graph, backend: str = "hip") -> Program:
+    """IR -> optimised IR -> fused kernel program."""
+    program = fuse(optimize(graph))
+    if os.environ.get("TENSORJIT_NO_ROW_FUSION") != "1":
+        program = row_fuse(program, max_n=ROW_FUSION_MAX_N.get(backend))
+    return program
+
+
+def compile_graph(graph: Graph, backend: str, device: str = "cuda", tune: bool = True):
+    program = lower(graph, backend)
+    if backend == "hip":
+        from .backends import hip_backend
+
+        return hip_backend.compile_program(program, device=device, tune=tune)
+    raise ValueError(backend)
+
+
+@dataclass
+class CompileStats:
+    compiles: int = 0
+    hits: int = 0
+    compile_time_s: float = 0.0
+    kernels: dict[str, int] = field(default_factory=dict)
+
+
+class JitFunction:
+    """Shape/dtype-specialising JIT wrapper around a Python function."""
+
+    def __init__(self, fn: Callable, backend: str | None = None, tune: bool = True):
+        self.fn = fn
+        self.backend = backend
+        self.tune = tune
+        self.cache: dict[tuple, object] = {}
+        self.stats = CompileStats()
+        self._lock = threading.Lock()
+        functools.update_wrapper(self, fn)
+
+    def _key(self, args: Sequence[torch.Tensor]) -> tuple:
+        dev = args[0].device
+        return (tuple((tuple(a.shape), a.dtype) for a in args), str(dev), pick_backend(dev.type, self.backend))
+
+    def trace(self, *args: torch.Tensor) -> Graph:
+        return trace(self.fn, [tensor_type_of(a) for a in args], name=getattr(self.fn, "__name__", "main"))
+
+    def program(self, *args: torch.Tensor) -> Program:
+        return lower(self.trace(*args), self._key(args)[2])
+
+    def compiled(self, *args: torch.Tensor):
+        key = self._key(args)
+        with self._lock:
+            cp = self.cache.get(key)
+            if cp is not None:
+                self.stats.hits += 1
+                return cp
+            t0 = time.perf_counter()
+            cp = compile_graph(self.trace(*args), key[2], device=key[1], tune=self.tune)
+            self.stats.compiles += 1
+            self.stats.compile_time_s += time.perf_counter() - t0
+            self.stats.kernels[str(key)] = cp.num_kernels
+            self.cache[key] = cp
+            return cp
+
+    def __call__(self, *args: torch.Tensor):
+        if not args or not all(isinstance(a, torch.Tensor) for a in args):
+            raise TypeError("jit functions take torch.Tensor positional arguments only")
+        outs = self.compiled(*args)(*args)
+        return outs[0] if len(outs) == 1 else tuple(outs)
+
+
+def jit(fn: Callable | None = None, *, backend: str | None = None, tune: bool = True):
+    """``@tensorjit.jit`` or ``@tensorjit.jit(backend="hip")``."""
+    if fn is None:
+        return lambda f: JitFunction(f, backend=backend, tune=tune)
+    return JitFunction(fn, backend=backend, tune=tune)

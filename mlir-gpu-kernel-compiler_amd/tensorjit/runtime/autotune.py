@@ -1,0 +1,207 @@
+"""GEMM tile autotuning for gfx950 (CDNA4).
+
+Flow as in the reference autotuner (``tensorjit/runtime/autotune.py:83-118``):
+an analytic cost model ranks the candidate tile configurations, only the
+best ``top_k`` are compiled and timed on real buffers, and the winner is
+persisted in ``AutotuneStore`` so later processes start warm.
+
+The model is re-derived for MI355X instead of the reference's GPU branch
+(``autotune.py:73-79``).  It prices one call as the slowest of
+
+* MFMA time: 2*M*N*K at the dense matrix-core peak, scaled by how well the
+  tile grid fills 256 CUs (tail rounds of workgroups) and by edge waste;
+* LDS time: every wave re-reads its A and B fragments from LDS each K step
+  (128 B/clk/CU);
+* L2 time: each workgroup streams a (BM + BN) x K panel;
+* HBM time: A, B and C once at 8 TB/s;
+
+and rejects tiles that exceed 160 KiB of double-buffered LDS or 512 VGPRs
+(accumulators + fragments + staging) per lane.
+"""
+from __future__ import annotations
+
+import math
+import os
+import time
+from dataclasses import dataclass
+from typing import Callable, Sequence
+
+from .cache import AutotuneStore
+
+# MI355X (gfx950) figures used by the model.
+CU_COUNT = 256
+CLOCK_HZ = 2.4e9
+LDS_BYTES_PER_CU = 160 * 1024
+LDS_BYTES_PER_CLK = 128
+MFMA_FLOP_PER_CLK_BF16 = 4096   # per CU: 2.5 PF / 256 CU / 2.4 GHz
+MFMA_FLOP_PER_CLK_F32 = 256     # per CU: 157.3 TF / 256 CU / 2.4 GHz
+HBM_BYTES_PER_S = 8.0e12
+L2_BYTES_PER_S = 16.0e12
+
+
+@dataclass(frozen=True)
+class MatmulConfig:
+    """A GEMM tiling: block tile TM x TN, K step TK, ``num_warps`` waves of 64 lanes.
+
+    ``WM`` x ``WN`` is the wave grid inside the workgroup (``WM * WN == num_warps``)
+    and ``MI`` the MFMA tile edge (32 -> 32x32 blocks, 16 -> 16x16 blocks).
+    ``SPLIT_K`` > 1 splits K across the waves of a workgroup (skinny GEMMs).
+    """
+
+    TM: int
+    TN: int
+    TK: int = 0
+    num_warps: int = 4
+    WM: int = 2
+    WN: int = 2
+    MI: int = 32
+    SPLIT_K: int = 1
+
+    def as_dict(self) -> dict:
+        return {"TM": self.TM, "TN": self.TN, "TK": self.TK, "num_warps": self.num_warps,
+                "WM": self.WM, "WN": self.WN, "MI": self.MI, "SPLIT_K": self.SPLIT_K}
+
+    @staticmethod
+    def from_dict(d: dict) -> "MatmulConfig":
+        return MatmulConfig(d["TM"], d["TN"], d.get("TK", 0), d.get("num_warps", 4), d.get("WM", 2),
+                            d.get("WN", 2), d.get("MI", 32), d.get("SPLIT_K", 1))
+
+
+# bf16 / fp16 candidates (MFMA 32x32x16 or 16x16x32)
+HIP_CANDIDATES: list[MatmulConfig] = [
+    MatmulConfig(256, 256, 64, 4, 2, 2, 32),
+    MatmulConfig(256, 128, 64, 4, 2, 2, 32),
+    MatmulConfig(128, 256, 64, 4, 2, 2, 32),
+    MatmulConfig(128, 128, 64, 4, 2, 2, 32),
+    MatmulConfig(128, 128, 32, 4, 2, 2, 32),
+    MatmulConfig(128, 64, 64, 4, 2, 2, 32),
+    MatmulConfig(64, 128, 64, 4, 2, 2, 32),
+    MatmulConfig(64, 64, 64, 4, 2, 2, 16),
+    MatmulConfig(64, 64, 32, 4, 2, 2, 16),
+    MatmulConfig(32, 64, 64, 4, 2, 2, 16),
+    MatmulConfig(16, 64, 256, 4, 1, 1, 16, 4),   # skinny: split K over 4 waves
+    MatmulConfig(16, 32, 256, 4, 1, 1, 16, 4),
+]
+
+# fp32 candidates (MFMA 32x32x2 / 16x16x4 f32)
+HIP_F32_CANDIDATES: list[MatmulConfig] = [
+    MatmulConfig(128, 128, 16, 4, 2, 2, 32),
+    MatmulConfig(128, 128, 32, 4, 2, 2, 32),
+    MatmulConfig(128, 64, 32, 4, 2, 2, 32),
+    MatmulConfig(64, 128, 32, 4, 2, 2, 32),
+    MatmulConfig(64, 64, 32, 4, 2, 2, 16),
+    MatmulConfig(64, 64, 16, 4, 2, 2, 16),
+    MatmulConfig(32, 32, 32, 4, 2, 2, 16),
+]
+
+
+def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) -> float:
+    tm, tn, tk = cfg.TM, cfg.TN, cfg.TK or 32
+    waves = cfg.num_warps
+    if cfg.SPLIT_K == 1 and (tm % (cfg.WM * cfg.MI) or tn % (cfg.WN * cfg.MI)):
+        return math.inf
+    pad = 16 // elem
+    lds = 2 * (tm + tn) * (tk + pad) * elem
+    if lds > LDS_BYTES_PER_CU:
+        return math.inf
+    acc = tm * tn / (64 * waves) * (cfg.SPLIT_K if cfg.SPLIT_K > 1 else 1)
+    frags = (tm / cfg.WM + tn / cfg.WN) * cfg.MI / 64 * (2 if elem == 2 else 1)
+    staging = (tm + tn) * tk * elem / (256 * 4 * 2)   # 16 B loads per lane, 4 B per VGPR
+    regs = acc + frags + staging + 32
+    if regs > 512:
+        return math.inf
+    occ = max(1, min(LDS_BYTES_PER_CU // lds, int(512 // regs), 8 // max(1, waves // 4)))
+    tiles = -(-M // tm) * -(-N // tn) * batch
+    slots = CU_COUNT * occ
+    rounds = -(-tiles // slots)
+    fill = tiles / (rounds * slots)
+    busy_cus = min(1.0, tiles / CU_COUNT)
+    edge = (M / (-(-M // tm) * tm)) * (N / (-(-N // tn) * tn))
+    flops = 2.0 * M * N * K * batch
+    peak = (MFMA_FLOP_PER_CLK_BF16 if elem == 2 else MFMA_FLOP_PER_CLK_F32) * CU_COUNT * CLOCK_HZ
+    t_mfma = flops / (peak * max(fill, 1e-3) * max(busy_cus, 1e-3) * edge)
+    # LDS: per K step each wave reads (tm/WM + tn/WN) x tk elements; per CU per tile
+    lds_bytes_tile = waves * (tm / cfg.WM + tn / cfg.WN) * K * elem
+    lds_bytes_tile += (tm + tn) * K * elem                         # the global->LDS writes
+    t_lds = tiles * lds_bytes_tile / (LDS_BYTES_PER_CLK * CLOCK_HZ * min(CU_COUNT, tiles))
+    t_l2 = tiles * (tm + tn) * K * elem / L2_BYTES_PER_S
+    t_hbm = (M * K + N * K + M * N) * batch * elem / HBM_BYTES_PER_S
+    t = max(t_mfma, t_lds, t_l2, t_hbm)
+    if cfg.SPLIT_K > 1:
+        # skinny kernels only make sense when M is a handful of rows
+        t *= 1.0 if M <= tm else 4.0
+    return t * 1e6
+
+
+def cost_model(cfg: MatmulConfig, M: int, N: int, K: int, backend: str, batch: int = 1) -> float:
+    """Lower is better.  ``backend``: "hip" (bf16/fp16) or "hip_f32"; CPU kinds
+    "c" / "c_dot" keep the reference's register-pressure heuristic."""
+    if backend in ("hip", "hip_f32"):
+        return _hip_cost(cfg, M, N, K, batch, 2 if backend == "hip" else 4)
+    tm, tn = cfg.TM, cfg.TN
+    tk = cfg.TK or K
+    cost = (4.0 * (tm * tk + tk * tn)) / (2.0 * tm * tn * tk)
+    cost /= (M / (-(-M // tm) * tm)) * (N / (-(-N // tn) * tn))
+    if backend == "c_dot":
+        regs = tm * tn + tm
+        if regs > 14:
+            cost *= (regs / 14.0) ** 2
+    elif backend == "c":
+        regs = tm * tn / 8.0
+        if regs > 12:
+            cost *= 1.0 + (regs - 12) / 4.0
+    if M / tm < 2 * (os.cpu_count() or 1):
+        cost *= 1.3
+    return cost
+
+
+def _wall_timer(run: Callable[[], None], warmup: int, iters: int) -> float:
+    for _ in range(warmup):
+        run()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        run()
+    return (time.perf_counter() - t0) / iters * 1e3
+
+
+def autotune(
+    key: str,
+    candidates: Sequence[MatmulConfig],
+    build: Callable[[MatmulConfig], Callable[[], None]],
+    shape: tuple,
+    backend: str,
+    top_k: int = 4,
+    store: AutotuneStore | None = None,
+    warmup: int = 2,
+    iters: int = 5,
+    timer: Callable[[Callable[[], None], int, int], float] | None = None,
+) -> MatmulConfig:
+    """Fastest candidate by measurement; ``build(cfg)`` returns a zero-arg runner.
+
+    ``timer(run, warmup, iters) -> ms`` measures one runner (device-event timing
+    for GPU kernels); candidates whose build or run raises are skipped.
+    """
+    store = store or AutotuneStore()
+    rank = lambda c: cost_model(c, *shape, backend)  # noqa: E731
+    if os.environ.get("TENSORJIT_NO_AUTOTUNE") == "1":
+        return min(candidates, key=rank)
+    cached = store.get(key)
+    if cached is not None:
+        return MatmulConfig.from_dict(cached["config"])
+    ranked = [c for c in sorted(candidates, key=rank) if math.isfinite(rank(c))][:top_k]
+    if not ranked:
+        ranked = [min(candidates, key=rank)]
+    timer = timer or _wall_timer
+    best, best_ms = ranked[0], math.inf
+    for cfg in ranked:
+        try:
+            ms = timer(build(cfg), warmup, iters)
+        except Exception:  # invalid for this shape: skip it
+            continue
+        if ms < best_ms:
+            best, best_ms = cfg, ms
+    store.put(key, best.as_dict(), best_ms)
+    return best
+
+
+__all__ = ["MatmulConfig", "HIP_CANDIDATES", "HIP_F32_CANDIDATES", "cost_model", "autotune"]

@@ -1,0 +1,388 @@
+"""hip backend on a real MI355X: parity with the CPU oracle (the restated reference
+`c` backend) and with eager PyTorch on the same seeded inputs.
+
+Tolerances (north star): fp32 |a-b| <= atol + 1e-5*|b| with atol = 1e-5 * max|b|
+(scaled to the output's magnitude, as the reference's own `_close` pairs atol with
+rtol); bf16/fp16 storage within 2e-2 of the fp32 oracle; integer / max / copy
+results bit-exact.  Case list follows the reference's tests/test_backends.py and
+tests/test_cuda_backend.py.
+"""
+import math
+import os
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+import tensorjit as tj
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _skip_without_gpu():
+    if not (torch.cuda.is_available() and torch.version.hip):
+        pytest.skip("needs a ROCm GPU")
+
+
+@pytest.fixture(autouse=True)
+def _env(monkeypatch, tmp_path_factory):
+    _skip_without_gpu()
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    monkeypatch.setenv("TENSORJIT_CACHE_DIR", str(tmp_path_factory.getbasetemp() / "tjcache"))
+    yield
+
+
+def _host(t):
+    # float64 for normal sizes; float32 for the full-size configs (1e8+ elements)
+    t = t.detach().cpu()
+    return t.double() if t.numel() < 2**25 else t.float()
+
+
+def close_f32(out, ref, rtol=1e-5, scale=1e-5):
+    out, ref = _host(out), _host(ref)
+    atol = scale * max(float(ref.abs().max()), 1e-30)
+    err = (out - ref).abs() - (atol + rtol * ref.abs())
+    assert float(err.max()) <= 0, f"max excess {float(err.max()):.3e} (atol {atol:.3e})"
+
+
+def close_lowp(out, ref, tol=2e-2):
+    out, ref = _host(out), _host(ref)
+    atol = tol * max(float(ref.abs().max()), 1e-30)
+    assert float(((out - ref).abs() - (atol + tol * ref.abs())).max()) <= 0
+
+
+def check_vs_oracle(fn, *args, rtol=1e-5, scale=1e-5):
+    f = tj.jit(fn)
+    outs = f(*args)
+    outs = outs if isinstance(outs, tuple) else (outs,)
+    refs = oracle.run(fn, *[a.float().cpu() for a in args])
+    for o, r in zip(outs, refs):
+        assert o.is_cuda and o.shape == r.shape
+        if o.dtype == torch.float32:
+            close_f32(o, r, rtol, scale)
+        else:
+            close_lowp(o, r)
+    return f, outs
+
+
+# ------------------------------------------------------------------ pointwise
+
+
+@pytest.mark.parametrize("shape", [(17,), (8, 33), (2, 3, 5), (64, 4096)])
+def test_elementwise_chain(shape):
+    torch.manual_seed(0)
+    x, y = torch.randn(*shape, device=DEV), torch.randn(shape[-1], device=DEV)
+    fn = lambda a, b: tj.exp(tj.relu(a * 2.0 + b)) / (1.0 + tj.sigmoid(a)) - tj.tanh(b)  # noqa: E731
+    f, (out,) = check_vs_oracle(fn, x, y)
+    ref = torch.exp(torch.relu(x * 2 + y)) / (1 + torch.sigmoid(x)) - torch.tanh(y)
+    torch.testing.assert_close(out, ref, atol=1e-4, rtol=1e-4)
+    assert f.compiled(x, y).backend == "hip"
+
+
+@pytest.mark.parametrize("op", ["gelu", "silu", "log", "sqrt", "rsqrt", "abs", "sigmoid", "exp", "tanh", "relu"])
+def test_unary_ops(op):
+    torch.manual_seed(0)
+    x = torch.rand(4096, device=DEV) + 0.5
+    check_vs_oracle(getattr(tj, op), x, rtol=2e-6, scale=2e-6)
+
+
+def test_where_maximum_pow():
+    torch.manual_seed(0)
+    x, y = torch.randn(40, device=DEV), torch.randn(40, device=DEV)
+    x[::7] = 0.0
+    check_vs_oracle(lambda a, b: tj.where(a, tj.maximum(a, b), tj.minimum(a, b)) + tj.abs(a) ** 2.0, x, y)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+def test_config2_chain_small(dt):
+    torch.manual_seed(0)
+    x, a, b = torch.randn(64, 4096, device=DEV), torch.randn(4096, device=DEV), torch.randn(4096, device=DEV)
+    c = torch.rand(64, 4096, device=DEV) * 8 - 4
+    args = [t.to(dt) for t in (x, a, b, c)]
+    check_vs_oracle(lambda x, a, b, c: tj.gelu(x * a + b) * tj.sigmoid(c) + x, *args)
+
+
+def test_transpose_reshape_and_copies_are_bit_exact():
+    torch.manual_seed(0)
+    x = torch.randn(3, 4, 5, device=DEV)
+    f = tj.jit(lambda t: tj.exp(tj.permute(t, 2, 0, 1)).reshape(5, 12) + 1.0)
+    torch.testing.assert_close(f(x), torch.exp(x.permute(2, 0, 1)).reshape(5, 12) + 1)
+    for dt in (torch.float32, torch.bfloat16, torch.int32):
+        y = (torch.randn(4, 64, 8, 32, device=DEV) * 100).to(dt)
+        g = tj.jit(lambda t: tj.transpose(t, 1, 2))
+        assert torch.equal(g(y), y.transpose(1, 2).contiguous())
+        h = tj.jit(lambda t: tj.permute(t, 3, 0, 2, 1))
+        assert torch.equal(h(y), y.permute(3, 0, 2, 1).contiguous())
+
+
+# ------------------------------------------------------------------ reductions / rows
+
+
+@pytest.mark.parametrize("n", [1, 17, 100, 1000, 100000])
+def test_reductions(n):
+    torch.manual_seed(0)
+    x = torch.randn(6, n, device=DEV)
+    f = tj.jit(lambda t: (tj.sum(t), tj.max(t), tj.mean(t, keepdim=True)))
+    s, m, mu = f(x)
+    refs = oracle.run(lambda t: (tj.sum(t), tj.max(t), tj.mean(t, keepdim=True)), x.cpu())
+    close_f32(s, refs[0], scale=1e-5 * math.sqrt(n))
+    assert torch.equal(m.cpu(), x.amax(-1).cpu())          # max is bit-exact
+    close_f32(mu, refs[2], scale=1e-5 * math.sqrt(n))
+
+
+def test_reduce_non_last_axis_via_transpose():
+    torch.manual_seed(0)
+    x = torch.randn(4, 5, 6, device=DEV)
+    check_vs_oracle(lambda t: tj.sum(t, axis=1), x)
+
+
+@pytest.mark.parametrize("shape", [(9, 70), (16, 768), (8, 4096), (4, 8192)])
+def test_softmax_layernorm_rmsnorm(shape):
+    torch.manual_seed(0)
+    n = shape[-1]
+    x = torch.randn(*shape, device=DEV)
+    g, b = torch.randn(n, device=DEV), torch.randn(n, device=DEV)
+    fn = lambda t, w, c: (tj.softmax(t), tj.layer_norm(t, w, c), tj.rms_norm(t, w))  # noqa: E731
+    f, (sm, ln, rms) = check_vs_oracle(fn, x, g, b, scale=2e-5)
+    torch.testing.assert_close(sm, torch.softmax(x, -1), atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(ln, F.layer_norm(x, (n,), g, b), atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_row_kernels_low_precision_storage(dt):
+    torch.manual_seed(0)
+    x = torch.randn(32, 4096, device=DEV).to(dt)
+    g = (1 + 0.1 * torch.randn(4096, device=DEV)).to(dt)
+    check_vs_oracle(lambda t, w: (tj.layer_norm(t, w), tj.rms_norm(t, w), tj.softmax(t)), x, g)
+
+
+# ------------------------------------------------------------------ matmul
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 13, 5), (64, 64, 64), (33, 128, 65), (256, 512, 384)])
+def test_matmul_with_epilogue_fp32(m, k, n):
+    torch.manual_seed(0)
+    a, b, bias = torch.randn(m, k, device=DEV), torch.randn(k, n, device=DEV), torch.randn(n, device=DEV)
+    f, (out,) = check_vs_oracle(lambda x, y, z: tj.gelu(tj.matmul(x, y) + z), a, b, bias, rtol=1e-5, scale=1e-5)
+    torch.testing.assert_close(out, F.gelu(a @ b + bias), atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,k,n", [(64, 128, 256), (33, 72, 65), (256, 1024, 512), (16, 4096, 512)])
+def test_matmul_low_precision_vs_fp32(dt, m, k, n):
+    torch.manual_seed(0)
+    x = torch.randn(m, k, device=DEV).to(dt)
+    w = (0.02 * torch.randn(n, k, device=DEV)).to(dt)
+    bias = torch.randn(n, device=DEV).to(dt)
+    f = tj.jit(lambda x, w, b: tj.gelu(tj.linear(x, w, b)))
+    out = f(x, w, bias)
+    ref = F.gelu(F.linear(x.float(), w.float(), bias.float()))
+    close_lowp(out, ref, tol=2e-2)
+    (orc,) = oracle.run(lambda x, w, b: tj.gelu(tj.linear(x, w, b)), x.float().cpu(), w.float().cpu(), bias.float().cpu())
+    close_lowp(out, orc, tol=2e-2)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+def test_mfma_layout_is_exact_on_integer_data(dt):
+    """Small integers are exact in every dtype and in fp32 accumulation, so any
+    misplaced fragment or accumulator element shows up as an exact mismatch."""
+    torch.manual_seed(0)
+    for (m, k, n, tb) in [(64, 64, 64, True), (128, 96, 160, False), (96, 64, 32, True)]:
+        a = torch.randint(-3, 4, (m, k), device=DEV).to(dt)
+        b = torch.randint(-3, 4, (n, k) if tb else (k, n), device=DEV).to(dt)
+        f = tj.jit((lambda x, y: tj.linear(x, y)) if tb else (lambda x, y: tj.matmul(x, y)))
+        out = f(a, b).double()
+        ref = a.double() @ (b.double().t() if tb else b.double())
+        assert torch.equal(out.cpu(), ref.cpu()), (m, k, n, tb, dt)
+
+
+def test_batched_matmul_broadcast_and_linear():
+    torch.manual_seed(0)
+    a, b = torch.randn(2, 3, 8, 16, device=DEV), torch.randn(3, 16, 8, device=DEV)
+    check_vs_oracle(lambda x, y: tj.relu(tj.matmul(x, y)), a, b)
+    x, w, bb = torch.randn(10, 32, device=DEV), torch.randn(48, 32, device=DEV), torch.randn(48, device=DEV)
+    check_vs_oracle(tj.linear, x, w, bb)
+
+
+def test_attention_shaped_batched_matmuls_bf16():
+    torch.manual_seed(0)
+    q = torch.randn(2, 4, 128, 64, device=DEV).bfloat16()
+    k = torch.randn(2, 4, 128, 64, device=DEV).bfloat16()
+    v = torch.randn(2, 4, 128, 64, device=DEV).bfloat16()
+    f = tj.jit(lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * 0.125), v))
+    out = f(q, k, v)
+    p = torch.softmax((q.float() @ k.float().transpose(-1, -2).contiguous()) * 0.125, -1)
+    ref = p @ v.float()
+    close_lowp(out, ref, tol=3e-2)
+
+
+# ------------------------------------------------------------------ programs / executor
+
+MLP = lambda x, g, w1, b1, w2, b2: x + tj.linear(tj.gelu(tj.linear(tj.layer_norm(x, g), w1, b1)), w2, b2)  # noqa: E731
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_mlp_matches_eager_with_and_without_graph(use_graph, monkeypatch):
+    monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "1" if use_graph else "0")
+    torch.manual_seed(0)
+    x, g = torch.randn(64, 128, device=DEV), torch.ones(128, device=DEV)
+    w1, b1 = torch.randn(256, 128, device=DEV), torch.randn(256, device=DEV)
+    w2, b2 = torch.randn(128, 256, device=DEV), torch.randn(128, device=DEV)
+    f = tj.jit(MLP)
+    out = f(x, g, w1, b1, w2, b2)
+    ref = x + F.linear(F.gelu(F.linear(F.layer_norm(x, (128,), g), w1, b1)), w2, b2)
+    torch.testing.assert_close(out, ref, atol=2e-3, rtol=2e-3)
+    out2 = f(x + 1, g, w1, b1, w2, b2)
+    ref2 = (x + 1) + F.linear(F.gelu(F.linear(F.layer_norm(x + 1, (128,), g), w1, b1)), w2, b2)
+    torch.testing.assert_close(out2, ref2, atol=2e-3, rtol=2e-3)
+    cp = f.compiled(x, g, w1, b1, w2, b2)
+    assert cp.stats["graph_replays"] == (2 if use_graph else 0)
+    assert cp.num_kernels == 3 and "__global__" in cp.source
+
+
+def test_graph_replays_match_eager_every_time(monkeypatch):
+    monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "1")
+    torch.manual_seed(0)
+    x = torch.randn(128, 768, device=DEV)
+    args = [torch.ones(768, device=DEV), torch.randn(3072, 768, device=DEV) * 0.02, torch.randn(3072, device=DEV) * 0.02,
+            torch.randn(768, 3072, device=DEV) * 0.02, torch.randn(768, device=DEV) * 0.02]
+    f = tj.jit(MLP)
+    first = f(x, *args).clone()
+    for i in range(5):
+        y = f(x, *args)
+        torch.cuda.synchronize()
+        assert torch.equal(y, first), i
+        _ = (x * 2).sum().item()          # eager work between replays
+    cp = f.compiled(x, *args)
+    assert cp.native_stats()["graph_captures"] <= 3 and cp.stats["graph_replays"] == 6
+
+
+def test_transformer_block_small():
+    torch.manual_seed(0)
+    T_, D, H = 12, 32, 64
+    t = [torch.randn(s, device=DEV) for s in [(T_, D), (D,), (H, D), (H,), (D, H), (D,), (D, D), (D, D)]]
+
+    def block(x, ln_g, w1, b1, w2, b2, wq, wk):
+        h = tj.layer_norm(x, ln_g)
+        q, k = tj.linear(h, wq), tj.linear(h, wk)
+        scores = tj.softmax(tj.matmul(q, k.T) * (1.0 / 8.0))
+        return x + tj.linear(tj.gelu(tj.linear(h, w1, b1)), w2, b2), scores
+
+    f, (out, sc) = check_vs_oracle(block, *t, rtol=1e-4, scale=1e-4)
+    assert f.compiled(*t).num_kernels < 20
+
+
+def test_specialisation_cache_hits_and_recompiles():
+    f = tj.jit(lambda a: tj.exp(a) + 1.0)
+    x = torch.randn(8, device=DEV)
+    f(x)
+    f(x)
+    assert f.stats.compiles == 1 and f.stats.hits == 1
+    f(torch.randn(9, device=DEV))
+    assert f.stats.compiles == 2
+
+
+def test_output_buffers_reused_only_when_dropped(monkeypatch):
+    monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "0")
+    f = tj.jit(lambda a: tj.exp(a))
+    x = torch.randn(256, 512, device=DEV)
+    a = f(x)
+    view = a[:3]
+    b = f(x + 1)
+    assert a.data_ptr() != b.data_ptr()
+    del view
+    c = f(x + 2)
+    assert c.data_ptr() not in (a.data_ptr(), b.data_ptr())
+    pa = a.data_ptr()
+    del a
+    d = f(x + 3)
+    assert d.data_ptr() == pa
+    torch.testing.assert_close(b, torch.exp(x + 1))
+    torch.testing.assert_close(c, torch.exp(x + 2))
+    torch.testing.assert_close(d, torch.exp(x + 3))
+
+
+def test_reshape_and_const_outputs_and_bad_inputs():
+    x = torch.randn(3, 4, 5, device=DEV)
+    f = tj.jit(lambda t: (tj.exp(t).reshape(5, 12), tj.sum(t * 0.0 + 2.0)))
+    a, b = f(x)
+    torch.testing.assert_close(a, torch.exp(x).reshape(5, 12))
+    torch.testing.assert_close(b, torch.full((3, 4), 10.0, device=DEV))
+    g = tj.jit(lambda t: tj.exp(t))
+    g(torch.randn(8, device=DEV))
+    with pytest.raises(TypeError):
+        g.compiled(torch.randn(8, device=DEV))(torch.randn(8, device=DEV), torch.randn(8, device=DEV))
+
+
+def test_misaligned_input_view_is_handled():
+    x = torch.randn(1025, device=DEV)[1:]          # contiguous but 4-byte offset
+    f = tj.jit(lambda t: tj.exp(t) * 2.0)
+    torch.testing.assert_close(f(x), torch.exp(x) * 2)
+
+
+def test_torch_compile_backend_matches_eager(monkeypatch):
+    monkeypatch.setenv("TENSORJIT_STRICT", "1")
+    torch.manual_seed(0)
+    torch._dynamo.reset()
+
+    class Block(torch.nn.Module):
+        def __init__(self, d=32, h=64):
+            super().__init__()
+            self.ln = torch.nn.LayerNorm(d)
+            self.fc1 = torch.nn.Linear(d, h)
+            self.fc2 = torch.nn.Linear(h, d)
+            self.drop = torch.nn.Dropout(0.0)
+
+        def forward(self, x):
+            h = self.drop(F.gelu(self.fc1(self.ln(x))))
+            y = x + self.fc2(h)
+            return torch.softmax(y, dim=-1) * 2 + y.mean(dim=-1, keepdim=True)
+
+    m = Block().to(DEV).eval()
+    x = torch.randn(16, 32, device=DEV)
+    c = torch.compile(m, backend=tj.torch_compile_backend)
+    with torch.no_grad():
+        torch.testing.assert_close(c(x), m(x), atol=1e-4, rtol=1e-4)
+
+
+# ------------------------------------------------------------------ benchmark configs at full size
+
+
+def test_config2_full_size_fp32_vs_oracle():
+    torch.manual_seed(0)
+    x = torch.randn(16384, 4096, device=DEV)
+    a, b = torch.randn(4096, device=DEV), torch.randn(4096, device=DEV)
+    c = torch.rand(16384, 4096, device=DEV) * 8 - 4
+    check_vs_oracle(lambda x, a, b, c: tj.gelu(x * a + b) * tj.sigmoid(c) + x, x, a, b, c)
+
+
+def test_config3_full_size_rows_vs_oracle():
+    torch.manual_seed(0)
+    x = torch.randn(65536, 4096, device=DEV).bfloat16()
+    g = (1 + 0.1 * torch.randn(4096, device=DEV)).bfloat16()
+    check_vs_oracle(lambda x, g: tj.layer_norm(x, g), x, g)
+    check_vs_oracle(lambda x, g: tj.rms_norm(x, g), x, g)
+    s = torch.randn(65536, 2048, device=DEV) * 3
+    f, (sm,) = check_vs_oracle(lambda s: tj.softmax(s), s, scale=1e-6)
+    # size-independent properties: rows sum to 1, argmax preserved
+    torch.testing.assert_close(sm.sum(-1), torch.ones(65536, device=DEV), atol=1e-5, rtol=0)
+    assert torch.equal(sm.argmax(-1), s.argmax(-1))
+
+
+def test_config4_gemm_full_size_bf16_rows_vs_oracle():
+    torch.manual_seed(0)
+    x = torch.randn(8192, 8192, device=DEV).bfloat16()
+    w = (0.02 * torch.randn(8192, 8192, device=DEV)).bfloat16()
+    bias = (0.02 * torch.randn(8192, device=DEV)).bfloat16()
+    f = tj.jit(lambda x, w, b: tj.gelu(tj.linear(x, w, b)))
+    out = f(x, w, bias)
+    # the oracle on a 64-row sample (rows are independent: same kernel, different tile)
+    rows = torch.arange(0, 8192, 128, device=DEV)
+    (orc,) = oracle.run(lambda x, w, b: tj.gelu(tj.linear(x, w, b)), x[rows].float().cpu(), w.float().cpu(),
+                        bias.float().cpu())
+    close_lowp(out[rows], orc, tol=2e-2)
+    # and against the library GEMM on the whole output
+    ref = F.gelu(F.linear(x.float(), w.float(), bias.float()))
+    close_lowp(out, ref, tol=2e-2)
