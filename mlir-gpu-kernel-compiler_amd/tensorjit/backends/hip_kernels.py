@@ -63,7 +63,20 @@ class KernelGen:
 
     @property
     def fname(self) -> str:
-        return f"kernel_{self.idx}"
+        """``tj<idx>_<kind>_<iteration shape>_<dtype>``: unique in the module, readable in profiles."""
+        k = self.k
+        if k.kind == "matmul":
+            a, b = k.anchor.inputs
+            M, K = a.shape[-2], a.shape[-1]
+            N = b.shape[-2] if k.anchor.attrs.get("trans_b") else b.shape[-1]
+            batch = math.prod(k.anchor.shape[:-2]) if len(k.anchor.shape) > 2 else 1
+            dims = (f"{batch}x" if batch > 1 else "") + f"{M}x{N}x{K}" + ("_nt" if k.anchor.attrs.get("trans_b") else "_nn")
+            dt = a.dtype.value
+        else:
+            shape = tuple(k.iter_shape)
+            dims = "x".join(str(d) for d in shape) or "1"
+            dt = (k.outputs[0].dtype if k.outputs else k.nodes[-1].dtype).value
+        return f"tj{self.idx}_{k.kind}_{dims}_{dt}"
 
     def params(self) -> str:
         ps = [f"const {CTYPE[n.dtype]}* __restrict__ {self.names[id(n)]}_p" for n in self.k.inputs]

@@ -41,7 +41,7 @@ def test_generated_hip_compiles_for_gfx950(name, dtype, tj_env):
 
 def test_source_is_hip_and_specialised():
     src, _ = hb.generate(_program("eltwise_cfg2", DType.f32))
-    assert "blockIdx.x" in src and "4096" in src and "erff(" in src
+    assert "blockIdx.x" in src and "4096" in src and "tj_gelu(" in src and "tj_sigmoid(" in src
     assert "cuda" not in src.lower() and "nvcuda" not in src
 
 
