@@ -196,7 +196,7 @@ def secondary(torch, dev, quick):
         f = tj.jit(_fn_mlp)
         f(*margs)
         res["graph" if mode == "1" else "eager"] = round(timed_steps(torch, f, margs, 200, 20) * 1e3, 2)
-    os.environ["TENSORJIT_HIP_GRAPH"] = "1"
+    os.environ.pop("TENSORJIT_HIP_GRAPH", None)
     out["c1_mlp_f32_us_per_call"] = res
     log(f"c1_mlp: {res}")
     return out

@@ -27,6 +27,7 @@ reduction is emitted as a flat family-1 loop nest over ``rows x N``.
 """
 from __future__ import annotations
 
+import hashlib
 import math
 from dataclasses import dataclass, field
 
@@ -76,7 +77,20 @@ class KernelGen:
             shape = tuple(k.iter_shape)
             dims = "x".join(str(d) for d in shape) or "1"
             dt = (k.outputs[0].dtype if k.outputs else k.nodes[-1].dtype).value
-        return f"tj{self.idx}_{k.kind}_{dims}_{dt}"
+        return f"tj{self.idx}_{k.kind}_{dims}_{dt}_{self._tag()}"
+
+    def _tag(self) -> str:
+        """Composite ops the kernel implements (ln, rms, softmax, linear), else a hash of its ops."""
+        short = {"layer_norm": "ln", "rms_norm": "rms", "softmax": "softmax", "linear": "linear"}
+        tags: list[str] = []
+        for n in self.k.nodes:
+            op = n.meta.get("composite", {}).get("op")
+            if op and short.get(op, op) not in tags:
+                tags.append(short.get(op, op))
+        if tags:
+            return "_".join(tags)
+        ops = ",".join(n.op for n in self.k.nodes)
+        return "op" + hashlib.sha1(ops.encode()).hexdigest()[:6]
 
     def params(self) -> str:
         ps = [f"const {CTYPE[n.dtype]}* __restrict__ {self.names[id(n)]}_p" for n in self.k.inputs]
