@@ -47,8 +47,9 @@ COMPILE_OPTS = ("-O3", "-std=c++17", "-fno-strict-aliasing", *NO_PACKED_FP32)
 # ---------------------------------------------------------------------------
 
 
-def _candidates(dt: DType) -> list[MatmulConfig]:
-    return [c for c in (HIP_F32_CANDIDATES if dt == DType.f32 else HIP_CANDIDATES) if config_ok(c, dt)]
+def _candidates(k: Kernel) -> list[MatmulConfig]:
+    dt = compute_dtype(k.anchor)
+    return [c for c in (HIP_F32_CANDIDATES if dt == DType.f32 else HIP_CANDIDATES) if config_ok(c, dt, k.anchor)]
 
 
 def matmul_key(k: Kernel, arch: str) -> str:
@@ -65,7 +66,7 @@ def analytic_config(k: Kernel) -> MatmulConfig:
     batch = math.prod(mm.shape[:-2]) if len(mm.shape) > 2 else 1
     dt = compute_dtype(mm)
     kind = "hip_f32" if dt == DType.f32 else "hip"
-    return min(_candidates(dt), key=lambda c: cost_model(c, M, N, K, kind, batch))
+    return min(_candidates(k), key=lambda c: cost_model(c, M, N, K, kind, batch))
 
 
 # ---------------------------------------------------------------------------
@@ -201,7 +202,7 @@ class HipProgram:
         cached = store.get(key)
         if cached is not None:
             cfg = MatmulConfig.from_dict(cached["config"])
-            if config_ok(cfg, compute_dtype(k.anchor)):
+            if config_ok(cfg, compute_dtype(k.anchor), k.anchor):
                 return cfg
         if not tune or os.environ.get("TENSORJIT_NO_AUTOTUNE") == "1":
             return analytic_config(k)
@@ -232,7 +233,7 @@ class HipProgram:
         def timer(run, warmup, iters):
             return run(warmup, iters)
 
-        return autotune(key, _candidates(dt), build, (M, N, K), kind, store=store, timer=timer)
+        return autotune(key, _candidates(k), build, (M, N, K, batch), kind, store=store, timer=timer)
 
     # -- protocol ---------------------------------------------------------------
     @property

@@ -17,8 +17,8 @@ gfx950 design:
   contiguous, 16-byte row padding so the 16-byte fragment reads of a wave hit
   distinct banks), double buffered: while the waves run the MFMAs of K step
   ``t`` from one buffer, the global loads of step ``t+1`` are already in
-  flight into registers and are written to the other buffer afterwards; one
-  barrier per K step.
+  flight into registers (issued a whole MFMA phase before they are written
+  to the other buffer); one barrier per K step.
 * ``trans_b`` (NT): both operands are K contiguous and load as 16-byte
   vectors straight into the LDS layout.  Plain B (NN, ``[K][N]``) loads 16
   bytes along N and is transposed on its way into LDS.
@@ -64,12 +64,151 @@ def compute_dtype(mm: Node) -> DType:
     return DType.f32
 
 
-def config_ok(cfg: MatmulConfig, dt: DType) -> bool:
-    if (dt, cfg.MI) not in MFMA or cfg.SPLIT_K != 1:
+def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
+    """Is ``cfg`` a valid tiling for operand type ``dt`` (and for matmul ``mm`` if given)?"""
+    if (dt, cfg.MI) not in MFMA:
         return False
     _, ki, _, _, _ = MFMA[(dt, cfg.MI)]
+    if cfg.SPLIT_K > 1:
+        # skinny kernel: one MI x MI tile per workgroup, K split over its waves (NT, bf16/fp16)
+        ok = (dt in (DType.bf16, DType.f16) and cfg.TM == cfg.MI and cfg.TN % cfg.MI == 0
+              and cfg.TN // cfg.MI <= 4 and cfg.num_warps == cfg.SPLIT_K and cfg.TK % ki == 0 and cfg.TK > 0)
+        if ok and mm is not None:
+            M, N, K, tb = matmul_dims(mm)
+            a, b = mm.inputs
+            ok = tb and M <= cfg.TM and K % 8 == 0 and a.dtype == b.dtype == dt
+        return ok
     return (cfg.WM * cfg.WN == cfg.num_warps and cfg.TM % (cfg.WM * cfg.MI) == 0
             and cfg.TN % (cfg.WN * cfg.MI) == 0 and cfg.TK % ki == 0 and cfg.TK > 0)
+
+
+def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
+    """Decode-shaped GEMM (M <= MI, NT layout): HBM-bound on streaming B.
+
+    A workgroup owns TN = NT * MI output columns; its ``SPLIT_K`` waves each take a
+    contiguous K slice.  The MFMA operands need no LDS: with K-contiguous A and B,
+    lane ``l``'s 16-byte load of row ``l % MI`` at k-chunk ``l / MI`` is exactly its
+    operand register, so each wave streams B straight from HBM into the matrix core,
+    ``U`` loads ahead, and reuses each A fragment for its NT column tiles.  Partial
+    tiles are summed through LDS (one barrier), then the epilogue runs per element."""
+    k = g.k
+    mm = k.anchor
+    a, b = mm.inputs
+    M, N, K, tb = matmul_dims(mm)
+    dt = compute_dtype(mm)
+    builtin, KI, KPL, NACC, opvec = MFMA[(dt, cfg.MI)]
+    MI, SK = cfg.MI, cfg.SPLIT_K
+    NT = cfg.TN // MI
+    TN = cfg.TN
+    THREADS = 64 * SK
+    U = cfg.TK // KI                                 # MFMA steps per unrolled iteration
+    out_shape = tuple(mm.shape)
+    batch_shape = out_shape[:-2]
+    batch = math.prod(batch_shape) if batch_shape else 1
+    steps_total = -(-K // KI)
+    steps_per_wave = -(-steps_total // SK)
+    iters = -(-steps_per_wave // U)
+    k_guard = steps_per_wave * SK * KI != K or iters * U != steps_per_wave
+    A, B = g.names[id(a)], g.names[id(b)]
+    epilogue = [n for n in k.nodes if n is not mm]
+    fname = g.fname
+    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {fname}({g.params()}) {{']
+    L.append(f"  __shared__ float red[{SK}][{MI}][{TN + 1}];")
+    L.append("  const unsigned int tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;")
+    L.append(f"  const unsigned int n0 = blockIdx.x * {TN}u;")
+    bidx: list[str] = []
+    if batch_shape:
+        L.append("  const unsigned int bi = blockIdx.z;")
+        rem = "bi"
+        for d, cst in enumerate(contiguous_strides(batch_shape)):
+            v = f"b{d}"
+            if d == len(batch_shape) - 1:
+                L.append(f"  const unsigned int {v} = {rem};")
+            else:
+                L.append(f"  const unsigned int {v} = {rem} / {cst}u, br{d} = {rem} % {cst}u;")
+                rem = f"br{d}"
+            bidx.append(v)
+
+        def boff(t: Node) -> str:
+            terms = [f"{v} * {s}u" for v, s in zip(bidx, _batch_strides(t, batch_shape)) if s]
+            return " + ".join(terms) if terms else "0u"
+
+        L.append(f"  const {CTYPE[a.dtype]}* __restrict__ Ab = {A}_p + ({boff(a)});")
+        L.append(f"  const {CTYPE[b.dtype]}* __restrict__ Bb = {B}_p + ({boff(b)});")
+    else:
+        L.append(f"  const {CTYPE[a.dtype]}* __restrict__ Ab = {A}_p;")
+        L.append(f"  const {CTYPE[b.dtype]}* __restrict__ Bb = {B}_p;")
+    L.append(f"  const unsigned int row = lane % {MI}u, kofs = (lane / {MI}u) * {KPL}u;")
+    L.append(f"  const bool arow_ok = row < {M}u;")
+    L.append(f"  const {CTYPE[a.dtype]}* Ar = Ab + (arow_ok ? row : 0u) * {K}u;")
+    L.append(f"  bool bcol_ok[{NT}];")
+    L.append(f"  const {CTYPE[b.dtype]}* Br[{NT}];")
+    L.append("#pragma unroll")
+    L.append(f"  for (int t = 0; t < {NT}; ++t) {{")
+    L.append(f"    bcol_ok[t] = n0 + t * {MI}u + row < {N}u;")
+    L.append(f"    Br[t] = Bb + (bcol_ok[t] ? n0 + t * {MI}u + row : 0u) * {K}u;")
+    L.append("  }")
+    acc_t = "tj_f32x16" if NACC == 16 else "tj_f32x4"
+    L.append(f"  {acc_t} acc[{NT}];")
+    L.append("#pragma unroll")
+    L.append(f"  for (int t = 0; t < {NT}; ++t) acc[t] = ({acc_t})(0.0f);")
+    L.append(f"  const unsigned int kw = wave * {steps_per_wave * KI}u;")
+    L.append(f"  for (int it = 0; it < {iters}; ++it) {{")
+    L.append(f"    tj_u32x4 ra[{U}], rb[{U}][{NT}];")
+    L.append("#pragma unroll")
+    L.append(f"    for (int u = 0; u < {U}; ++u) {{")
+    L.append(f"      const unsigned int kk = kw + (it * {U} + u) * {KI}u + kofs;")
+    if k_guard:
+        L.append(f"      const bool kin = (it * {U} + u) < {steps_per_wave} && kk < {K}u;")
+    else:
+        L.append("      const bool kin = true;")
+    L.append("      ra[u] = (arow_ok && kin) ? *(const tj_u32x4*)(Ar + kk) : (tj_u32x4){0u, 0u, 0u, 0u};")
+    L.append("#pragma unroll")
+    L.append(f"      for (int t = 0; t < {NT}; ++t)")
+    L.append("        rb[u][t] = (bcol_ok[t] && kin) ? *(const tj_u32x4*)(Br[t] + kk) : (tj_u32x4){0u, 0u, 0u, 0u};")
+    L.append("    }")
+    L.append("#pragma unroll")
+    L.append(f"    for (int u = 0; u < {U}; ++u)")
+    L.append("#pragma unroll")
+    L.append(f"      for (int t = 0; t < {NT}; ++t)")
+    L.append(f"        acc[t] = {builtin}(__builtin_bit_cast({opvec}, ra[u]), __builtin_bit_cast({opvec}, rb[u][t]), acc[t], 0, 0, 0);")
+    L.append("  }")
+    if MI == 32:
+        row_of, col_of = "(r / 4) * 8 + (lane / 32u) * 4 + (r % 4)", "lane % 32u"
+    else:
+        row_of, col_of = "(lane / 16u) * 4 + r", "lane % 16u"
+    L.append("#pragma unroll")
+    L.append(f"  for (int t = 0; t < {NT}; ++t)")
+    L.append("#pragma unroll")
+    L.append(f"    for (int r = 0; r < {NACC}; ++r) red[wave][{row_of}][t * {MI}u + {col_of}] = acc[t][r];")
+    L.append("  __syncthreads();")
+    L.append(f"  for (unsigned int e = tid; e < {MI * TN}u; e += {THREADS}u) {{")
+    L.append(f"    const unsigned int i = e / {TN}u, jj = e % {TN}u, j = n0 + jj;")
+    L.append(f"    if (i >= {M}u || j >= {N}u) continue;")
+    L.append("    float s = 0.0f;")
+    L.append("#pragma unroll")
+    L.append(f"    for (int w = 0; w < {SK}; ++w) s += red[w][i][jj];")
+    L.append(f"    const float {g.names[id(mm)]} = s;")
+    local = {id(mm): g.names[id(mm)]}
+    full_idx = list(bidx) + ["i", "j"]
+    for n in [i for i in k.inputs if i is not a and i is not b]:
+        consumer = next((c for c in epilogue if n in c.inputs), epilogue[0] if epilogue else mm)
+        st = access_strides(n, consumer, out_shape)
+        terms = [v if s_ == 1 else f"{v} * {s_}u" for v, s_ in zip(full_idx, st) if s_]
+        L.append(f"    const float {g.names[id(n)]}_e = tj_ld({g.names[id(n)]}_p[{' + '.join(terms) if terms else '0u'}]);")
+        local[id(n)] = f"{g.names[id(n)]}_e"
+    for n in epilogue:
+        L.append(f"    const float {g.names[id(n)]} = {emit_expr(n, local)};")
+        local[id(n)] = g.names[id(n)]
+    obase = f"bi * {M * N}u + " if batch_shape else ""
+    for jj, o in enumerate(k.outputs):
+        L.append(f"    tj_st(out{jj}_p + {obase}i * {N}u + j, {local[id(o)]});")
+    L.append("  }")
+    L.append("}")
+    grid = (-(-N // TN), 1, batch)
+    meta = {"family": "matmul_skinny", "config": cfg.as_dict(), "dtype": dt.value, "M": M, "N": N, "K": K,
+            "batch": batch, "trans_b": tb, "lds_bytes": SK * MI * (TN + 1) * 4, "flops": 2.0 * M * N * K * batch}
+    return "\n".join(L), Launch(fname, grid, (THREADS, 1, 1), 0, meta)
 
 
 def _batch_strides(t: Node, batch_shape: tuple) -> tuple[int, ...]:
@@ -82,6 +221,33 @@ def _batch_strides(t: Node, batch_shape: tuple) -> tuple[int, ...]:
     return tuple(st)
 
 
+XCDS = 8   # MI355X: workgroups are dispatched round-robin over 8 XCDs, each with its own L2
+
+
+def tile_order_lines(ntm: int, ntn: int, group_m: int, BM: int, BN: int) -> list[str]:
+    """(m0, n0) of this workgroup.
+
+    The grid is launched as (ntn, ntm).  Workgroup ``w`` (x-fastest linear id) runs on XCD
+    ``w % 8``; re-numbering tiles so that XCD ``x`` owns the contiguous range
+    ``[x*T/8, (x+1)*T/8)`` of a grouped order (``group_m`` tile rows walked column by
+    column) makes the workgroups that share an L2 work on a compact block of tiles, so
+    they share A row panels and B column panels in that L2 instead of each XCD streaming
+    every panel from HBM / MALL."""
+    T = ntm * ntn
+    if group_m <= 0 or T < 2 * XCDS or T % XCDS:
+        return [f"  const unsigned int m0 = blockIdx.y * {BM}u, n0 = blockIdx.x * {BN}u;"]
+    gm = min(group_m, ntm)
+    per_group = gm * ntn
+    return [
+        f"  const unsigned int w_ = blockIdx.y * {ntn}u + blockIdx.x;",
+        f"  const unsigned int t_ = (w_ % {XCDS}u) * {T // XCDS}u + w_ / {XCDS}u;",
+        f"  const unsigned int g_ = t_ / {per_group}u, first_ = g_ * {gm}u;",
+        f"  const unsigned int gsz_ = ({ntm}u - first_) < {gm}u ? ({ntm}u - first_) : {gm}u;",
+        f"  const unsigned int r_ = t_ % {per_group}u;",
+        f"  const unsigned int m0 = (first_ + r_ % gsz_) * {BM}u, n0 = (r_ / gsz_) * {BN}u;",
+    ]
+
+
 def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, Launch]:
     k = g.k
     mm = k.anchor
@@ -91,8 +257,10 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     batch_shape = out_shape[:-2]
     batch = math.prod(batch_shape) if batch_shape else 1
     dt = compute_dtype(mm)
-    if not config_ok(cfg, dt):
-        raise ValueError(f"matmul config {cfg} is not valid for {dt.value}")
+    if not config_ok(cfg, dt, mm):
+        raise ValueError(f"matmul config {cfg} is not valid for {dt.value} {M}x{N}x{K}")
+    if cfg.SPLIT_K > 1:
+        return gen_skinny_matmul(g, cfg)
     builtin, KI, KPL, NACC, opvec = MFMA[(dt, cfg.MI)]
     BM, BN, BK, MI = cfg.TM, cfg.TN, cfg.TK, cfg.MI
     WM, WN = cfg.WM, cfg.WN
@@ -122,7 +290,8 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     L.append(f"  __shared__ __attribute__((aligned(16))) {lds_t} Bs[2][{BN}][{LDK}];")
     L.append("  const unsigned int tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;")
     L.append(f"  const unsigned int wm = wave / {WN}u, wn = wave % {WN}u;")
-    L.append(f"  const unsigned int m0 = blockIdx.y * {BM}u, n0 = blockIdx.x * {BN}u;")
+    ntm, ntn = -(-M // BM), -(-N // BN)
+    L += tile_order_lines(ntm, ntn, cfg.GROUP_M, BM, BN)
     # batch offsets
     if batch_shape:
         L.append(f"  const {idx_t} bi = blockIdx.z;")
@@ -288,33 +457,56 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     L.append(f"  const unsigned int brow = wn * {BN // WN}u + (lane % {MI}u);")
     L.append(f"  const unsigned int kofs = (lane / {MI}u) * {KPL}u;")
 
+    KS = BK // KI
+
     def compute_lines(buf: str) -> list[str]:
-        out = ["#pragma unroll", f"  for (int ks = 0; ks < {BK // KI}; ++ks) {{"]
-        out.append(f"    {opvec} fa[{TMW}], fb[{TNW}];")
-        out.append("#pragma unroll")
-        out.append(f"    for (int x = 0; x < {TMW}; ++x) fa[x] = *(const {opvec}*)&As[{buf}][arow + x * {MI}u][ks * {KI} + kofs];")
-        out.append("#pragma unroll")
-        out.append(f"    for (int y = 0; y < {TNW}; ++y) fb[y] = *(const {opvec}*)&Bs[{buf}][brow + y * {MI}u][ks * {KI} + kofs];")
+        """MFMAs of one K step.  Fragment registers are double buffered: the LDS reads
+        of sub-step ks+1 are issued before the MFMAs of ks, so LDS latency overlaps
+        the matrix cores instead of stalling them."""
+        def frag_loads(slot: str, ks: str) -> list[str]:
+            return ["#pragma unroll",
+                    f"    for (int x = 0; x < {TMW}; ++x) fa[{slot}][x] = *(const {opvec}*)&As[{buf}][arow + x * {MI}u][{ks} * {KI} + kofs];",
+                    "#pragma unroll",
+                    f"    for (int y = 0; y < {TNW}; ++y) fb[{slot}][y] = *(const {opvec}*)&Bs[{buf}][brow + y * {MI}u][{ks} * {KI} + kofs];"]
+        out = ["  {", f"    {opvec} fa[2][{TMW}], fb[2][{TNW}];"]
+        out += frag_loads("0", "0")
+        out += ["#pragma unroll", f"  for (int ks = 0; ks < {KS}; ++ks) {{"]
+        if KS > 1:
+            out.append(f"    if (ks + 1 < {KS}) {{")
+            out += ["  " + x for x in frag_loads("(ks + 1) & 1", "(ks + 1)")]
+            out.append("    }")
+        # keep the compiler's scheduler from sinking the next fragments' LDS reads
+        # below this sub-step's MFMAs (it otherwise serialises read -> wait -> MFMA)
+        out.append("    __builtin_amdgcn_sched_barrier(0);")
         out.append("#pragma unroll")
         out.append(f"    for (int x = 0; x < {TMW}; ++x)")
         out.append("#pragma unroll")
-        out.append(f"      for (int y = 0; y < {TNW}; ++y) acc[x][y] = {builtin}(fa[x], fb[y], acc[x][y], 0, 0, 0);")
+        out.append(f"      for (int y = 0; y < {TNW}; ++y) acc[x][y] = {builtin}(fa[ks & 1][x], fb[ks & 1][y], acc[x][y], 0, 0, 0);")
+        out.append("    __builtin_amdgcn_sched_barrier(0);")
+        out.append("  }")
         out.append("  }")
         return out
 
+    # Pipeline: registers always hold the tile one K step ahead of LDS.  Step kt runs
+    # the MFMAs on LDS[kt & 1], then writes the registers (tile kt+1, loaded one full
+    # MFMA phase earlier) to LDS[(kt+1) & 1], then issues the global loads of tile kt+2
+    # so their latency hides behind the next step's MFMAs; one barrier per step.
     L.append("  unsigned int k0 = 0;")
     L += load_lines()
     L += store_lines("0")
+    if KT > 1:
+        L.append(f"  k0 = {BK}u;")
+        L += load_lines()
     L.append("  __syncthreads();")
     L.append(f"  for (int kt = 0; kt < {KT}; ++kt) {{")
     L.append("    const int cur = kt & 1;")
-    L.append(f"    k0 = (kt + 1) * {BK}u;")
-    L.append(f"    if (kt + 1 < {KT}) {{")
-    L += ["    " + s for s in load_lines()]
-    L.append("    }")
     L += ["  " + s for s in compute_lines("cur")]
     L.append(f"    if (kt + 1 < {KT}) {{")
     L += ["    " + s for s in store_lines("cur ^ 1")]
+    L.append("    }")
+    L.append(f"    if (kt + 2 < {KT}) {{")
+    L.append(f"      k0 = (kt + 2) * {BK}u;")
+    L += ["    " + s for s in load_lines()]
     L.append("    }")
     L.append("    __syncthreads();")
     L.append("  }")

@@ -56,19 +56,23 @@ class MatmulConfig:
     WN: int = 2
     MI: int = 32
     SPLIT_K: int = 1
+    GROUP_M: int = 8        # tile rows per group of the XCD-aware tile order (0 = plain row-major order)
 
     def as_dict(self) -> dict:
         return {"TM": self.TM, "TN": self.TN, "TK": self.TK, "num_warps": self.num_warps,
-                "WM": self.WM, "WN": self.WN, "MI": self.MI, "SPLIT_K": self.SPLIT_K}
+                "WM": self.WM, "WN": self.WN, "MI": self.MI, "SPLIT_K": self.SPLIT_K, "GROUP_M": self.GROUP_M}
 
     @staticmethod
     def from_dict(d: dict) -> "MatmulConfig":
         return MatmulConfig(d["TM"], d["TN"], d.get("TK", 0), d.get("num_warps", 4), d.get("WM", 2),
-                            d.get("WN", 2), d.get("MI", 32), d.get("SPLIT_K", 1))
+                            d.get("WN", 2), d.get("MI", 32), d.get("SPLIT_K", 1), d.get("GROUP_M", 8))
 
 
 # bf16 / fp16 candidates (MFMA 32x32x16 or 16x16x32)
 HIP_CANDIDATES: list[MatmulConfig] = [
+    MatmulConfig(256, 256, 64, 8, 2, 4, 32),
+    MatmulConfig(256, 256, 32, 8, 2, 4, 32),
+    MatmulConfig(256, 128, 64, 8, 4, 2, 32),
     MatmulConfig(256, 256, 64, 4, 2, 2, 32),
     MatmulConfig(256, 128, 64, 4, 2, 2, 32),
     MatmulConfig(128, 256, 64, 4, 2, 2, 32),
@@ -79,8 +83,14 @@ HIP_CANDIDATES: list[MatmulConfig] = [
     MatmulConfig(64, 64, 64, 4, 2, 2, 16),
     MatmulConfig(64, 64, 32, 4, 2, 2, 16),
     MatmulConfig(32, 64, 64, 4, 2, 2, 16),
-    MatmulConfig(16, 64, 256, 4, 1, 1, 16, 4),   # skinny: split K over 4 waves
-    MatmulConfig(16, 32, 256, 4, 1, 1, 16, 4),
+    # skinny (M <= 16 / 32): one MI x MI tile per workgroup, K split over its waves
+    MatmulConfig(16, 32, 256, 8, 1, 1, 16, 8, 0),
+    MatmulConfig(16, 64, 256, 8, 1, 1, 16, 8, 0),
+    MatmulConfig(16, 32, 128, 16, 1, 1, 16, 16, 0),
+    MatmulConfig(16, 64, 128, 16, 1, 1, 16, 16, 0),
+    MatmulConfig(16, 16, 256, 8, 1, 1, 16, 8, 0),
+    MatmulConfig(32, 32, 128, 8, 1, 1, 32, 8, 0),
+    MatmulConfig(32, 64, 64, 16, 1, 1, 32, 16, 0),
 ]
 
 # fp32 candidates (MFMA 32x32x2 / 16x16x4 f32)
@@ -95,7 +105,20 @@ HIP_F32_CANDIDATES: list[MatmulConfig] = [
 ]
 
 
+def _skinny_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) -> float:
+    """Streaming kernel: the B panel once from HBM; needs enough waves in flight."""
+    if M > cfg.TM or elem != 2:
+        return math.inf
+    t_hbm = (M * K + N * K + M * N) * batch * elem / HBM_BYTES_PER_S
+    waves = -(-N // cfg.TN) * batch * cfg.SPLIT_K
+    fill = min(1.0, waves / (CU_COUNT * 8.0))           # ~8 streaming waves per CU saturate HBM
+    a_reads = 1.0 + cfg.TM / cfg.TN * 0.5                # A panel re-read per TN columns (from L2)
+    return t_hbm / max(fill, 1e-3) * a_reads * 1e6
+
+
 def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) -> float:
+    if cfg.SPLIT_K > 1:
+        return _skinny_cost(cfg, M, N, K, batch, elem)
     tm, tn, tk = cfg.TM, cfg.TN, cfg.TK or 32
     waves = cfg.num_warps
     if cfg.SPLIT_K == 1 and (tm % (cfg.WM * cfg.MI) or tn % (cfg.WN * cfg.MI)):
@@ -105,8 +128,8 @@ def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) 
     if lds > LDS_BYTES_PER_CU:
         return math.inf
     acc = tm * tn / (64 * waves) * (cfg.SPLIT_K if cfg.SPLIT_K > 1 else 1)
-    frags = (tm / cfg.WM + tn / cfg.WN) * cfg.MI / 64 * (2 if elem == 2 else 1)
-    staging = (tm + tn) * tk * elem / (256 * 4 * 2)   # 16 B loads per lane, 4 B per VGPR
+    frags = 2 * (tm / cfg.WM + tn / cfg.WN) / cfg.MI * (4 if elem == 2 else 1)  # double-buffered
+    staging = (tm + tn) * tk * elem / (64 * waves * 4)  # staged K step per lane, 4 B per VGPR
     regs = acc + frags + staging + 32
     if regs > 512:
         return math.inf
@@ -127,9 +150,6 @@ def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) 
     t_l2 = tiles * (tm + tn) * K * elem / L2_BYTES_PER_S
     t_hbm = (M * K + N * K + M * N) * batch * elem / HBM_BYTES_PER_S
     t = max(t_mfma, t_lds, t_l2, t_hbm)
-    if cfg.SPLIT_K > 1:
-        # skinny kernels only make sense when M is a handful of rows
-        t *= 1.0 if M <= tm else 4.0
     return t * 1e6
 
 

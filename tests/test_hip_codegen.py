@@ -76,7 +76,7 @@ def test_every_candidate_config_generates_valid_code():
     p32 = _program("gemm", DType.f32)
     for cands, p, dt in [(HIP_CANDIDATES, p16, DType.bf16), (HIP_F32_CANDIDATES, p32, DType.f32)]:
         for cfg in cands:
-            if not hb.config_ok(cfg, dt):
+            if not hb.config_ok(cfg, dt, p.kernels[0].anchor):
                 continue
             src, launches = hb.generate(p, {0: cfg})
             assert launches[0].meta["lds_bytes"] <= 160 * 1024
@@ -86,3 +86,41 @@ def test_config2_row_group_lowers_to_vectorised_flat_loop():
     src, launches = hb.generate(_program("eltwise_cfg2", DType.f32))
     assert launches[0].meta["family"] == "pointwise" and launches[0].meta["vec"] == 4
     assert "tj_ldv(" in src and "tj_stv(" in src
+
+
+def test_skinny_decode_shapes_use_the_streaming_kernel():
+    for m in (1, 7, 16):
+        g = tj.trace(lambda x, w, b: tj.gelu(tj.linear(x, w, b)),
+                     [TensorType(s, DType.bf16) for s in [(m, 8192), (8192, 8192), (8192,)]])
+        p = C.lower(g, "hip")
+        cfg = hb.analytic_config(p.kernels[0])
+        assert cfg.SPLIT_K > 1, cfg
+        src, launches = hb.generate(p, {0: cfg})
+        assert launches[0].meta["family"] == "matmul_skinny" and launches[0].grid[0] == 8192 // cfg.TN
+        hb.compile_source(src, "gfx950")
+
+
+def test_tile_order_is_a_bijection_when_compiled_for_the_host(tmp_path):
+    """The XCD-aware tile order text is compiled with gcc on the CPU (blockIdx as
+    arguments) and must visit every tile of the grid exactly once."""
+    import subprocess
+
+    from tensorjit.backends.hip_gemm import tile_order_lines
+
+    cases = [(32, 32, 8), (64, 48, 8), (7, 9, 8), (3, 40, 4), (33, 17, 8), (1, 16, 8), (16, 1, 8)]
+    fns = []
+    for ci, (ntm, ntn, gm) in enumerate(cases):
+        body = "\n".join(tile_order_lines(ntm, ntn, gm, 1, 1)).replace("blockIdx.x", "bx").replace("blockIdx.y", "by")
+        fns.append(f"static void order{ci}(unsigned bx, unsigned by, unsigned* mo, unsigned* no) {{\n{body}\n"
+                   "  *mo = m0; *no = n0; }")
+    checks = []
+    for ci, (ntm, ntn, gm) in enumerate(cases):
+        checks.append(f"""  {{ static unsigned char seen[{ntm}][{ntn}]; unsigned m, n;
+    for (unsigned by = 0; by < {ntm}u; ++by) for (unsigned bx = 0; bx < {ntn}u; ++bx) {{
+      order{ci}(bx, by, &m, &n); if (m >= {ntm}u || n >= {ntn}u || seen[m][n]++) return {ci + 1}; }} }}""")
+    src = "\n".join(fns) + "\nint main(void) {\n" + "\n".join(checks) + "\n  return 0;\n}\n"
+    c = tmp_path / "order.c"
+    c.write_text(src)
+    exe = tmp_path / "order"
+    subprocess.run(["gcc", "-O1", "-o", str(exe), str(c)], check=True)
+    assert subprocess.run([str(exe)]).returncode == 0

@@ -184,6 +184,25 @@ def test_matmul_low_precision_vs_fp32(dt, m, k, n):
     close_lowp(out, orc, tol=2e-2)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 512), (5, 1000, 300), (16, 8192, 1024), (20, 2048, 96), (32, 512, 64)])
+def test_skinny_decode_matmul(dt, m, k, n):
+    torch.manual_seed(0)
+    x = torch.randn(m, k, device=DEV).to(dt)
+    w = (0.02 * torch.randn(n, k, device=DEV)).to(dt)
+    bias = torch.randn(n, device=DEV).to(dt)
+    fn = lambda x, w, b: tj.gelu(tj.linear(x, w, b))  # noqa: E731
+    out = tj.jit(fn)(x, w, bias)
+    (orc,) = oracle.run(fn, x.float().cpu(), w.float().cpu(), bias.float().cpu())
+    close_lowp(out, orc, tol=2e-2)
+    # exact on small integers: catches a misplaced lane or k-slice
+    xi = torch.randint(-2, 3, (m, k), device=DEV).to(dt)
+    wi = torch.randint(-2, 3, (n, k), device=DEV).to(dt)
+    yi = tj.jit(lambda x, w: tj.linear(x, w))(xi, wi)
+    # the exact integer sum, rounded once to the storage dtype (RNE, as the kernel stores)
+    assert torch.equal(yi.cpu(), (xi.double() @ wi.double().t()).to(dt).cpu())
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
 def test_mfma_layout_is_exact_on_integer_data(dt):
     """Small integers are exact in every dtype and in fp32 accumulation, so any
@@ -193,8 +212,8 @@ def test_mfma_layout_is_exact_on_integer_data(dt):
         a = torch.randint(-3, 4, (m, k), device=DEV).to(dt)
         b = torch.randint(-3, 4, (n, k) if tb else (k, n), device=DEV).to(dt)
         f = tj.jit((lambda x, y: tj.linear(x, y)) if tb else (lambda x, y: tj.matmul(x, y)))
-        out = f(a, b).double()
-        ref = a.double() @ (b.double().t() if tb else b.double())
+        out = f(a, b)
+        ref = (a.double() @ (b.double().t() if tb else b.double())).to(dt)
         assert torch.equal(out.cpu(), ref.cpu()), (m, k, n, tb, dt)
 
 
