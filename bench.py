@@ -76,6 +76,32 @@ def _fn_mlp(x, g, w1, b1, w2, b2):
     return x + tj.linear(tj.gelu(tj.linear(tj.layer_norm(x, g), w1, b1)), w2, b2)
 
 
+def _fn_block(x, g1, wq, wk, wv, wo, g2, w1, w2):
+    """Config 5: one pre-norm transformer layer (RMSNorm, q/k/v projections, attention
+    with materialised scores, out-projection + residual, RMSNorm, gelu MLP + residual)."""
+    import tensorjit as tj
+
+    B, S, D = x.shape
+    H, Dh = 32, D // 32
+    h = tj.rms_norm(x, g1)
+    q = tj.linear(h, wq).reshape(B, S, H, Dh).transpose(1, 2)
+    k = tj.linear(h, wk).reshape(B, S, H, Dh).transpose(1, 2)
+    v = tj.linear(h, wv).reshape(B, S, H, Dh).transpose(1, 2)
+    p = tj.softmax(tj.matmul(q, k.transpose(-1, -2)) * (1.0 / Dh ** 0.5))
+    o = tj.matmul(p, v).transpose(1, 2).reshape(B, S, D)
+    x = x + tj.linear(o, wo)
+    return x + tj.linear(tj.gelu(tj.linear(tj.rms_norm(x, g2), w1)), w2)
+
+
+def block_inputs(torch, dev, B=4, S=2048, D=4096, F=11008, dt=None):
+    dt = dt or torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(0)
+    w = lambda *s: (0.02 * torch.randn(*s, device=dev, generator=g)).to(dt)  # noqa: E731
+    x = torch.randn(B, S, D, device=dev, generator=g).to(dt)
+    ones = torch.ones(D, device=dev, dtype=dt)
+    return [x, ones, w(D, D), w(D, D), w(D, D), w(D, D), ones.clone(), w(F, D), w(D, F)]
+
+
 def c2_inputs(torch, dt, dev):
     g = torch.Generator(device=dev).manual_seed(0)
     x = torch.randn(16384, 4096, device=dev, generator=g)
@@ -199,6 +225,29 @@ def secondary(torch, dev, quick):
     os.environ.pop("TENSORJIT_HIP_GRAPH", None)
     out["c1_mlp_f32_us_per_call"] = res
     log(f"c1_mlp: {res}")
+    # config 5: chained transformer block, bf16, arena + (optional) hipGraph
+    bargs = block_inputs(torch, dev)
+    res = {}
+    for mode in ("0", "1"):
+        os.environ["TENSORJIT_HIP_GRAPH"] = mode
+        f = tj.jit(_fn_block)
+        f(*bargs)
+        res["graph_us" if mode == "1" else "eager_us"] = round(timed_steps(torch, f, bargs, 10, 2) * 1e3, 1)
+    os.environ.pop("TENSORJIT_HIP_GRAPH", None)
+    cp = f.compiled(*bargs)
+    flops = 2851.9e9
+    kernels = []
+    for i, l in enumerate(cp.launches):
+        kus = cp.kernel_time_ms(i, *bargs, warmup=1, iters=5) * 1e3
+        entry = {"kernel": l.name, "us": round(kus, 1)}
+        if "flops" in l.meta:
+            entry["TFLOP/s"] = round(l.meta["flops"] / kus / 1e6, 1)
+        kernels.append(entry)
+    best = min(res.values())
+    out["c5_block_bf16"] = {**res, "TFLOP/s": round(flops / best / 1e6, 1), "frac_peak": round(flops / best / 1e6 / BF16_PEAK_TFLOPS, 4),
+                            "kernels": len(cp.launches), "arena_MiB": round(cp.plan.arena_bytes / 2**20, 1),
+                            "per_kernel": kernels}
+    log(f"c5_block: {out['c5_block_bf16']}")
     return out
 
 

@@ -231,9 +231,13 @@ class HipProgram:
             return lambda warmup, iters: prog.kernel_time(0, ip, op, stream, warmup, iters)
 
         def timer(run, warmup, iters):
-            return run(warmup, iters)
+            # enough launches for ~2 ms of device time per measurement (>= 3)
+            first = run(1, 1)
+            n = int(min(max(3, 2.0 / max(first, 1e-3)), 200))
+            return run(warmup, n)
 
-        return autotune(key, _candidates(k), build, (M, N, K, batch), kind, store=store, timer=timer)
+        return autotune(key, _candidates(k), build, (M, N, K, batch), kind, store=store, timer=timer, top_k=6,
+                        rounds=3)
 
     # -- protocol ---------------------------------------------------------------
     @property

@@ -78,6 +78,8 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
             a, b = mm.inputs
             ok = tb and M <= cfg.TM and K % 8 == 0 and a.dtype == b.dtype == dt
         return ok
+    if cfg.PINGPONG and cfg.num_warps % 2:
+        return False
     return (cfg.WM * cfg.WN == cfg.num_warps and cfg.TM % (cfg.WM * cfg.MI) == 0
             and cfg.TN % (cfg.WN * cfg.MI) == 0 and cfg.TK % ki == 0 and cfg.TK > 0)
 
@@ -221,6 +223,89 @@ def _batch_strides(t: Node, batch_shape: tuple) -> tuple[int, ...]:
     return tuple(st)
 
 
+def staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, BM, BN, WM, WN, MI,
+                          TMW, TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t):
+    """Epilogue through LDS: the accumulators are written to LDS in row-major order
+    (``P`` passes of BM/P rows when the tile does not fit at once), then every lane
+    processes 16-byte runs of a row, so the epilogue's extra inputs (bias, residual)
+    are read and its outputs written as coalesced vectors instead of one element per
+    lane per accumulator register.  Returns None when no pass size fits in LDS."""
+    out_dt = k.outputs[0].dtype
+    if any(o.dtype != out_dt for o in k.outputs):
+        return None
+    ve = 16 // out_dt.itemsize if N % (16 // out_dt.itemsize) == 0 else 1
+    ldc = BN + 4
+    P = None
+    for cand in range(1, TMW + 1):
+        if TMW % cand == 0 and (BM // cand) * ldc * 4 <= lds_bytes:
+            P = cand
+            break
+    if P is None:
+        return None
+    XP = TMW // P
+    rows = BM // P
+    if MI == 32:
+        row_of, col_of = "(r / 4) * 8 + (lane / 32u) * 4 + (r % 4)", "lane % 32u"
+    else:
+        row_of, col_of = "(lane / 16u) * 4 + r", "lane % 16u"
+    chunks = rows * (BN // ve)
+    L = ["  float* Cs = (float*)tj_lds;"]
+    full_idx = list(bidx) + ["i", "j"]
+    for p in range(P):
+        L.append("  __syncthreads();")
+        L.append("#pragma unroll")
+        L.append(f"  for (int x = {p * XP}; x < {(p + 1) * XP}; ++x)")
+        L.append("#pragma unroll")
+        L.append(f"  for (int y = 0; y < {TNW}; ++y)")
+        L.append("#pragma unroll")
+        L.append(f"  for (int r = 0; r < {NACC}; ++r)")
+        L.append(f"    Cs[(wm * {XP * MI}u + (x - {p * XP}) * {MI}u + {row_of}) * {ldc}u + wn * {BN // WN}u + y * {MI}u + "
+                 f"{col_of}] = acc[x][y][r];")
+        L.append("  __syncthreads();")
+        L.append(f"  for (unsigned int c = tid; c < {chunks}u; c += {THREADS}u) {{")
+        L.append(f"    const unsigned int lr = c / {BN // ve}u, cc = (c % {BN // ve}u) * {ve}u;")
+        L.append(f"    const {idx_t} i = m0 + (lr / {XP * MI}u) * {BM // WM}u + {p * XP * MI}u + lr % {XP * MI}u;")
+        L.append(f"    const {idx_t} j = n0 + cc;")
+        conds = ([f"i < {M}u"] if guard_m else []) + ([f"j < {N}u"] if guard_n else [])
+        if conds:
+            L.append(f"    if (!({' && '.join(conds)})) continue;")
+        L.append(f"    float acc_v[{ve}];")
+        L.append("#pragma unroll")
+        L.append(f"    for (int q = 0; q < {ve}; ++q) acc_v[q] = Cs[lr * {ldc}u + cc + q];")
+        local = {id(mm): "acc_v[q]"}
+        for n in epi_inputs:
+            consumer = next((c for c in epilogue if n in c.inputs), epilogue[0] if epilogue else mm)
+            st = access_strides(n, consumer, out_shape)
+            terms = [v if s_ == 1 else f"{v} * {s_}u" for v, s_ in zip(full_idx, st) if s_]
+            off = " + ".join(terms) if terms else "0u"
+            nm = g.names[id(n)]
+            L.append(f"    float {nm}_v[{ve}];")
+            inner = st[-1]
+            if ve > 1 and inner == 1 and 16 // n.dtype.itemsize == ve:
+                L.append(f"    tj_ldv({nm}_p + ({off}), {nm}_v);")
+            elif inner == 0:
+                L.append(f"    {{ const float s_ = tj_ld({nm}_p[{off}]); for (int q = 0; q < {ve}; ++q) {nm}_v[q] = s_; }}")
+            else:
+                L.append(f"    for (int q = 0; q < {ve}; ++q) {nm}_v[q] = tj_ld({nm}_p[({off}) + q * {inner}u]);")
+            local[id(n)] = f"{nm}_v[q]"
+        for jj in range(len(k.outputs)):
+            L.append(f"    float o{jj}_v[{ve}];")
+        L.append("#pragma unroll")
+        L.append(f"    for (int q = 0; q < {ve}; ++q) {{")
+        for n in epilogue:
+            L.append(f"      const float {g.names[id(n)]} = {emit_expr(n, local)};")
+            local[id(n)] = g.names[id(n)]
+        for jj, o in enumerate(k.outputs):
+            L.append(f"      o{jj}_v[q] = {local[id(o)]};")
+        L.append("    }")
+        obase = f"bi * {M * N}u + " if batch_shape else ""
+        for jj in range(len(k.outputs)):
+            dst = f"out{jj}_p + {obase}i * {N}u + j"
+            L.append(f"    tj_stv({dst}, o{jj}_v);" if ve > 1 else f"    tj_st({dst}, o{jj}_v[0]);")
+        L.append("  }")
+    return L
+
+
 XCDS = 8   # MI355X: workgroups are dispatched round-robin over 8 XCDs, each with its own L2
 
 
@@ -286,8 +371,11 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     idx_t = "unsigned long" if batch * M * N >= 2**31 or batch * max(M, N) * K >= 2**31 else "unsigned int"
 
     L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {fname}({g.params()}) {{']
-    L.append(f"  __shared__ __attribute__((aligned(16))) {lds_t} As[2][{BM}][{LDK}];")
-    L.append(f"  __shared__ __attribute__((aligned(16))) {lds_t} Bs[2][{BN}][{LDK}];")
+    a_bytes = 2 * BM * LDK * esz
+    lds_bytes = a_bytes + 2 * BN * LDK * esz
+    L.append(f"  __shared__ __attribute__((aligned(16))) char tj_lds[{lds_bytes}];")
+    L.append(f"  {lds_t} (*As)[{BM}][{LDK}] = ({lds_t} (*)[{BM}][{LDK}])tj_lds;")
+    L.append(f"  {lds_t} (*Bs)[{BN}][{LDK}] = ({lds_t} (*)[{BN}][{LDK}])(tj_lds + {a_bytes});")
     L.append("  const unsigned int tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;")
     L.append(f"  const unsigned int wm = wave / {WN}u, wn = wave % {WN}u;")
     ntm, ntn = -(-M // BM), -(-N // BN)
@@ -385,8 +473,9 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
             conds = ([f"gn < {N}u"] if guard_n else []) + ([f"gk < {K}u"] if guard_k else [])
             src = f"Bb[gn * {K}u + gk]"
         else:
-            per_row = BN // b_ve
-            out.append(f"    const unsigned int krow = c / {per_row}u, nn = (c % {per_row}u) * {b_ve}u;")
+            # consecutive lanes take consecutive k rows of one 16-byte column chunk, so the
+            # transposing 2-byte LDS stores below hit consecutive addresses (no bank conflicts)
+            out.append(f"    const unsigned int krow = c % {BK}u, nn = (c / {BK}u) * {b_ve}u;")
             out.append(f"    const {idx_t} gn = n0 + nn, gk = k0 + krow;")
             conds = ([f"gn < {N}u"] if guard_n else []) + ([f"gk < {K}u"] if guard_k else [])
             src = f"Bb[gk * {N}u + gn]"
@@ -425,8 +514,7 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
             else:
                 out.append(f"    Bs[{buf}][row][kk] = rb[i];")
         else:
-            per_row = BN // b_ve
-            out.append(f"    const unsigned int krow = c / {per_row}u, nn = (c % {per_row}u) * {b_ve}u;")
+            out.append(f"    const unsigned int krow = c % {BK}u, nn = (c / {BK}u) * {b_ve}u;")
             if b_ve > 1:
                 out.append("#pragma unroll")
                 out.append("    for (int w = 0; w < 4; ++w) {")
@@ -487,6 +575,10 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         out.append("  }")
         return out
 
+    if cfg.PINGPONG:
+        L += pingpong_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_lines, store_lines)
+        return _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW,
+                              TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
     # Pipeline: registers always hold the tile one K step ahead of LDS.  Step kt runs
     # the MFMAs on LDS[kt & 1], then writes the registers (tile kt+1, loaded one full
     # MFMA phase earlier) to LDS[(kt+1) & 1], then issues the global loads of tile kt+2
@@ -511,8 +603,82 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     L.append("    __syncthreads();")
     L.append("  }")
 
+    return _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW, TNW,
+                          NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
+
+
+def pingpong_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_lines, store_lines) -> list[str]:
+    """Main loop with two wave groups a phase apart ("ping-pong").
+
+    Waves ``[0, W/2)`` and ``[W/2, W)`` form two groups; each SIMD runs one wave of
+    each.  Every K step is a memory phase (read this step's fragments from LDS
+    stage ``kt & 1``, write the staged tile kt+1 to the other stage, issue the
+    global loads of tile kt+2) and a compute phase (the step's MFMA burst at raised
+    priority), separated by barriers.  Group 1 starts one barrier late, so on every
+    SIMD one wave computes while the other moves data.  Ordering: tile kt+1 is
+    written in phases 2kt (group 0) and 2kt+1 (group 1) and first read in phase
+    2kt+2; the stage it overwrites was last read in phase 2kt-1.  Every wave
+    executes 2*KT+2 barriers in total (one extra at the start or the end)."""
+    L = ["  unsigned int k0 = 0;"]
+    L += load_lines()
+    L += store_lines("0")
+    if KT > 1:
+        L.append(f"  k0 = {BK}u;")
+        L += load_lines()
+    L.append("  __syncthreads();")
+    L.append(f"  const bool grp1 = wave >= {cfg.num_warps // 2}u;")
+    L.append("  if (grp1) __syncthreads();")
+    L.append(f"  {opvec} fa[{KS}][{TMW}], fb[{KS}][{TNW}];")
+    L.append(f"  for (int kt = 0; kt < {KT}; ++kt) {{")
+    L.append("    const int cur = kt & 1;")
+    L.append("#pragma unroll")
+    L.append(f"    for (int ks = 0; ks < {KS}; ++ks) {{")
+    L.append("#pragma unroll")
+    L.append(f"      for (int x = 0; x < {TMW}; ++x) fa[ks][x] = *(const {opvec}*)&As[cur][arow + x * {MI}u][ks * {KI} + kofs];")
+    L.append("#pragma unroll")
+    L.append(f"      for (int y = 0; y < {TNW}; ++y) fb[ks][y] = *(const {opvec}*)&Bs[cur][brow + y * {MI}u][ks * {KI} + kofs];")
+    L.append("    }")
+    L.append(f"    if (kt + 1 < {KT}) {{")
+    L += ["    " + s for s in store_lines("cur ^ 1")]
+    L.append("    }")
+    L.append(f"    if (kt + 2 < {KT}) {{")
+    L.append(f"      k0 = (kt + 2) * {BK}u;")
+    L += ["    " + s for s in load_lines()]
+    L.append("    }")
+    L.append("    __builtin_amdgcn_sched_barrier(0);")
+    L.append("    __syncthreads();")
+    L.append("    __builtin_amdgcn_sched_barrier(0);")
+    L.append("    __builtin_amdgcn_s_setprio(1);")
+    L.append("#pragma unroll")
+    L.append(f"    for (int ks = 0; ks < {KS}; ++ks)")
+    L.append("#pragma unroll")
+    L.append(f"      for (int x = 0; x < {TMW}; ++x)")
+    L.append("#pragma unroll")
+    L.append(f"        for (int y = 0; y < {TNW}; ++y) acc[x][y] = {builtin}(fa[ks][x], fb[ks][y], acc[x][y], 0, 0, 0);")
+    L.append("    __builtin_amdgcn_s_setprio(0);")
+    L.append("    __builtin_amdgcn_sched_barrier(0);")
+    L.append("    __syncthreads();")
+    L.append("    __builtin_amdgcn_sched_barrier(0);")
+    L.append("  }")
+    L.append("  if (!grp1) __syncthreads();")
+    return L
+
+
+def _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW, TNW, NACC,
+                   THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname):
+    a, b = mm.inputs
     # ---- epilogue on accumulators ------------------------------------------------------
     epi_inputs = [i for i in k.inputs if i is not a and i is not b]
+    staged = staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, BM, BN, WM, WN,
+                                   MI, TMW, TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t)
+    if staged is not None:
+        L += staged
+        L.append("}")
+        grid = (-(-N // BN), -(-M // BM), batch)
+        meta = {"family": "matmul", "config": cfg.as_dict(), "dtype": dt.value, "M": M, "N": N, "K": K,
+                "batch": batch, "trans_b": tb, "lds_bytes": lds_bytes, "flops": 2.0 * M * N * K * batch,
+                "epilogue": "lds-staged"}
+        return "\n".join(L), Launch(fname, grid, (THREADS, 1, 1), 0, meta)
     nrow_regs = NACC
     if MI == 32:
         row_of = "(r / 4) * 8 + (lane / 32u) * 4 + (r % 4)"
@@ -553,7 +719,6 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     L.append("}")
 
     grid = (-(-N // BN), -(-M // BM), batch)
-    lds = 2 * (BM + BN) * LDK * esz
     meta = {"family": "matmul", "config": cfg.as_dict(), "dtype": dt.value, "M": M, "N": N, "K": K, "batch": batch,
-            "trans_b": tb, "lds_bytes": lds, "flops": 2.0 * M * N * K * batch}
+            "trans_b": tb, "lds_bytes": lds_bytes, "flops": 2.0 * M * N * K * batch}
     return "\n".join(L), Launch(fname, grid, (THREADS, 1, 1), 0, meta)

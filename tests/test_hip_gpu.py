@@ -405,3 +405,75 @@ def test_config4_gemm_full_size_bf16_rows_vs_oracle():
     # and against the library GEMM on the whole output
     ref = F.gelu(F.linear(x.float(), w.float(), bias.float()))
     close_lowp(out, ref, tol=2e-2)
+
+
+def test_config5_transformer_block_small_bf16_vs_oracle():
+    """Config 5's layer (RMSNorm, q/k/v, attention with materialised scores, out-proj +
+    residual, RMSNorm, gelu MLP + residual) at a small shape, bf16 vs the fp32 oracle."""
+    import bench
+
+    torch.manual_seed(0)
+    args = bench.block_inputs(torch, torch.device(DEV), B=2, S=64, D=256, F=512)
+    f = tj.jit(bench._fn_block)
+    out = f(*args)
+    assert f.compiled(*args).num_kernels == 16
+    (ref,) = oracle.run(bench._fn_block, *[a.float().cpu() for a in args])
+    close_lowp(out, ref, tol=3e-2)
+    # graph replay of the same program gives the same bits as eager launches
+    cp = f.compiled(*args)
+    eager = cp(*args)[0].clone()
+    cp.use_graph = True
+    for _ in range(3):
+        assert torch.equal(cp(*args)[0], eager)
+    cp.use_graph = False
+
+
+def _run_with_config(fn, args, cfg):
+    """Compile ``fn`` for ``args`` with its single matmul forced to tile config ``cfg``."""
+    from tensorjit.backends import hip_backend as hb
+    from tensorjit.compiler import lower
+    from tensorjit.frontend.tracer import tensor_type_of
+    from tensorjit.runtime import hip as rt
+
+    p = lower(tj.trace(fn, [tensor_type_of(a) for a in args]), "hip")
+    (k,) = p.kernels
+    src, launches = hb.generate(p, {0: cfg})
+    code = hb.compile_source(src, hb.arch_of(0))
+    out = torch.empty(k.outputs[0].shape, device=DEV, dtype=args[0].dtype)
+    refs = [[(rt.INPUT, j) for j in range(len(args))] + [(rt.OUTPUT, 0)]]
+    prog = rt.NativeHipProgram(0, code, [launches[0].name], [(launches[0].grid, launches[0].block, 0)], refs, 0,
+                               len(args), 1)
+    prog.run([a.data_ptr() for a in args], [out.data_ptr()], torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("tb", [True, False])
+def test_every_bf16_tile_config_is_exact_on_integer_data(tb):
+    """Every candidate tiling (incl. the ping-pong schedule and the skinny kernel) on
+    a shape with ragged M / N / K edges, exact on small-integer data."""
+    from tensorjit.backends import hip_backend as hb
+    from tensorjit.runtime.autotune import HIP_CANDIDATES
+
+    torch.manual_seed(0)
+    for m, n, kk in [(300, 520, 136), (16, 200, 512)]:
+        a = torch.randint(-2, 3, (m, kk), device=DEV).bfloat16()
+        b = torch.randint(-2, 3, (n, kk) if tb else (kk, n), device=DEV).bfloat16()
+        fn = (lambda x, y: tj.linear(x, y)) if tb else (lambda x, y: tj.matmul(x, y))
+        ref = (a.double() @ (b.double().t() if tb else b.double())).bfloat16()
+        mm = C_lower(fn, a, b).kernels[0].anchor
+        tried = 0
+        for cfg in HIP_CANDIDATES:
+            if not hb.config_ok(cfg, hb.compute_dtype(mm), mm):
+                continue
+            out = _run_with_config(fn, [a, b], cfg)
+            assert torch.equal(out, ref), (m, n, kk, tb, cfg)
+            tried += 1
+        assert tried >= (3 if m > 16 else 1)
+
+
+def C_lower(fn, *args):
+    from tensorjit.compiler import lower
+    from tensorjit.frontend.tracer import tensor_type_of
+
+    return lower(tj.trace(fn, [tensor_type_of(a) for a in args]), "hip")

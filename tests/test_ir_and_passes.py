@@ -191,3 +191,18 @@ def test_plan_launch_geometry_shape_of_mlp():
     # reference tests/test_cuda_backend.py:60-63: the MLP is [row, matmul, matmul]
     kinds, _ = _plan(MLP, (64, 128), (128,), (256, 128), (256,), (128, 256), (128,))
     assert [k for k, _ in kinds] == ["row", "matmul", "matmul"]
+
+
+def test_plan_transformer_block_config5():
+    import bench
+
+    shapes = [(4, 2048, 4096), (4096,), (4096, 4096), (4096, 4096), (4096, 4096), (4096, 4096), (4096,),
+              (11008, 4096), (4096, 11008)]
+    kinds, p = _plan(bench._fn_block, *shapes, dtype=DType.bf16)
+    assert [k for k, _ in kinds] == ["row", "matmul", "copy", "matmul", "copy", "matmul", "copy", "matmul", "row",
+                                     "matmul", "copy", "matmul", "row", "matmul", "matmul", "elementwise"]
+    qk = p.kernels[7]
+    assert qk.anchor.attrs.get("trans_b") and [n.op for n in qk.nodes] == ["matmul", "mul"]   # k^T folded, scale fused
+    assert [n.op for n in p.kernels[8].nodes] == ["max", "sub", "exp", "sum", "div"]
+    assert [n.op for n in p.kernels[11].nodes] == ["matmul", "add", "mul"]                  # residual (+ next x*x) fused
+    assert [n.op for n in p.kernels[13].nodes] == ["matmul", "gelu"]
