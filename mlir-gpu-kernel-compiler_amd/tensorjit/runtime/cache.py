@@ -35,8 +35,28 @@ def _atomic_write(path: Path, data: bytes) -> None:
     os.replace(tmp, path)
 
 
+TUNED_DIR = Path(__file__).resolve().parents[1] / "tuned"
+
+
+def _packaged(key: str) -> dict | None:
+    """Read-only warm-start table shipped with the package (``tuned/<target>.json``),
+    keyed like the user store; consulted when the user store has no entry."""
+    parts = key.split("|")
+    if len(parts) < 2:
+        return None
+    try:
+        table = json.loads((TUNED_DIR / f"{parts[1]}.json").read_text())
+    except (OSError, ValueError):
+        return None
+    return table.get(key)
+
+
 class AutotuneStore:
-    """JSON file of ``key -> {"config": ..., "ms": ...}``; writes are atomic renames."""
+    """JSON file of ``key -> {"config": ..., "ms": ...}``; writes are atomic renames.
+
+    Lookups fall back to the package's warm-start table for the key's gfx target,
+    so a fresh machine starts with measured tile choices instead of re-tuning;
+    set ``TENSORJIT_RETUNE=1`` to ignore that table."""
 
     _lock = threading.Lock()
 
@@ -54,7 +74,10 @@ class AutotuneStore:
 
     def get(self, key: str) -> dict | None:
         with self._lock:
-            return self._load().get(key)
+            hit = self._load().get(key)
+        if hit is None and os.environ.get("TENSORJIT_RETUNE") != "1":
+            hit = _packaged(key)
+        return hit
 
     def put(self, key: str, cfg: dict, ms: float) -> None:
         with self._lock:
