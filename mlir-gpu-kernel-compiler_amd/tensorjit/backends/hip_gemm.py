@@ -78,8 +78,17 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
             a, b = mm.inputs
             ok = tb and M <= cfg.TM and K % 8 == 0 and a.dtype == b.dtype == dt
         return ok
-    if cfg.PINGPONG and cfg.num_warps % 2:
-        return False
+    if cfg.PINGPONG:
+        if cfg.num_warps % 2 or cfg.PINGPONG > 2:
+            return False
+        # ping-pong holds accumulators, one step's fragments and PINGPONG staging sets
+        # in registers at once; past ~216 of the 256 VGPRs (addresses need the rest) it spills
+        tmw, tnw = cfg.TM // (cfg.WM * cfg.MI), cfg.TN // (cfg.WN * cfg.MI)
+        acc = tmw * tnw * cfg.MI * cfg.MI // 64
+        frag = (cfg.TK // ki) * (tmw + tnw) * 4
+        stage = cfg.PINGPONG * (cfg.TM + cfg.TN) * cfg.TK * dt.itemsize // (cfg.num_warps * 64 * 4)
+        if acc + frag + stage > 216:
+            return False
     return (cfg.WM * cfg.WN == cfg.num_warps and cfg.TM % (cfg.WM * cfg.MI) == 0
             and cfg.TN % (cfg.WN * cfg.MI) == 0 and cfg.TK % ki == 0 and cfg.TK > 0)
 
@@ -431,6 +440,9 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     a_st_t, b_st_t = stage_type(a_ve, a.dtype), stage_type(b_ve, b.dtype)
     L.append(f"  {a_st_t} ra[{a_cnt}];")
     L.append(f"  {b_st_t} rb[{b_cnt}];")
+    if cfg.PINGPONG > 1:
+        L.append(f"  {a_st_t} ra2[{a_cnt}];")
+        L.append(f"  {b_st_t} rb2[{b_cnt}];")
 
     def conv(src_dt: DType, expr: str) -> str:
         """Scalar global element -> LDS element type."""
@@ -438,7 +450,7 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
             return expr
         return f"tj_ld({expr})"   # fp32 LDS path for mixed / integer operands
 
-    def load_lines() -> list[str]:
+    def load_lines(sa: str = "ra", sb: str = "rb") -> list[str]:
         out = ["#pragma unroll", f"  for (int i = 0; i < {a_cnt}; ++i) {{",
                f"    const unsigned int c = i * {THREADS}u + tid;"]
         if a_tot % THREADS:
@@ -459,7 +471,7 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         else:
             ld = conv(a.dtype, src)
             zero = f"({lds_t})0"
-        out.append(f"    ra[i] = ({cond}) ? {ld} : {zero};" if cond else f"    ra[i] = {ld};")
+        out.append(f"    {sa}[i] = ({cond}) ? {ld} : {zero};" if cond else f"    {sa}[i] = {ld};")
         out.append("  }")
         # B
         out += ["#pragma unroll", f"  for (int i = 0; i < {b_cnt}; ++i) {{",
@@ -486,11 +498,11 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         else:
             ld = conv(b.dtype, src)
             zero = f"({lds_t})0"
-        out.append(f"    rb[i] = ({cond}) ? {ld} : {zero};" if cond else f"    rb[i] = {ld};")
+        out.append(f"    {sb}[i] = ({cond}) ? {ld} : {zero};" if cond else f"    {sb}[i] = {ld};")
         out.append("  }")
         return out
 
-    def store_lines(buf: str) -> list[str]:
+    def store_lines(buf: str, sa: str = "ra", sb: str = "rb") -> list[str]:
         out = ["#pragma unroll", f"  for (int i = 0; i < {a_cnt}; ++i) {{",
                f"    const unsigned int c = i * {THREADS}u + tid;"]
         if a_tot % THREADS:
@@ -498,9 +510,9 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         per_row = BK // a_ve
         out.append(f"    const unsigned int row = c / {per_row}u, kk = (c % {per_row}u) * {a_ve}u;")
         if a_ve > 1:
-            out.append(f"    *(tj_u32x4*)&As[{buf}][row][kk] = ra[i];")
+            out.append(f"    *(tj_u32x4*)&As[{buf}][row][kk] = {sa}[i];")
         else:
-            out.append(f"    As[{buf}][row][kk] = ra[i];")
+            out.append(f"    As[{buf}][row][kk] = {sa}[i];")
         out.append("  }")
         out += ["#pragma unroll", f"  for (int i = 0; i < {b_cnt}; ++i) {{",
                 f"    const unsigned int c = i * {THREADS}u + tid;"]
@@ -510,15 +522,15 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
             per_row = BK // b_ve
             out.append(f"    const unsigned int row = c / {per_row}u, kk = (c % {per_row}u) * {b_ve}u;")
             if b_ve > 1:
-                out.append(f"    *(tj_u32x4*)&Bs[{buf}][row][kk] = rb[i];")
+                out.append(f"    *(tj_u32x4*)&Bs[{buf}][row][kk] = {sb}[i];")
             else:
-                out.append(f"    Bs[{buf}][row][kk] = rb[i];")
+                out.append(f"    Bs[{buf}][row][kk] = {sb}[i];")
         else:
             out.append(f"    const unsigned int krow = c % {BK}u, nn = (c / {BK}u) * {b_ve}u;")
             if b_ve > 1:
                 out.append("#pragma unroll")
                 out.append("    for (int w = 0; w < 4; ++w) {")
-                out.append("      const unsigned int x_ = rb[i][w];")
+                out.append(f"      const unsigned int x_ = {sb}[i][w];")
                 if esz == 4:
                     out.append(f"      Bs[{buf}][nn + w][krow] = __builtin_bit_cast(float, x_);")
                 else:
@@ -529,7 +541,7 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
                     out.append(f"      Bs[{buf}][nn + 2 * w + 1][krow] = {hi};")
                 out.append("    }")
             else:
-                out.append(f"    Bs[{buf}][nn][krow] = rb[i];")
+                out.append(f"    Bs[{buf}][nn][krow] = {sb}[i];")
         out.append("  }")
         return out
 
@@ -613,53 +625,80 @@ def pingpong_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_
     Waves ``[0, W/2)`` and ``[W/2, W)`` form two groups; each SIMD runs one wave of
     each.  Every K step is a memory phase (read this step's fragments from LDS
     stage ``kt & 1``, write the staged tile kt+1 to the other stage, issue the
-    global loads of tile kt+2) and a compute phase (the step's MFMA burst at raised
+    global loads of tile kt+PF) and a compute phase (the step's MFMA burst at raised
     priority), separated by barriers.  Group 1 starts one barrier late, so on every
     SIMD one wave computes while the other moves data.  Ordering: tile kt+1 is
     written in phases 2kt (group 0) and 2kt+1 (group 1) and first read in phase
     2kt+2; the stage it overwrites was last read in phase 2kt-1.  Every wave
-    executes 2*KT+2 barriers in total (one extra at the start or the end)."""
+    executes 2*KT+2 barriers in total (one extra at the start or the end).
+
+    Prefetch distance ``PF = PINGPONG + 1``: tile t's global loads are issued at K
+    step t-PF into staging register set ``t % (PF-1)`` and written to LDS at step t-1,
+    so PF-1 steps of load latency are hidden.  The loop body holds two K steps (even
+    and odd), which makes every LDS stage and register set a compile-time choice; the
+    last steps, which have no tile left to load, are peeled."""
+    pf = cfg.PINGPONG + 1
+    nsets = pf - 1
+    sets = [("ra", "rb"), ("ra2", "rb2")][:nsets]
+
+    def step(kt: str, stage: int, do_store: bool, do_load: bool, ind: str) -> list[str]:
+        out = ["#pragma unroll", f"for (int ks = 0; ks < {KS}; ++ks) {{", "#pragma unroll",
+               f"  for (int x = 0; x < {TMW}; ++x) fa[ks][x] = *(const {opvec}*)&As[{stage}][arow + x * {MI}u][ks * {KI} + kofs];",
+               "#pragma unroll",
+               f"  for (int y = 0; y < {TNW}; ++y) fb[ks][y] = *(const {opvec}*)&Bs[{stage}][brow + y * {MI}u][ks * {KI} + kofs];",
+               "}"]
+        if do_store or do_load:
+            # tile kt+1 lives in set (kt+1) % nsets; kt+PF maps to the same set
+            sel = f"(({kt}) + 1) % {nsets}" if nsets > 1 else "0"
+            for j, (sa, sb) in enumerate(sets):
+                body = []
+                if do_store:
+                    body += store_lines(str(1 - stage), sa, sb)
+                if do_store and do_load:
+                    # loads after the stores: hoisted above the fragment reads they slow the phase
+                    body.append("__builtin_amdgcn_sched_barrier(0);")
+                if do_load:
+                    body.append(f"k0 = (({kt}) + {pf}) * {BK}u;")
+                    body += load_lines(sa, sb)
+                if nsets > 1:
+                    out.append(f"if ({sel} == {j}) {{")
+                    out += ["  " + x.strip() for x in body]
+                    out.append("}")
+                else:
+                    out += [x.strip() for x in body]
+        out += ["__builtin_amdgcn_sched_barrier(0);", "__syncthreads();", "__builtin_amdgcn_sched_barrier(0);",
+                "__builtin_amdgcn_s_setprio(1);", "#pragma unroll", f"for (int ks = 0; ks < {KS}; ++ks)",
+                "#pragma unroll", f"  for (int x = 0; x < {TMW}; ++x)", "#pragma unroll",
+                f"    for (int y = 0; y < {TNW}; ++y) acc[x][y] = {builtin}(fa[ks][x], fb[ks][y], acc[x][y], 0, 0, 0);",
+                "__builtin_amdgcn_s_setprio(0);", "__builtin_amdgcn_sched_barrier(0);", "__syncthreads();",
+                "__builtin_amdgcn_sched_barrier(0);"]
+        return [ind + x for x in out]
+
     L = ["  unsigned int k0 = 0;"]
-    L += load_lines()
-    L += store_lines("0")
-    if KT > 1:
-        L.append(f"  k0 = {BK}u;")
-        L += load_lines()
+    L += load_lines(*sets[0])
+    L += store_lines("0", *sets[0])
+    for t in range(1, pf):
+        if t < KT:
+            # keep the tiles' loads in issue order: the loop's vmcnt waits assume it
+            L.append("  __builtin_amdgcn_sched_barrier(0);")
+            L.append(f"  k0 = {t * BK}u;")
+            L += load_lines(*sets[t % nsets])
     L.append("  __syncthreads();")
     L.append(f"  const bool grp1 = wave >= {cfg.num_warps // 2}u;")
     L.append("  if (grp1) __syncthreads();")
     L.append(f"  {opvec} fa[{KS}][{TMW}], fb[{KS}][{TNW}];")
-    L.append(f"  for (int kt = 0; kt < {KT}; ++kt) {{")
-    L.append("    const int cur = kt & 1;")
-    L.append("#pragma unroll")
-    L.append(f"    for (int ks = 0; ks < {KS}; ++ks) {{")
-    L.append("#pragma unroll")
-    L.append(f"      for (int x = 0; x < {TMW}; ++x) fa[ks][x] = *(const {opvec}*)&As[cur][arow + x * {MI}u][ks * {KI} + kofs];")
-    L.append("#pragma unroll")
-    L.append(f"      for (int y = 0; y < {TNW}; ++y) fb[ks][y] = *(const {opvec}*)&Bs[cur][brow + y * {MI}u][ks * {KI} + kofs];")
-    L.append("    }")
-    L.append(f"    if (kt + 1 < {KT}) {{")
-    L += ["    " + s for s in store_lines("cur ^ 1")]
-    L.append("    }")
-    L.append(f"    if (kt + 2 < {KT}) {{")
-    L.append(f"      k0 = (kt + 2) * {BK}u;")
-    L += ["    " + s for s in load_lines()]
-    L.append("    }")
-    L.append("    __builtin_amdgcn_sched_barrier(0);")
-    L.append("    __syncthreads();")
-    L.append("    __builtin_amdgcn_sched_barrier(0);")
-    L.append("    __builtin_amdgcn_s_setprio(1);")
-    L.append("#pragma unroll")
-    L.append(f"    for (int ks = 0; ks < {KS}; ++ks)")
-    L.append("#pragma unroll")
-    L.append(f"      for (int x = 0; x < {TMW}; ++x)")
-    L.append("#pragma unroll")
-    L.append(f"        for (int y = 0; y < {TNW}; ++y) acc[x][y] = {builtin}(fa[ks][x], fb[ks][y], acc[x][y], 0, 0, 0);")
-    L.append("    __builtin_amdgcn_s_setprio(0);")
-    L.append("    __builtin_amdgcn_sched_barrier(0);")
-    L.append("    __syncthreads();")
-    L.append("    __builtin_amdgcn_sched_barrier(0);")
-    L.append("  }")
+    # steps 0 .. KT-PF-1 load tile kt+PF; run them in even/odd pairs, then peel the rest
+    nload = max(0, KT - pf)
+    npair = nload // 2
+    if npair:
+        L.append(f"  for (int kt = 0; kt < {2 * npair}; kt += 2) {{")
+        L += step("kt", 0, True, True, "    ")
+        L += step("kt + 1", 1, True, True, "    ")
+        L.append("  }")
+    for kt in range(2 * npair, KT):
+        L.append(f"  {{  // K step {kt}")
+        L += step(str(kt), kt % 2, kt + 1 < KT, kt + pf < KT, "    ")
+        L.append("  }")
     L.append("  if (!grp1) __syncthreads();")
     return L
 

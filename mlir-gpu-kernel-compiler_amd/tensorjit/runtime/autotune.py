@@ -57,7 +57,7 @@ class MatmulConfig:
     MI: int = 32
     SPLIT_K: int = 1
     GROUP_M: int = 8        # tile rows per group of the XCD-aware tile order (0 = plain row-major order)
-    PINGPONG: int = 0       # 1: two wave groups alternate MFMA and memory phases (8 waves)
+    PINGPONG: int = 0       # n>0: two wave groups alternate MFMA and memory phases, loads n+1 K steps ahead
 
     def as_dict(self) -> dict:
         return {"TM": self.TM, "TN": self.TN, "TK": self.TK, "num_warps": self.num_warps,
@@ -76,6 +76,9 @@ HIP_CANDIDATES: list[MatmulConfig] = [
     MatmulConfig(256, 256, 32, 8, 2, 4, 32, 1, 8, 1),
     MatmulConfig(256, 256, 32, 8, 4, 2, 32, 1, 8, 1),
     MatmulConfig(256, 128, 32, 8, 4, 2, 32, 1, 8, 1),
+    MatmulConfig(256, 256, 32, 8, 2, 4, 32, 1, 8, 2),
+    MatmulConfig(256, 256, 32, 8, 4, 2, 32, 1, 8, 2),
+    MatmulConfig(256, 128, 32, 8, 4, 2, 32, 1, 8, 2),
     MatmulConfig(256, 256, 64, 8, 2, 4, 32),
     MatmulConfig(256, 256, 32, 8, 2, 4, 32),
     MatmulConfig(256, 128, 64, 8, 4, 2, 32),

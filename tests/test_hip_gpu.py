@@ -456,7 +456,7 @@ def test_every_bf16_tile_config_is_exact_on_integer_data(tb):
     from tensorjit.runtime.autotune import HIP_CANDIDATES
 
     torch.manual_seed(0)
-    for m, n, kk in [(300, 520, 136), (16, 200, 512)]:
+    for m, n, kk in [(300, 520, 136), (100, 72, 40), (16, 200, 512)]:
         a = torch.randint(-2, 3, (m, kk), device=DEV).bfloat16()
         b = torch.randint(-2, 3, (n, kk) if tb else (kk, n), device=DEV).bfloat16()
         fn = (lambda x, y: tj.linear(x, y)) if tb else (lambda x, y: tj.matmul(x, y))
