@@ -149,7 +149,7 @@ def cpu_baseline(torch, args_gpu, nbytes, seconds):
         prog(*host)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 200:
+        if el >= seconds or n >= 5000:
             break
     per = el / n
     cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
@@ -254,7 +254,8 @@ def secondary(torch, dev, quick):
 def profile_set(torch, dev, steps) -> None:
     """Kernels for rocprofv3 counter runs: the headline kernel, a plain copy-like
     calibration kernel of known traffic (y = x + 0.5, fp32 [16384,4096]: 256 MiB
-    read + 256 MiB written) and the row configs, ``steps`` launches each."""
+    read + 256 MiB written), the row configs and the config-4 bf16 GEMM, ``steps``
+    launches each."""
     import tensorjit as tj
 
     args = c2_inputs(torch, torch.float32, dev)
@@ -278,6 +279,13 @@ def profile_set(torch, dev, steps) -> None:
     jf = tj.jit(_fn_softmax)
     for _ in range(steps):
         jf(s)
+    del s
+    xg = torch.randn(8192, 8192, device=dev, generator=gen).bfloat16()
+    wg = (0.02 * torch.randn(8192, 8192, device=dev, generator=gen)).bfloat16()
+    bg = (0.02 * torch.randn(8192, device=dev, generator=gen)).bfloat16()
+    jf = tj.jit(_fn_gemm)
+    for _ in range(steps):
+        jf(xg, wg, bg)
     torch.cuda.synchronize()
     log(f"profile set done ({steps} launches per kernel)")
 
@@ -287,7 +295,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget (seconds)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--quick", action="store_true", help="skip the GEMM / MLP secondaries")
