@@ -78,15 +78,19 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
             a, b = mm.inputs
             ok = tb and M <= cfg.TM and K % 8 == 0 and a.dtype == b.dtype == dt
         return ok
+    if cfg.INTERLEAVE and (cfg.PINGPONG or (cfg.TK // ki) % 2):
+        return False
     if cfg.PINGPONG:
-        if cfg.num_warps % 2 or cfg.PINGPONG > 2:
+        ks = cfg.TK // ki
+        if cfg.num_warps % 2 or cfg.PINGPONG > 3 or (cfg.PINGPONG == 3 and ks % 2):
             return False
-        # ping-pong holds accumulators, one step's fragments and PINGPONG staging sets
-        # in registers at once; past ~216 of the 256 VGPRs (addresses need the rest) it spills
+        # ping-pong holds accumulators, one step's fragments and its staging registers at
+        # once; past ~216 of the 256 VGPRs (addresses need the rest) it spills
         tmw, tnw = cfg.TM // (cfg.WM * cfg.MI), cfg.TN // (cfg.WN * cfg.MI)
         acc = tmw * tnw * cfg.MI * cfg.MI // 64
-        frag = (cfg.TK // ki) * (tmw + tnw) * 4
-        stage = cfg.PINGPONG * (cfg.TM + cfg.TN) * cfg.TK * dt.itemsize // (cfg.num_warps * 64 * 4)
+        frag = (ks // 2 if cfg.PINGPONG == 3 else ks) * (tmw + tnw) * 4
+        sets = 2 if cfg.PINGPONG == 2 else 1
+        stage = sets * (cfg.TM + cfg.TN) * cfg.TK * dt.itemsize // (cfg.num_warps * 64 * 4)
         if acc + frag + stage > 216:
             return False
     return (cfg.WM * cfg.WN == cfg.num_warps and cfg.TM % (cfg.WM * cfg.MI) == 0
@@ -440,7 +444,7 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     a_st_t, b_st_t = stage_type(a_ve, a.dtype), stage_type(b_ve, b.dtype)
     L.append(f"  {a_st_t} ra[{a_cnt}];")
     L.append(f"  {b_st_t} rb[{b_cnt}];")
-    if cfg.PINGPONG > 1:
+    if cfg.PINGPONG == 2:
         L.append(f"  {a_st_t} ra2[{a_cnt}];")
         L.append(f"  {b_st_t} rb2[{b_cnt}];")
 
@@ -450,7 +454,15 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
             return expr
         return f"tj_ld({expr})"   # fp32 LDS path for mixed / integer operands
 
-    def load_lines(sa: str = "ra", sb: str = "rb") -> list[str]:
+    def load_lines(sa: str = "ra", sb: str = "rb", parts: str = "ab") -> list[str]:
+        out = []
+        if "a" in parts:
+            out += a_load_lines(sa)
+        if "b" in parts:
+            out += b_load_lines(sb)
+        return out
+
+    def a_load_lines(sa: str) -> list[str]:
         out = ["#pragma unroll", f"  for (int i = 0; i < {a_cnt}; ++i) {{",
                f"    const unsigned int c = i * {THREADS}u + tid;"]
         if a_tot % THREADS:
@@ -473,9 +485,11 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
             zero = f"({lds_t})0"
         out.append(f"    {sa}[i] = ({cond}) ? {ld} : {zero};" if cond else f"    {sa}[i] = {ld};")
         out.append("  }")
-        # B
-        out += ["#pragma unroll", f"  for (int i = 0; i < {b_cnt}; ++i) {{",
-                f"    const unsigned int c = i * {THREADS}u + tid;"]
+        return out
+
+    def b_load_lines(sb: str) -> list[str]:
+        out = ["#pragma unroll", f"  for (int i = 0; i < {b_cnt}; ++i) {{",
+               f"    const unsigned int c = i * {THREADS}u + tid;"]
         if b_tot % THREADS:
             out.append(f"    if (c >= {b_tot}u) break;")
         if tb:
@@ -502,7 +516,15 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         out.append("  }")
         return out
 
-    def store_lines(buf: str, sa: str = "ra", sb: str = "rb") -> list[str]:
+    def store_lines(buf: str, sa: str = "ra", sb: str = "rb", parts: str = "ab") -> list[str]:
+        out = []
+        if "a" in parts:
+            out += a_store_lines(buf, sa)
+        if "b" in parts:
+            out += b_store_lines(buf, sb)
+        return out
+
+    def a_store_lines(buf: str, sa: str) -> list[str]:
         out = ["#pragma unroll", f"  for (int i = 0; i < {a_cnt}; ++i) {{",
                f"    const unsigned int c = i * {THREADS}u + tid;"]
         if a_tot % THREADS:
@@ -514,8 +536,11 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         else:
             out.append(f"    As[{buf}][row][kk] = {sa}[i];")
         out.append("  }")
-        out += ["#pragma unroll", f"  for (int i = 0; i < {b_cnt}; ++i) {{",
-                f"    const unsigned int c = i * {THREADS}u + tid;"]
+        return out
+
+    def b_store_lines(buf: str, sb: str) -> list[str]:
+        out = ["#pragma unroll", f"  for (int i = 0; i < {b_cnt}; ++i) {{",
+               f"    const unsigned int c = i * {THREADS}u + tid;"]
         if b_tot % THREADS:
             out.append(f"    if (c >= {b_tot}u) break;")
         if tb:
@@ -587,6 +612,11 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         out.append("  }")
         return out
 
+    if cfg.INTERLEAVE:
+        L += interleaved_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_lines, store_lines,
+                                    a_cnt, b_cnt)
+        return _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW,
+                              TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
     if cfg.PINGPONG:
         L += pingpong_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_lines, store_lines)
         return _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW,
@@ -623,29 +653,36 @@ def pingpong_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_
     """Main loop with two wave groups a phase apart ("ping-pong").
 
     Waves ``[0, W/2)`` and ``[W/2, W)`` form two groups; each SIMD runs one wave of
-    each.  Every K step is a memory phase (read this step's fragments from LDS
-    stage ``kt & 1``, write the staged tile kt+1 to the other stage, issue the
-    global loads of tile kt+PF) and a compute phase (the step's MFMA burst at raised
-    priority), separated by barriers.  Group 1 starts one barrier late, so on every
-    SIMD one wave computes while the other moves data.  Ordering: tile kt+1 is
-    written in phases 2kt (group 0) and 2kt+1 (group 1) and first read in phase
-    2kt+2; the stage it overwrites was last read in phase 2kt-1.  Every wave
-    executes 2*KT+2 barriers in total (one extra at the start or the end).
+    each.  Every step is a memory phase (read the step's fragments from LDS stage
+    ``kt & 1``, write staged data of tile kt+1 to the other stage, issue global loads)
+    and a compute phase (the step's MFMA burst at raised priority), separated by
+    barriers.  Group 1 starts one barrier late, so on every SIMD one wave computes
+    while the other moves data.  Ordering: tile kt+1 is written in the memory phases
+    of tile kt and first read after the barrier that ends them; the stage it overwrites
+    was last read before the barrier that starts them.  Every wave executes the same
+    number of barriers plus one (at the start for group 1, at the end for group 0).
 
-    Prefetch distance ``PF = PINGPONG + 1``: tile t's global loads are issued at K
-    step t-PF into staging register set ``t % (PF-1)`` and written to LDS at step t-1,
-    so PF-1 steps of load latency are hidden.  The loop body holds two K steps (even
-    and odd), which makes every LDS stage and register set a compile-time choice; the
-    last steps, which have no tile left to load, are peeled."""
-    pf = cfg.PINGPONG + 1
+    ``PINGPONG`` 1 and 2: one step per tile; tile t's global loads are issued at step
+    t-PF (PF = PINGPONG + 1) into staging register set ``t % (PF-1)`` and written to LDS
+    at step t-1.  ``PINGPONG`` 3: tiles are twice as wide in K as a step (BK = 64 bf16
+    = a full 128-byte line per row, half the L2 requests of BK = 32) and each tile is
+    computed in two half steps; the first half step moves the A part of the staged
+    tile, the second the B part, so PF = 2 with one register set.  The loop body holds
+    two tiles (even and odd), which makes every LDS stage and register set a
+    compile-time choice; the last tiles, which have no tile left to load, are peeled."""
+    split = cfg.PINGPONG == 3
+    pf = 2 if split else cfg.PINGPONG + 1
     nsets = pf - 1
     sets = [("ra", "rb"), ("ra2", "rb2")][:nsets]
+    ksh = KS // 2 if split else KS
+    halves = [(0, ksh, "a"), (ksh, KS, "b")] if split else [(0, KS, "ab")]
 
-    def step(kt: str, stage: int, do_store: bool, do_load: bool, ind: str) -> list[str]:
-        out = ["#pragma unroll", f"for (int ks = 0; ks < {KS}; ++ks) {{", "#pragma unroll",
-               f"  for (int x = 0; x < {TMW}; ++x) fa[ks][x] = *(const {opvec}*)&As[{stage}][arow + x * {MI}u][ks * {KI} + kofs];",
+    def step(kt: str, stage: int, ks0: int, ks1: int, parts: str, do_store: bool, do_load: bool,
+             ind: str) -> list[str]:
+        out = ["#pragma unroll", f"for (int ks = {ks0}; ks < {ks1}; ++ks) {{", "#pragma unroll",
+               f"  for (int x = 0; x < {TMW}; ++x) fa[ks - {ks0}][x] = *(const {opvec}*)&As[{stage}][arow + x * {MI}u][ks * {KI} + kofs];",
                "#pragma unroll",
-               f"  for (int y = 0; y < {TNW}; ++y) fb[ks][y] = *(const {opvec}*)&Bs[{stage}][brow + y * {MI}u][ks * {KI} + kofs];",
+               f"  for (int y = 0; y < {TNW}; ++y) fb[ks - {ks0}][y] = *(const {opvec}*)&Bs[{stage}][brow + y * {MI}u][ks * {KI} + kofs];",
                "}"]
         if do_store or do_load:
             # tile kt+1 lives in set (kt+1) % nsets; kt+PF maps to the same set
@@ -653,13 +690,13 @@ def pingpong_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_
             for j, (sa, sb) in enumerate(sets):
                 body = []
                 if do_store:
-                    body += store_lines(str(1 - stage), sa, sb)
+                    body += store_lines(str(1 - stage), sa, sb, parts)
                 if do_store and do_load:
                     # loads after the stores: hoisted above the fragment reads they slow the phase
                     body.append("__builtin_amdgcn_sched_barrier(0);")
                 if do_load:
                     body.append(f"k0 = (({kt}) + {pf}) * {BK}u;")
-                    body += load_lines(sa, sb)
+                    body += load_lines(sa, sb, parts)
                 if nsets > 1:
                     out.append(f"if ({sel} == {j}) {{")
                     out += ["  " + x.strip() for x in body]
@@ -667,12 +704,18 @@ def pingpong_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_
                 else:
                     out += [x.strip() for x in body]
         out += ["__builtin_amdgcn_sched_barrier(0);", "__syncthreads();", "__builtin_amdgcn_sched_barrier(0);",
-                "__builtin_amdgcn_s_setprio(1);", "#pragma unroll", f"for (int ks = 0; ks < {KS}; ++ks)",
+                "__builtin_amdgcn_s_setprio(1);", "#pragma unroll", f"for (int ks = 0; ks < {ks1 - ks0}; ++ks)",
                 "#pragma unroll", f"  for (int x = 0; x < {TMW}; ++x)", "#pragma unroll",
                 f"    for (int y = 0; y < {TNW}; ++y) acc[x][y] = {builtin}(fa[ks][x], fb[ks][y], acc[x][y], 0, 0, 0);",
                 "__builtin_amdgcn_s_setprio(0);", "__builtin_amdgcn_sched_barrier(0);", "__syncthreads();",
                 "__builtin_amdgcn_sched_barrier(0);"]
         return [ind + x for x in out]
+
+    def tile(kt: str, stage: int, do_store: bool, do_load: bool, ind: str) -> list[str]:
+        out = []
+        for ks0, ks1, parts in halves:
+            out += step(kt, stage, ks0, ks1, parts, do_store, do_load, ind)
+        return out
 
     L = ["  unsigned int k0 = 0;"]
     L += load_lines(*sets[0])
@@ -686,20 +729,110 @@ def pingpong_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_
     L.append("  __syncthreads();")
     L.append(f"  const bool grp1 = wave >= {cfg.num_warps // 2}u;")
     L.append("  if (grp1) __syncthreads();")
-    L.append(f"  {opvec} fa[{KS}][{TMW}], fb[{KS}][{TNW}];")
-    # steps 0 .. KT-PF-1 load tile kt+PF; run them in even/odd pairs, then peel the rest
+    L.append(f"  {opvec} fa[{ksh}][{TMW}], fb[{ksh}][{TNW}];")
+    # tiles 0 .. KT-PF-1 load tile kt+PF; run them in even/odd pairs, then peel the rest
     nload = max(0, KT - pf)
     npair = nload // 2
     if npair:
         L.append(f"  for (int kt = 0; kt < {2 * npair}; kt += 2) {{")
-        L += step("kt", 0, True, True, "    ")
-        L += step("kt + 1", 1, True, True, "    ")
+        L += tile("kt", 0, True, True, "    ")
+        L += tile("kt + 1", 1, True, True, "    ")
         L.append("  }")
     for kt in range(2 * npair, KT):
-        L.append(f"  {{  // K step {kt}")
-        L += step(str(kt), kt % 2, kt + 1 < KT, kt + pf < KT, "    ")
+        L.append(f"  {{  // K tile {kt}")
+        L += tile(str(kt), kt % 2, kt + 1 < KT, kt + pf < KT, "    ")
         L.append("  }")
     L.append("  if (!grp1) __syncthreads();")
+    return L
+
+
+# __builtin_amdgcn_sched_group_barrier instruction classes
+SG_MFMA, SG_VMEM_READ, SG_DS_READ, SG_DS_WRITE = 0x008, 0x020, 0x100, 0x200
+
+
+def interleaved_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, load_lines, store_lines,
+                           a_cnt, b_cnt) -> list[str]:
+    """Main loop for one wave per SIMD (``INTERLEAVE``): the wave's own memory traffic
+    is threaded between its MFMAs instead of being given to a second wave.
+
+    Each wave owns a large output tile (128x128 of a 256x256 block: accumulators in
+    the 256 AGPRs), so every 16-byte fragment read feeds twice as many MFMAs as in the
+    8-wave layouts.  Tile kt (LDS stage ``kt & 1``) is computed in KS sub-steps with
+    fragments double-buffered in registers.  The first KS-1 sub-steps form one
+    scheduling region holding their MFMAs, the fragment reads of the next sub-steps,
+    the LDS stores of the staged tile kt+1 (into the other stage) and the global loads
+    of tile kt+2 (into the staging registers just stored); ``sched_group_barrier``
+    places one memory instruction after each MFMA.  One barrier per tile follows (the
+    stores are complete and the other stage is no longer read), then the last
+    sub-step's MFMAs run with the reads of tile kt+1's first fragments."""
+    nmm = TMW * TNW                      # MFMAs per sub-step
+
+    def frag_reads(buf: str, stage: int, ks: str) -> list[str]:
+        return ["#pragma unroll",
+                f"for (int x = 0; x < {TMW}; ++x) fa[{buf}][x] = *(const {opvec}*)&As[{stage}][arow + x * {MI}u][({ks}) * {KI} + kofs];",
+                "#pragma unroll",
+                f"for (int y = 0; y < {TNW}; ++y) fb[{buf}][y] = *(const {opvec}*)&Bs[{stage}][brow + y * {MI}u][({ks}) * {KI} + kofs];"]
+
+    def mfmas(buf: str) -> list[str]:
+        return ["#pragma unroll", f"for (int x = 0; x < {TMW}; ++x)", "#pragma unroll",
+                f"  for (int y = 0; y < {TNW}; ++y) acc[x][y] = {builtin}(fa[{buf}][x], fb[{buf}][y], acc[x][y], 0, 0, 0);"]
+
+    def pattern(n_mfma: int, n_read: int, n_write: int, n_vmem: int) -> list[str]:
+        """One MFMA, then at most one memory instruction, repeated: reads first, then
+        stores, then global loads, spread evenly over the MFMAs."""
+        out = []
+        mem = [SG_DS_READ] * n_read + [SG_DS_WRITE] * n_write + [SG_VMEM_READ] * n_vmem
+        per = max(1, -(-len(mem) // max(n_mfma, 1)))
+        for i in range(n_mfma):
+            out.append(f"__builtin_amdgcn_sched_group_barrier({SG_MFMA}, 1, 0);")
+            for m in mem[i * per:(i + 1) * per]:
+                out.append(f"__builtin_amdgcn_sched_group_barrier({m}, 1, 0);")
+        return out
+
+    def tile(kt: str, stage: int, do_store: bool, do_load: bool, next_reads: bool, ind: str) -> list[str]:
+        out = []
+        # region A: sub-steps 0 .. KS-2
+        for ks in range(KS - 1):
+            out += mfmas(str(ks % 2))
+            out += frag_reads(str((ks + 1) % 2), stage, str(ks + 1))
+        if do_store:
+            out += [x.strip() for x in store_lines(str(1 - stage))]
+        if do_load:
+            out.append(f"k0 = (({kt}) + 2) * {BK}u;")
+            out += [x.strip() for x in load_lines()]
+        nreads = (KS - 1) * (TMW + TNW)
+        out += pattern((KS - 1) * nmm, nreads, (a_cnt + b_cnt) if do_store else 0, (a_cnt + b_cnt) if do_load else 0)
+        out += ["__builtin_amdgcn_sched_barrier(0);", "__syncthreads();", "__builtin_amdgcn_sched_barrier(0);"]
+        # region B: last sub-step, with the next tile's first fragments
+        out += mfmas(str((KS - 1) % 2))
+        if next_reads:
+            out += frag_reads(str(KS % 2), 1 - stage, "0")
+        out += pattern(nmm, (TMW + TNW) if next_reads else 0, 0, 0)
+        out.append("__builtin_amdgcn_sched_barrier(0);")
+        return [ind + x for x in out]
+
+    assert KS % 2 == 0, "interleaved schedule needs an even number of sub-steps per tile"
+    L = ["  unsigned int k0 = 0;"]
+    L += load_lines()
+    L += store_lines("0")
+    if KT > 1:
+        L.append("  __builtin_amdgcn_sched_barrier(0);")
+        L.append(f"  k0 = {BK}u;")
+        L += load_lines()
+    L.append("  __syncthreads();")
+    L.append(f"  {opvec} fa[2][{TMW}], fb[2][{TNW}];")
+    L += ["  " + x for x in frag_reads("0", 0, "0")]
+    nload = max(0, KT - 2)
+    npair = nload // 2
+    if npair:
+        L.append(f"  for (int kt = 0; kt < {2 * npair}; kt += 2) {{")
+        L += tile("kt", 0, True, True, True, "    ")
+        L += tile("kt + 1", 1, True, True, True, "    ")
+        L.append("  }")
+    for kt in range(2 * npair, KT):
+        L.append(f"  {{  // K tile {kt}")
+        L += tile(str(kt), kt % 2, kt + 1 < KT, kt + 2 < KT, kt + 1 < KT, "    ")
+        L.append("  }")
     return L
 
 
