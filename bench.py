@@ -159,6 +159,55 @@ def cpu_baseline(torch, args_gpu, nbytes, seconds):
             "ms_per_call": round(per * 1e3, 3)}
 
 
+def cpu_secondary(torch, seconds_cap: float = 20.0) -> dict:
+    """The CPU oracle (C/OpenMP restatement of the reference ``c`` backend, fp32 only)
+    on the secondary configurations: config 1 per call (warmup 3, iters 20), the
+    config-3 rows on fp32 copies (1 warmup, 3 iters),
+    and config 4 on a 128-row sample of x scaled to the full 8192 rows."""
+    import oracle
+
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    gen = torch.Generator().manual_seed(0)
+    out = {"kind": "port", "cores": cores, "dtype": "f32 (bf16 configs on fp32 copies)"}
+    t_start = time.perf_counter()
+
+    def timed(fn, args, warmup, iters):
+        prog = oracle.compile_program(oracle.lower_f32(fn, *[t.shape for t in args]))
+        for _ in range(warmup):
+            prog(*args)
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            prog(*args)
+        return (time.perf_counter() - t0) / iters
+
+    shapes = [(512, 768), (768,), (3072, 768), (3072,), (768, 3072), (768,)]
+    margs = [torch.randn(sh, generator=gen) * (1 if i < 2 else 0.02) for i, sh in enumerate(shapes)]
+    out["c1_mlp_us_per_call"] = round(timed(_fn_mlp, margs, 3, 20) * 1e6, 1)
+    x = torch.randn(65536, 4096, generator=gen).bfloat16().float()
+    gn = (1 + 0.1 * torch.randn(4096, generator=gen)).bfloat16().float()
+    nb = 2 * 65536 * 4096 * 2 + 4096 * 2
+    for name, fn in (("c3_layernorm", _fn_ln), ("c3_rmsnorm", _fn_rms)):
+        if time.perf_counter() - t_start < seconds_cap:
+            t = timed(fn, [x, gn], 1, 3)
+            out[name] = {"ms_per_call": round(t * 1e3, 2), "GB/s_bf16_equiv": round(nb / t / 1e9, 2)}
+    del x
+    sm = torch.randn(65536, 2048, generator=gen) * 3
+    if time.perf_counter() - t_start < seconds_cap:
+        t = timed(_fn_softmax, [sm], 1, 3)
+        out["c3_softmax"] = {"ms_per_call": round(t * 1e3, 2), "GB/s": round(2 * 65536 * 2048 * 4 / t / 1e9, 2)}
+    del sm
+    if time.perf_counter() - t_start < seconds_cap:
+        rows = 128
+        xg = torch.randn(rows, 8192, generator=gen).bfloat16().float()
+        wg = (0.02 * torch.randn(8192, 8192, generator=gen)).bfloat16().float()
+        bg = (0.02 * torch.randn(8192, generator=gen)).bfloat16().float()
+        t = timed(_fn_gemm, [xg, wg, bg], 1, 1) * (8192 / rows)
+        out["c4_gemm_8192"] = {"ms_per_call_est": round(t * 1e3, 1), "TFLOP/s": round(2 * 8192 ** 3 / t / 1e12, 3),
+                               "sample": f"{rows} of 8192 rows of x, time scaled by {8192 // rows}"}
+    log(f"cpu secondary: {out}")
+    return out
+
+
 def secondary(torch, dev, quick):
     import tensorjit as tj
 
@@ -363,6 +412,8 @@ def main() -> int:
     del args
     if not a.no_secondary:
         line["secondary"] = secondary(torch, dev, a.quick)
+        if not a.no_cpu_baseline and not a.quick:
+            line["secondary"]["cpu_oracle"] = cpu_secondary(torch)
     print(json.dumps(line), flush=True)
     return 0
 
