@@ -31,6 +31,7 @@ from ..runtime.autotune import HIP_CANDIDATES, HIP_F32_CANDIDATES, MatmulConfig,
 from ..runtime.cache import AutotuneStore, CodeObjectCache
 from ..runtime.dtypes import TORCH_DTYPE
 from ..runtime.pool import BufferPool
+from .hip_attention import fuse_attention, gen_attention
 from .hip_gemm import compute_dtype, config_ok, gen_matmul, matmul_dims
 from .hip_kernels import KernelGen, Launch, gen_copy, gen_elementwise, gen_row
 from .hip_prelude import PRELUDE
@@ -87,6 +88,8 @@ def generate_kernel(k: Kernel, idx: int, cfg: MatmulConfig | None = None) -> tup
         return gen_row(g, [k], tuple(x.shape[:-1]), x.shape[-1])
     if k.kind == "matmul":
         return gen_matmul(g, cfg or analytic_config(k))
+    if k.kind == "attention":
+        return gen_attention(k, idx)
     raise NotImplementedError(k.kind)
 
 
@@ -140,6 +143,8 @@ class HipProgram:
 
     def __init__(self, program: Program, device: str | torch.device = "cuda", use_graph: bool | None = None,
                  tune: bool = True):
+        # backend-level rewrite of the planned program: attention chains -> one kernel
+        program = fuse_attention(program)
         self.program = program
         self.device = torch.device(device)
         if self.device.type != "cuda":

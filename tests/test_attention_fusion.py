@@ -1,0 +1,94 @@
+"""Fused attention (hip backend rewrite of matmul -> softmax -> matmul), CPU side:
+which planned programs are rewritten, what the rewritten program looks like, and
+that the generated flash-attention kernel compiles for gfx950 with hipRTC."""
+import pytest
+
+import tensorjit as tj
+import tensorjit.compiler as C
+from tensorjit.backends import hip_backend as hb
+from tensorjit.backends.hip_attention import fuse_attention
+from tensorjit.ir import DType, TensorType
+from tensorjit.passes.memory_planner import plan_memory
+
+
+def attn(q, k, v, scale=0.125):
+    s = tj.matmul(q, tj.transpose(k, -1, -2))
+    return tj.matmul(tj.softmax(s * scale if scale != 1.0 else s), v)
+
+
+def lowered(fn, shapes, dtype=DType.bf16):
+    return C.lower(tj.trace(fn, [TensorType(s, dtype) for s in shapes]), "hip")
+
+
+QKV = [(2, 4, 128, 64), (2, 4, 128, 64), (2, 4, 128, 64)]
+
+
+def test_plain_attention_chain_becomes_one_kernel():
+    p = lowered(attn, QKV)
+    assert [k.kind for k in p.kernels] == ["matmul", "row", "matmul"]
+    f = fuse_attention(p)
+    assert [k.kind for k in f.kernels] == ["attention"]
+    k = f.kernels[0]
+    assert [i.shape for i in k.inputs] == [(2, 4, 128, 64)] * 3
+    assert k.outputs[0].shape == (2, 4, 128, 64) and k.attn["scale"] == 0.125
+    # the scores and probabilities get no arena space any more
+    assert plan_memory(p).arena_bytes >= 2 * 4 * 128 * 128 * 2
+    assert plan_memory(f).arena_bytes == 0
+
+
+def test_unscaled_and_differently_sized_value_heads():
+    f = fuse_attention(lowered(lambda q, k, v: attn(q, k, v, 1.0), [(3, 50, 32), (3, 70, 32), (3, 70, 96)]))
+    assert [k.kind for k in f.kernels] == ["attention"] and f.kernels[0].attn["scale"] == 1.0
+
+
+@pytest.mark.parametrize("case", ["fp32", "probs_returned", "scores_reused", "head_dim_8", "extra_epilogue"])
+def test_chains_that_must_stay_unfused(case):
+    if case == "fp32":
+        p = lowered(attn, QKV, DType.f32)
+    elif case == "probs_returned":
+        def fn(q, k, v):
+            pr = tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * 0.1)
+            return tj.matmul(pr, v), pr
+        p = lowered(fn, QKV)
+    elif case == "scores_reused":
+        def fn(q, k, v):
+            s = tj.matmul(q, tj.transpose(k, -1, -2)) * 0.1
+            return tj.matmul(tj.softmax(s), v) + tj.sum(s, axis=-1, keepdim=True)
+        p = lowered(fn, QKV)
+    elif case == "head_dim_8":
+        p = lowered(attn, [(2, 16, 8)] * 3)
+    else:
+        p = lowered(lambda q, k, v: tj.relu(attn(q, k, v)), QKV)
+    f = fuse_attention(p)
+    assert all(k.kind != "attention" for k in f.kernels)
+
+
+def test_env_switch_keeps_the_reference_plan(monkeypatch):
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION", "0")
+    p = lowered(attn, QKV)
+    assert fuse_attention(p) is p
+
+
+def test_config5_block_fuses_its_attention():
+    import bench
+
+    shapes = [(4, 2048, 4096), (4096,), (4096, 4096), (4096, 4096), (4096, 4096), (4096, 4096), (4096,),
+              (11008, 4096), (4096, 11008)]
+    p = lowered(bench._fn_block, shapes)
+    assert len(p.kernels) == 16
+    f = fuse_attention(p)
+    assert len(f.kernels) == 14 and [k.kind for k in f.kernels].count("attention") == 1
+    # the 1 GiB score and probability buffers are gone from the arena (2.25 GiB -> 428 MiB)
+    assert plan_memory(f).arena_bytes < plan_memory(p).arena_bytes - 1.5 * 2**30
+
+
+@pytest.mark.parametrize("dtype", [DType.bf16, DType.f16])
+@pytest.mark.parametrize("shapes", [QKV, [(1, 100, 32), (1, 75, 32), (1, 75, 64)], [(2, 2, 256, 128)] * 3])
+def test_flash_kernel_compiles_for_gfx950(shapes, dtype, tj_env):
+    f = fuse_attention(lowered(attn, shapes, dtype))
+    src, launches = hb.generate(f)
+    (l,) = launches
+    assert "attention" in l.name and l.block == (256, 1, 1)
+    assert l.grid == (-(-shapes[0][-2] // 128), l.meta["batch"], 1)
+    code = hb.compile_source(src, "gfx950")
+    assert len(code) > 1000

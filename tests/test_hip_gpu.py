@@ -237,6 +237,49 @@ def test_attention_shaped_batched_matmuls_bf16():
     close_lowp(out, ref, tol=3e-2)
 
 
+ATTN = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * 0.125), v)  # noqa: E731
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shapes", [[(2, 4, 128, 64)] * 3, [(1, 100, 32), (1, 75, 32), (1, 75, 64)],
+                                    [(1, 2, 300, 128), (1, 2, 1000, 128), (1, 2, 1000, 128)]],
+                         ids=["even", "ragged_dv64", "multi_block_ragged"])
+def test_fused_attention_vs_oracle_and_unfused_plan(shapes, dt, monkeypatch):
+    """The flash kernel against the fp32 oracle (which runs the reference plan:
+    materialised scores, softmax row kernel, PV product) and against this backend's
+    own unfused three-kernel plan."""
+    torch.manual_seed(0)
+    q, k, v = [torch.randn(sh, device=DEV).to(dt) for sh in shapes]
+    print(f"attention {shapes} {dt}", flush=True)
+    f = tj.jit(ATTN)
+    out = f(q, k, v)
+    cp = f.compiled(q, k, v)
+    assert cp.num_kernels == 1 and "attention" in cp.launches[0].name
+    (ref,) = oracle.run(ATTN, *[t.float().cpu() for t in (q, k, v)])
+    close_lowp(out, ref, tol=2e-2)
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION", "0")
+    f3 = tj.jit(ATTN)
+    out3 = f3(q, k, v)
+    assert f3.compiled(q, k, v).num_kernels == 3
+    close_lowp(out, out3, tol=2e-2)
+
+
+def test_fused_attention_large_logits_and_unit_scale():
+    """Scores of magnitude ~100 (online max subtraction must keep exp2 in range) and
+    no scale multiply in the chain."""
+    torch.manual_seed(1)
+    q = (3 * torch.randn(2, 256, 64, device=DEV)).bfloat16()
+    k = (3 * torch.randn(2, 640, 64, device=DEV)).bfloat16()
+    v = torch.randn(2, 640, 96, device=DEV).bfloat16()
+    fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2))), v)  # noqa: E731
+    f = tj.jit(fn)
+    out = f(q, k, v)
+    assert f.compiled(q, k, v).num_kernels == 1
+    ref = torch.softmax(q.float() @ k.float().transpose(-1, -2).contiguous(), -1) @ v.float()
+    assert torch.isfinite(out.float()).all()
+    close_lowp(out, ref, tol=3e-2)
+
+
 # ------------------------------------------------------------------ programs / executor
 
 MLP = lambda x, g, w1, b1, w2, b2: x + tj.linear(tj.gelu(tj.linear(tj.layer_norm(x, g), w1, b1)), w2, b2)  # noqa: E731
