@@ -9,16 +9,17 @@ so the scores never leave the chip and the memory planner no longer reserves
 arena space for them.
 
 ``gen_attention`` emits a gfx950 flash-attention forward kernel: a workgroup of
-4 waves owns 128 query rows (32 per wave) of one (batch, head); key/value blocks
+4 or 8 waves owns 32 query rows per wave of one (batch, head); key/value blocks
 of 64 rows stream through double-buffered LDS.  Each wave computes the scores
 transposed, ``Sᵀ = K·Qᵀ`` (MFMA 32x32x16, queries as columns), so every lane owns
 one query column: the online-softmax max / sum need one cross-lane exchange
 (``lane ^ 32``) per block, the rescale of the output accumulator is a per-lane
 multiply, and the probabilities go from the score accumulator straight into the
-B operand of ``Oᵀ += Vᵀ·Pᵀ`` without an LDS round trip.  For that, V is stored
-transposed in LDS with the keys of every 16-key chunk permuted (bits 2 and 3 of
-the key offset swapped) so one 16-byte read returns the keys in the order the
-score accumulator holds them.
+B operand of ``Oᵀ += Vᵀ·Pᵀ`` without an LDS round trip.  V stays in its natural
+``[key][d]`` layout in LDS; the ``Vᵀ`` operand is gathered with gfx950's
+transposing LDS read ``ds_read_b64_tr_b16`` (within each 16 lanes, lane ``i``
+receives element ``i % 4`` of the 8-byte rows loaded by lanes ``4e + i / 4``,
+e = 0..3), two per fragment, in the key order of the score accumulator.
 """
 from __future__ import annotations
 
@@ -30,7 +31,6 @@ from ..passes import Kernel, Program
 from .hip_prelude import CTYPE
 
 BQ_PER_WAVE = 32
-WAVES = 4
 BKV = 64
 MAX_HEAD_DIM = 128
 
@@ -120,7 +120,7 @@ def match_attention(program: Program, i3: int) -> dict | None:
         return None
     if D % 16 or D > MAX_HEAD_DIM or Dv % 32 or Dv > MAX_HEAD_DIM or Sq < 1 or Sk < 1:
         return None
-    if math.prod(q.shape[:-2]) > 65535:         # one (batch, head) per grid row
+    if math.prod(q.shape[:-2]) > 65535 or scale == 0.0:   # one (batch, head) per grid row
         return None
     return {"i1": i1, "i2": i2, "i3": i3, "q": q, "k": kk, "v": v, "out": mm3, "scale": float(scale),
             "nodes": k1.nodes + k2.nodes + k3.nodes}
@@ -157,9 +157,11 @@ def fuse_attention(program: Program) -> Program:
 # ---------------------------------------------------------------------------
 
 
-def _perm16(x: str) -> str:
-    """Position of key offset ``x`` inside its 16-key chunk (bits 2 and 3 swapped)."""
-    return f"((({x}) & ~12u) | ((({x}) & 4u) << 1) | ((({x}) & 8u) >> 1))"
+def attention_waves(Sq: int, D: int, Dv: int) -> int:
+    """Waves per workgroup (32 query rows each).  Eight share every K/V block that
+    passes through LDS between twice as many queries (half the L2->CU traffic of
+    four) when the shapes divide evenly and there are enough query rows."""
+    return 8 if D % 64 == 0 and Dv % 64 == 0 and Sq >= 512 else 4
 
 
 def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
@@ -173,10 +175,14 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     batch = math.prod(q.shape[:-2]) if len(q.shape) > 2 else 1
     Sq, D = q.shape[-2:]
     Sk, Dv = kk.shape[-2], v.shape[-1]
-    NW, THREADS = WAVES, WAVES * 64
+    NW = attention_waves(Sq, D, Dv)
+    THREADS = NW * 64
     BQ = BQ_PER_WAVE * NW
     KB = -(-Sk // BKV)
-    DP, VP = D + 8, BKV + 8                     # 16-byte row padding: conflict-free fragment reads
+    DP = D + 8                                  # 16-byte row padding: conflict-free fragment reads
+    # V rows: a transposing read touches 8 rows x 64 bytes; a pitch of 32 or 96 (mod 128)
+    # elements puts rows r and r+1..r+3 on disjoint bank ranges
+    VP = Dv + next(p for p in (0, 32, 64, 96) if (Dv + p) % 128 in (32, 96))
     opvec = "tj_bf16x8" if dt == DType.bf16 else "tj_f16x8"
     mfma = "__builtin_amdgcn_mfma_f32_32x32x16_bf16" if dt == DType.bf16 else "__builtin_amdgcn_mfma_f32_32x32x16_f16"
     KC = BKV * D // 8 // THREADS                  # 16-byte K chunks per lane per block
@@ -199,7 +205,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
          f"    const {T}* __restrict__ in0_p, const {T}* __restrict__ in1_p, const {T}* __restrict__ in2_p,",
          f"    {T}* __restrict__ out0_p) {{",
          f"  __shared__ __attribute__((aligned(16))) {T} Ks[2][{BKV}][{DP}];",
-         f"  __shared__ __attribute__((aligned(16))) {T} Vs[2][{Dv}][{VP}];",
+         f"  __shared__ __attribute__((aligned(16))) {T} Vs[2][{BKV}][{VP}];",
          "  const unsigned int tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;",
          "  const unsigned int g = lane / 32u, col = lane % 32u;",
          f"  const {idx_t} bh = blockIdx.y;",
@@ -219,107 +225,141 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
          "  float m_run = -__builtin_inff(), l_run = 0.0f;",
          f"  tj_u32x4 rk[{KC}], rv[{VC}];"]
 
-    def load(blk: str) -> list[str]:
-        out_l = ["#pragma unroll", f"  for (int i = 0; i < {KC}; ++i) {{",
-                 f"    const unsigned int c = i * {THREADS}u + tid, row = c / {D // 8}u, d8 = (c % {D // 8}u) * 8u;",
-                 f"    unsigned int key = ({blk}) * {BKV}u + row;"]
+    def k_load(blk: str) -> list[str]:
+        out_l = ["#pragma unroll", f"for (int i = 0; i < {KC}; ++i) {{",
+                 f"  const unsigned int c = i * {THREADS}u + tid, row = c / {D // 8}u, d8 = (c % {D // 8}u) * 8u;",
+                 f"  unsigned int key = ({blk}) * {BKV}u + row;"]
         if ragged:
-            out_l.append(f"    key = key < {Sk}u ? key : {Sk - 1}u;")
-        out_l += [f"    rk[i] = *(const tj_u32x4*)&Kb[key * {D}u + d8];", "  }",
-                  "#pragma unroll", f"  for (int i = 0; i < {VC}; ++i) {{",
-                  # consecutive lanes take consecutive keys: the transposing 2-byte LDS
-                  # stores below then hit consecutive addresses
-                  f"    const unsigned int c = i * {THREADS}u + tid, row = c % {BKV}u, d8 = (c / {BKV}u) * 8u;",
-                  f"    unsigned int key = ({blk}) * {BKV}u + row;"]
+            out_l.append(f"  key = key < {Sk}u ? key : {Sk - 1}u;")
+        return out_l + [f"  rk[i] = *(const tj_u32x4*)&Kb[key * {D}u + d8];", "}"]
+
+    def v_load(blk: str) -> list[str]:
+        out_l = ["#pragma unroll", f"for (int i = 0; i < {VC}; ++i) {{",
+                 f"  const unsigned int c = i * {THREADS}u + tid, row = c / {Dv // 8}u, d8 = (c % {Dv // 8}u) * 8u;",
+                 f"  unsigned int key = ({blk}) * {BKV}u + row;"]
         if ragged:
-            out_l.append(f"    key = key < {Sk}u ? key : {Sk - 1}u;")
-        out_l += [f"    rv[i] = *(const tj_u32x4*)&Vb[key * {Dv}u + d8];", "  }"]
+            out_l.append(f"  key = key < {Sk}u ? key : {Sk - 1}u;")
+        return out_l + [f"  rv[i] = *(const tj_u32x4*)&Vb[key * {Dv}u + d8];", "}"]
+
+    def k_store(stage: int) -> list[str]:
+        return ["#pragma unroll", f"for (int i = 0; i < {KC}; ++i) {{",
+                f"  const unsigned int c = i * {THREADS}u + tid, row = c / {D // 8}u, d8 = (c % {D // 8}u) * 8u;",
+                f"  *(tj_u32x4*)&Ks[{stage}][row][d8] = rk[i];", "}"]
+
+    def v_store(stage: int) -> list[str]:
+        return ["#pragma unroll", f"for (int i = 0; i < {VC}; ++i) {{",
+                f"  const unsigned int c = i * {THREADS}u + tid, row = c / {Dv // 8}u, d8 = (c % {Dv // 8}u) * 8u;",
+                f"  *(tj_u32x4*)&Vs[{stage}][row][d8] = rv[i];", "}"]
+
+    def scores(dst: str, stage: int) -> list[str]:
+        """S^T = K Q^T over D in 16-wide chunks: tile t covers keys t*32 .. t*32+31."""
+        return ["#pragma unroll", f"for (int t = 0; t < {BKV // 32}; ++t) {dst}[t] = (tj_f32x16)(0.0f);",
+                "#pragma unroll", f"for (int c = 0; c < {D // 16}; ++c)", "#pragma unroll",
+                f"  for (int t = 0; t < {BKV // 32}; ++t)",
+                f"    {dst}[t] = {mfma}(*(const {opvec}*)&Ks[{stage}][t * 32 + col][c * 16 + g * 8u], qf[c], {dst}[t], 0, 0, 0);"]
+
+    # online softmax, one query column per lane (its 32 keys here + lane ^ 32's 32).
+    # The extreme is taken on the raw scores (max(s*cs) = cs*max(s) for cs > 0, min for
+    # cs < 0) so the scale folds into the exponent's FMA.  Lazy rescaling: the running
+    # reference max moves only when some lane's block max exceeds it by more than 8
+    # (exponents then stay <= 2^8); otherwise the output accumulator is left alone.
+    ext, ext_init, masked = ("fmaxf", "-__builtin_inff()", "-__builtin_inff()") if cs > 0 else \
+        ("fminf", "__builtin_inff()", "__builtin_inff()")
+
+    def block_max(sc: str, j: int | None) -> list[str]:
+        out_l = [f"float mx = {ext_init};", "#pragma unroll", f"for (int t = 0; t < {BKV // 32}; ++t)",
+                 "#pragma unroll", "  for (int r = 0; r < 16; ++r) {"]
+        if ragged and j == KB - 1:
+            out_l.append(f"    if ({j * BKV} + t * 32 + (r / 4) * 8 + (int)g * 4 + r % 4 >= {Sk}) {sc}[t][r] = {masked};")
+        out_l += [f"    mx = {ext}(mx, {sc}[t][r]);", "  }",
+                  f"mx = {ext}(mx, __shfl_xor(mx, 32, 64));",
+                  f"const float mb = mx * {cs!r}f;",
+                  "if (__builtin_amdgcn_ballot_w64(mb > m_run + 8.0f)) {",
+                  "  const float m_new = fmaxf(m_run, mb);",
+                  "  const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);",
+                  "  l_run *= alpha;",
+                  "#pragma unroll",
+                  f"  for (int u = 0; u < {Dv // 32}; ++u) o[u] *= alpha;",
+                  "  m_run = m_new;",
+                  "}"]
         return out_l
 
-    def store(buf: str) -> list[str]:
-        out_l = ["#pragma unroll", f"  for (int i = 0; i < {KC}; ++i) {{",
-                 f"    const unsigned int c = i * {THREADS}u + tid, row = c / {D // 8}u, d8 = (c % {D // 8}u) * 8u;",
-                 f"    *(tj_u32x4*)&Ks[{buf}][row][d8] = rk[i];", "  }",
-                 "#pragma unroll", f"  for (int i = 0; i < {VC}; ++i) {{",
-                 f"    const unsigned int c = i * {THREADS}u + tid, row = c % {BKV}u, d8 = (c / {BKV}u) * 8u;",
-                 f"    const unsigned int pos = (row & ~15u) | {_perm16('row & 15u')};",
-                 "#pragma unroll", "    for (int w = 0; w < 4; ++w) {",
-                 "      const unsigned int x_ = rv[i][w];"]
-        lo, hi = "(unsigned short)(x_ & 0xffffu)", "(unsigned short)(x_ >> 16)"
-        if dt == DType.f16:
-            lo, hi = f"__builtin_bit_cast(_Float16, {lo})", f"__builtin_bit_cast(_Float16, {hi})"
-        out_l += [f"      Vs[{buf}][d8 + 2 * w][pos] = {lo};", f"      Vs[{buf}][d8 + 2 * w + 1][pos] = {hi};",
-                  "    }", "  }"]
+    def probs(sc: str) -> list[str]:
+        """exp2 of the block's scores, their sum, and the P^T operands (chunk 2t+h)."""
+        cvt = ("tj_f2bf2({0}, {1})" if dt == DType.bf16 else "tj_f2h({0}) | (tj_f2h({1}) << 16)")
+        return ["float rs = 0.0f;", "#pragma unroll", f"for (int t = 0; t < {BKV // 32}; ++t)",
+                "#pragma unroll", "  for (int h = 0; h < 2; ++h) {",
+                "    tj_u32x4 pw;", "#pragma unroll", "    for (int w = 0; w < 4; ++w) {",
+                f"      const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[t][8 * h + 2 * w], {cs!r}f, -m_run));",
+                f"      const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[t][8 * h + 2 * w + 1], {cs!r}f, -m_run));",
+                "      rs += e0 + e1;",
+                "      pw[w] = " + cvt.format("e0", "e1") + ";",
+                "    }",
+                f"    pf[2 * t + h] = __builtin_bit_cast({opvec}, pw);",
+                "  }"]
+
+    def pv(stage: int) -> list[str]:
+        """O^T += V^T P^T.  The V^T fragment of chunk ch holds keys ch*16 + g*4 + 0..3 then
+        ch*16 + 8 + g*4 + 0..3 (the score accumulator's order) for d = u*32 + lane % 32,
+        gathered by two transposing reads of V's natural rows."""
+        return ["#pragma unroll", f"for (int ch = 0; ch < {BKV // 16}; ++ch) {{",
+                "  const unsigned int vrow = ch * 16 + g * 4u + (lane % 16u) / 4u;",
+                "#pragma unroll", f"  for (int u = 0; u < {Dv // 32}; ++u) {{",
+                "    const unsigned int vcol = u * 32 + ((lane / 16u) % 2u) * 16u + (lane % 4u) * 4u;",
+                f"    tj_i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)&Vs[{stage}][vrow][vcol]);",
+                f"    tj_i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)&Vs[{stage}][vrow + 8u][vcol]);",
+                "    tj_i16x8 vv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);",
+                f"    o[u] = {mfma}(__builtin_bit_cast({opvec}, vv), pf[ch], o[u], 0, 0, 0);",
+                "  }", "}"]
+
+    def iteration(j: str, jc: int | None, par: int, has_next: bool, store_k: bool, store_v: bool,
+                  load_k: bool, load_v: bool) -> list[str]:
+        """Block j: the softmax of S(j) runs while the MFMAs of S(j+1) are in flight,
+        then O += P(j) V(j); K(j+2) and V(j+1) move from registers to LDS and the loads
+        of K(j+3), V(j+2) are issued.  LDS: Ks[(j+1)%2] = K(j+1), Vs[j%2] = V(j)."""
+        sc, sn = ("sA", "sB") if par == 0 else ("sB", "sA")
+        out_l = block_max(sc, jc)
+        if has_next:
+            out_l += scores(sn, 1 - par)
+        out_l += probs(sc)
+        out_l += ["l_run += rs + __shfl_xor(rs, 32, 64);"]
+        out_l += pv(par)
+        if store_k:
+            out_l += k_store(par)
+        if store_v:
+            out_l += v_store(1 - par)
+        if load_k:
+            out_l += k_load(f"({j}) + 3u")
+        if load_v:
+            out_l += v_load(f"({j}) + 2u")
+        out_l.append("__syncthreads();")
         return out_l
 
-    L += load("0u")
-    L += store("0")
+    L += [f"  tj_f32x16 sA[{BKV // 32}], sB[{BKV // 32}];", f"  {opvec} pf[{BKV // 16}];"]
+    # prologue: K(0), K(1), V(0) into LDS, S(0), then K(2) and V(1) into registers
+    L += ["  " + x for x in k_load("0u") + k_store(0)]
     if KB > 1:
-        L += load("1u")
+        L += ["  " + x for x in k_load("1u") + k_store(1)]
+    L += ["  " + x for x in v_load("0u") + v_store(0)]
     L.append("  __syncthreads();")
-    L.append(f"  for (int j = 0; j < {KB}; ++j) {{")
-    L.append("    const int buf = j & 1;")
-    # S^T = K Q^T over D in 16-wide chunks: tile t covers keys t*32 .. t*32+31
-    L += [f"    tj_f32x16 s[{BKV // 32}];",
-          "#pragma unroll",
-          f"    for (int t = 0; t < {BKV // 32}; ++t) s[t] = (tj_f32x16)(0.0f);",
-          "#pragma unroll",
-          f"    for (int c = 0; c < {D // 16}; ++c)",
-          "#pragma unroll",
-          f"      for (int t = 0; t < {BKV // 32}; ++t)",
-          f"        s[t] = {mfma}(*(const {opvec}*)&Ks[buf][t * 32 + col][c * 16 + g * 8u], qf[c], s[t], 0, 0, 0);"]
-    # online softmax, one query column per lane (its 32 keys here + lane ^ 32's 32)
-    L += ["    float mx = -__builtin_inff();",
-          "#pragma unroll",
-          f"    for (int t = 0; t < {BKV // 32}; ++t)",
-          "#pragma unroll",
-          "      for (int r = 0; r < 16; ++r) {",
-          f"        float x = s[t][r] * {cs!r}f;"]
-    if ragged:
-        L.append(f"        if (j * {BKV} + t * 32 + (r / 4) * 8 + (int)g * 4 + r % 4 >= {Sk}) x = -__builtin_inff();")
-    L += ["        s[t][r] = x;",
-          "        mx = fmaxf(mx, x);",
-          "      }",
-          "    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));",
-          "    const float m_new = fmaxf(m_run, mx);",
-          "    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);",
-          "    float rs = 0.0f;",
-          "#pragma unroll",
-          f"    for (int t = 0; t < {BKV // 32}; ++t)",
-          "#pragma unroll",
-          "      for (int r = 0; r < 16; ++r) {",
-          "        const float e = __builtin_amdgcn_exp2f(s[t][r] - m_new);",
-          "        s[t][r] = e;",
-          "        rs += e;",
-          "      }",
-          "    rs += __shfl_xor(rs, 32, 64);",
-          "    l_run = l_run * alpha + rs;",
-          "    m_run = m_new;",
-          "#pragma unroll",
-          f"    for (int u = 0; u < {Dv // 32}; ++u) o[u] *= alpha;"]
-    # O^T += V^T P^T: chunk ch = 2t + h holds keys t*32 + 16h .. +15 (in the permuted order)
-    L += ["#pragma unroll",
-          f"    for (int t = 0; t < {BKV // 32}; ++t)",
-          "#pragma unroll",
-          "      for (int h = 0; h < 2; ++h) {",
-          "        tj_u32x4 pw;",
-          "#pragma unroll",
-          "        for (int w = 0; w < 4; ++w) pw[w] = "
-          + ("tj_f2bf2(s[t][8 * h + 2 * w], s[t][8 * h + 2 * w + 1]);" if dt == DType.bf16 else
-             "tj_f2h(s[t][8 * h + 2 * w]) | (tj_f2h(s[t][8 * h + 2 * w + 1]) << 16);"),
-          f"        const {opvec} pf = __builtin_bit_cast({opvec}, pw);",
-          "#pragma unroll",
-          f"        for (int u = 0; u < {Dv // 32}; ++u)",
-          f"          o[u] = {mfma}(*(const {opvec}*)&Vs[buf][u * 32 + col][(2 * t + h) * 16 + g * 8u], pf, o[u], 0, 0, 0);",
-          "      }"]
-    L.append(f"    if (j + 1 < {KB}) {{")
-    L += ["    " + x for x in store("buf ^ 1")]
-    L.append("    }")
-    L.append(f"    if (j + 2 < {KB}) {{")
-    L += ["    " + x for x in load("(unsigned int)(j + 2)")]
-    L.append("    }")
-    L.append("    __syncthreads();")
-    L.append("  }")
+    L += ["  " + x for x in scores("sA", 0)]
+    L.append("  __syncthreads();   // every wave has read Ks[0] before K(2) replaces it")
+    if KB > 2:
+        L += ["  " + x for x in k_load("2u")]
+    if KB > 1:
+        L += ["  " + x for x in v_load("1u")]
+    # blocks 0 .. KB-4 have every step; run them in even/odd pairs, then peel the rest
+    npair = max(0, KB - 3) // 2
+    if npair:
+        L.append(f"  for (unsigned int j = 0; j < {2 * npair}u; j += 2u) {{")
+        L += ["    {"] + ["      " + x for x in iteration("j", None, 0, True, True, True, True, True)] + ["    }"]
+        L += ["    {"] + ["      " + x for x in iteration("j + 1u", None, 1, True, True, True, True, True)] + ["    }"]
+        L.append("  }")
+    for j in range(2 * npair, KB):
+        L.append(f"  {{  // block {j}")
+        L += ["    " + x for x in iteration(f"{j}u", j, j % 2, j + 1 < KB, j + 2 < KB, j + 1 < KB, j + 3 < KB,
+                                            j + 2 < KB)]
+        L.append("  }")
     # O = O^T / l: lane holds 4 consecutive dv per (u, r/4) for its query
     L += [f"  if (qrow < {Sq}u) {{",
           "    const float inv = 1.0f / l_run;",
@@ -334,7 +374,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
           "      }",
           "  }",
           "}"]
-    lds = 2 * (BKV * DP + Dv * VP) * dt.itemsize
+    lds = 2 * BKV * (DP + VP) * dt.itemsize
     flops = 2.0 * batch * Sq * Sk * (D + Dv)
     meta = {"family": "attention", "dtype": dt.value, "batch": batch, "Sq": Sq, "Sk": Sk, "D": D, "Dv": Dv,
             "scale": scale, "lds_bytes": lds, "flops": flops}

@@ -83,12 +83,14 @@ def test_config5_block_fuses_its_attention():
 
 
 @pytest.mark.parametrize("dtype", [DType.bf16, DType.f16])
-@pytest.mark.parametrize("shapes", [QKV, [(1, 100, 32), (1, 75, 32), (1, 75, 64)], [(2, 2, 256, 128)] * 3])
+@pytest.mark.parametrize("shapes", [QKV, [(1, 100, 32), (1, 75, 32), (1, 75, 64)], [(2, 2, 256, 128)] * 3,
+                                    [(1, 2, 600, 64), (1, 2, 1000, 64), (1, 2, 1000, 128)]])
 def test_flash_kernel_compiles_for_gfx950(shapes, dtype, tj_env):
     f = fuse_attention(lowered(attn, shapes, dtype))
     src, launches = hb.generate(f)
     (l,) = launches
-    assert "attention" in l.name and l.block == (256, 1, 1)
-    assert l.grid == (-(-shapes[0][-2] // 128), l.meta["batch"], 1)
+    waves = 8 if shapes[0][-1] % 64 == 0 and shapes[2][-1] % 64 == 0 and shapes[0][-2] >= 512 else 4
+    assert "attention" in l.name and l.block == (64 * waves, 1, 1)
+    assert l.grid == (-(-shapes[0][-2] // (32 * waves)), l.meta["batch"], 1)
     code = hb.compile_source(src, "gfx950")
     assert len(code) > 1000
