@@ -70,6 +70,13 @@ def _fn_gemm(x, w, b):
     return tj.gelu(tj.linear(x, w, b))
 
 
+def _fn_attn(q, k, v):
+    """Config 5's attention core: softmax(q k^T / sqrt(d)) v over [B, H, S, 128] heads."""
+    import tensorjit as tj
+
+    return tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * (1.0 / q.shape[-1] ** 0.5)), v)
+
+
 def _fn_mlp(x, g, w1, b1, w2, b2):
     import tensorjit as tj
 
@@ -297,14 +304,35 @@ def secondary(torch, dev, quick):
                             "kernels": len(cp.launches), "arena_MiB": round(cp.plan.arena_bytes / 2**20, 1),
                             "per_kernel": kernels}
     log(f"c5_block: {out['c5_block_bf16']}")
+    del bargs, f, cp
+    # config 5's attention alone: the fused flash kernel vs the reference plan's three
+    # kernels (scores, softmax row kernel, PV product) at the block's shape
+    qkv = [torch.randn(4, 32, 2048, 128, device=dev, generator=gen).to(bf) for _ in range(3)]
+    res = {}
+    for mode in ("1", "0"):
+        os.environ["TENSORJIT_HIP_ATTENTION"] = mode
+        f = tj.jit(_fn_attn)
+        f(*qkv)
+        cp = f.compiled(*qkv)
+        us = sum(cp.kernel_time_ms(i, *qkv, warmup=3, iters=10) for i in range(len(cp.launches))) * 1e3
+        res["fused_us" if mode == "1" else "unfused_us"] = round(us, 1)
+        if mode == "1":
+            res["kernel"] = cp.launches[0].name
+    os.environ.pop("TENSORJIT_HIP_ATTENTION", None)
+    flops = 4.0 * 4 * 32 * 2048 * 2048 * 128
+    res["TFLOP/s"] = round(flops / res["fused_us"] / 1e6, 1)
+    res["frac_peak"] = round(flops / res["fused_us"] / 1e6 / BF16_PEAK_TFLOPS, 4)
+    res["speedup_vs_unfused"] = round(res["unfused_us"] / res["fused_us"], 2)
+    out["c5_attention_bf16"] = res
+    log(f"c5_attention: {res}")
     return out
 
 
 def profile_set(torch, dev, steps) -> None:
     """Kernels for rocprofv3 counter runs: the headline kernel, a plain copy-like
     calibration kernel of known traffic (y = x + 0.5, fp32 [16384,4096]: 256 MiB
-    read + 256 MiB written), the row configs and the config-4 bf16 GEMM, ``steps``
-    launches each."""
+    read + 256 MiB written), the row configs, the config-4 bf16 GEMM and config 5's
+    fused attention, ``steps`` launches each."""
     import tensorjit as tj
 
     args = c2_inputs(torch, torch.float32, dev)
@@ -335,6 +363,11 @@ def profile_set(torch, dev, steps) -> None:
     jf = tj.jit(_fn_gemm)
     for _ in range(steps):
         jf(xg, wg, bg)
+    del xg, wg, bg
+    qkv = [torch.randn(4, 32, 2048, 128, device=dev, generator=gen).bfloat16() for _ in range(3)]
+    jf = tj.jit(_fn_attn)
+    for _ in range(steps):
+        jf(*qkv)
     torch.cuda.synchronize()
     log(f"profile set done ({steps} launches per kernel)")
 
