@@ -157,6 +157,21 @@ def fuse_attention(program: Program) -> Program:
 # ---------------------------------------------------------------------------
 
 
+XCDS = 8
+
+
+def _tile_lines(nq: int, batch: int, idx_t: str) -> list[str]:
+    """Workgroup -> (batch*head ``bh``, query tile ``qt``).  Workgroups are dealt to the
+    8 XCDs round-robin; in groups of 8 heads the ``nq`` query tiles of one head share
+    ``blockIdx.x % 8``, so they run on one XCD and its L2 serves the head's K and V once
+    instead of once per XCD."""
+    if nq > 1 and batch % XCDS == 0:
+        return [f"  const unsigned int grp = blockIdx.x / {XCDS * nq}u, rem = blockIdx.x % {XCDS * nq}u;",
+                f"  const {idx_t} bh = grp * {XCDS}u + rem % {XCDS}u;",
+                f"  const unsigned int qt = rem / {XCDS}u;"]
+    return [f"  const {idx_t} bh = blockIdx.x / {nq}u;", f"  const unsigned int qt = blockIdx.x % {nq}u;"]
+
+
 def attention_waves(Sq: int, D: int, Dv: int) -> int:
     """Waves per workgroup (32 query rows each).  Eight share every K/V block that
     passes through LDS between twice as many queries (half the L2->CU traffic of
@@ -208,12 +223,12 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
          f"  __shared__ __attribute__((aligned(16))) {T} Vs[2][{BKV}][{VP}];",
          "  const unsigned int tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;",
          "  const unsigned int g = lane / 32u, col = lane % 32u;",
-         f"  const {idx_t} bh = blockIdx.y;",
+         *_tile_lines(-(-Sq // (BQ_PER_WAVE * NW)), batch, idx_t),
          f"  const {T}* __restrict__ Qb = in0_p + bh * {Sq * D}u;",
          f"  const {T}* __restrict__ Kb = in1_p + bh * {Sk * D}u;",
          f"  const {T}* __restrict__ Vb = in2_p + bh * {Sk * Dv}u;",
          f"  {T}* __restrict__ Ob = out0_p + bh * {Sq * Dv}u;",
-         f"  const unsigned int qrow = blockIdx.x * {BQ}u + wave * 32u + col;",
+         f"  const unsigned int qrow = qt * {BQ}u + wave * 32u + col;",
          f"  const unsigned int qc = qrow < {Sq}u ? qrow : {Sq - 1}u;",
          # Q as the B operand of S^T = K Q^T: chunk c holds Q[q][c*16 + g*8 .. +8]
          f"  {opvec} qf[{D // 16}];",
@@ -378,4 +393,4 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     flops = 2.0 * batch * Sq * Sk * (D + Dv)
     meta = {"family": "attention", "dtype": dt.value, "batch": batch, "Sq": Sq, "Sk": Sk, "D": D, "Dv": Dv,
             "scale": scale, "lds_bytes": lds, "flops": flops}
-    return "\n".join(L), Launch(fname, (-(-Sq // BQ), batch, 1), (THREADS, 1, 1), 0, meta)
+    return "\n".join(L), Launch(fname, (-(-Sq // BQ) * batch, 1, 1), (THREADS, 1, 1), 0, meta)
