@@ -231,7 +231,9 @@ def autotune(
     whose build or run raises are skipped.
     """
     store = store or AutotuneStore()
-    rank = lambda c: cost_model(c, *shape, backend)  # noqa: E731
+    M, N, K = shape[:3]
+    batch = shape[3] if len(shape) > 3 else 1
+    rank = lambda c: cost_model(c, M, N, K, backend, batch)  # noqa: E731
     if os.environ.get("TENSORJIT_NO_AUTOTUNE") == "1":
         return min(candidates, key=rank)
     cached = store.get(key)

@@ -42,3 +42,25 @@ def test_every_packaged_config_is_legal_for_its_dtype(key):
     cfg = MatmulConfig.from_dict(entry["config"])
     assert hip_gemm.config_ok(cfg, DType(key.split("|")[4])), (key, cfg)
     assert entry["ms"] > 0
+
+
+def test_autotune_times_the_cost_models_best_candidates(tmp_path):
+    """The candidates that get timed are the top-k of the hip cost model for the
+    (M, N, K, batch) shape, and the fastest measured one is stored."""
+    from tensorjit.runtime.autotune import HIP_F32_CANDIDATES, autotune, cost_model
+
+    shape = (512, 768, 3072, 1)
+    timed = []
+
+    def build(cfg):
+        return cfg
+
+    def timer(cfg, warmup, iters):
+        timed.append(cfg)
+        return 1.0 + 0.01 * len(timed) if cfg.TM == 64 and cfg.TN == 64 else 5.0
+
+    store = cache.AutotuneStore(tmp_path / "autotune.json")
+    best = autotune("k", HIP_F32_CANDIDATES, build, shape, "hip_f32", top_k=3, store=store, timer=timer)
+    expect = sorted(HIP_F32_CANDIDATES, key=lambda c: cost_model(c, 512, 768, 3072, "hip_f32", 1))[:3]
+    assert set(timed) == set(expect)
+    assert store.get("k")["config"] == best.as_dict()
