@@ -115,6 +115,9 @@ HIP_F32_CANDIDATES: list[MatmulConfig] = [
     MatmulConfig(64, 64, 32, 4, 2, 2, 16),
     MatmulConfig(64, 64, 16, 4, 2, 2, 16),
     MatmulConfig(32, 32, 32, 4, 2, 2, 16),
+    MatmulConfig(32, 64, 32, 4, 2, 2, 16),
+    MatmulConfig(64, 32, 32, 4, 2, 2, 16),
+    MatmulConfig(32, 32, 64, 4, 2, 2, 16),
 ]
 
 
