@@ -120,9 +120,10 @@ FUNCTION_MAP: dict[object, Callable] = {
     torch.minimum: T.minimum,
     torch.where: T.where,
     torch.clamp_min: T.maximum,
-    F.relu: T.relu,
-    F.gelu: lambda x, approximate="none": T.gelu(x),
-    F.silu: T.silu,
+    # FX records the defaulted ``inplace`` flag of the activations; it has no meaning here
+    F.relu: lambda x, inplace=False: T.relu(x),
+    F.gelu: lambda x, approximate="none": T.gelu(x) if approximate == "none" else _unsupported("gelu(tanh)"),
+    F.silu: lambda x, inplace=False: T.silu(x),
     F.sigmoid: T.sigmoid,
     F.tanh: T.tanh,
     F.softmax: _softmax,
