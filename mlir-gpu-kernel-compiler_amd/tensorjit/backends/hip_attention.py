@@ -172,11 +172,16 @@ def _tile_lines(nq: int, batch: int, idx_t: str) -> list[str]:
     return [f"  const {idx_t} bh = blockIdx.x / {nq}u;", f"  const unsigned int qt = blockIdx.x % {nq}u;"]
 
 
-def attention_waves(Sq: int, D: int, Dv: int) -> int:
-    """Waves per workgroup (32 query rows each).  Eight share every K/V block that
-    passes through LDS between twice as many queries (half the L2->CU traffic of
-    four) when the shapes divide evenly and there are enough query rows."""
-    return 8 if D % 64 == 0 and Dv % 64 == 0 and Sq >= 512 else 4
+def attention_layout(Sq: int, D: int, Dv: int) -> tuple[int, int]:
+    """(waves per workgroup, 32-row query tiles per wave).  Long sequences: 8 waves in
+    two ping-pong groups sharing every K/V block between 256 queries (half the L2->CU
+    traffic of 4 waves), while on each SIMD one group's softmax arithmetic runs under
+    the other group's MFMAs.  Two query tiles per wave would halve the LDS fragment
+    reads per FLOP, but its accumulators do not fit beside the softmax operands in the
+    256 VGPRs the rescale arithmetic needs (the compiler spills)."""
+    if D % 64 == 0 and Dv % 64 == 0 and Sq >= 512:
+        return 8, 1
+    return 4, 1
 
 
 def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
@@ -190,9 +195,13 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     batch = math.prod(q.shape[:-2]) if len(q.shape) > 2 else 1
     Sq, D = q.shape[-2:]
     Sk, Dv = kk.shape[-2], v.shape[-1]
-    NW = attention_waves(Sq, D, Dv)
+    NW, QT = attention_layout(Sq, D, Dv)
+    assert QT == 1, "one query tile per wave"
     THREADS = NW * 64
-    BQ = BQ_PER_WAVE * NW
+    # 8 waves: two groups of 4 a phase apart (ping-pong) over 3 LDS stages
+    pingpong = NW == 8
+    NST = 3 if pingpong else 2
+    BQ = BQ_PER_WAVE * QT * NW
     KB = -(-Sk // BKV)
     DP = D + 8                                  # 16-byte row padding: conflict-free fragment reads
     # V rows: a transposing read touches 8 rows x 64 bytes; a pitch of 32 or 96 (mod 128)
@@ -214,31 +223,40 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         pack4 = ("(unsigned long)(tj_f2h({0}) | (tj_f2h({1}) << 16)) | "
                  "((unsigned long)(tj_f2h({2}) | (tj_f2h({3}) << 16)) << 32)")
 
-    # two waves per SIMD (two workgroups per CU): one wave's softmax arithmetic runs
-    # under the other's MFMAs; the compiler then keeps everything in 256 VGPRs
-    L = [f'extern "C" __global__ void __launch_bounds__({THREADS}) __attribute__((amdgpu_waves_per_eu(2, 2))) {fname}(',
+    # two waves per SIMD: one wave's softmax arithmetic runs under the other's MFMAs;
+    # the compiler then keeps everything in 256 VGPRs
+    occ = 2
+    L = [f'extern "C" __global__ void __launch_bounds__({THREADS}) __attribute__((amdgpu_waves_per_eu({occ}, {occ}))) {fname}(',
          f"    const {T}* __restrict__ in0_p, const {T}* __restrict__ in1_p, const {T}* __restrict__ in2_p,",
          f"    {T}* __restrict__ out0_p) {{",
-         f"  __shared__ __attribute__((aligned(16))) {T} Ks[2][{BKV}][{DP}];",
-         f"  __shared__ __attribute__((aligned(16))) {T} Vs[2][{BKV}][{VP}];",
+         f"  __shared__ __attribute__((aligned(16))) {T} Ks[{NST}][{BKV}][{DP}];",
+         f"  __shared__ __attribute__((aligned(16))) {T} Vs[{NST}][{BKV}][{VP}];",
          "  const unsigned int tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;",
          "  const unsigned int g = lane / 32u, col = lane % 32u;",
-         *_tile_lines(-(-Sq // (BQ_PER_WAVE * NW)), batch, idx_t),
+         *_tile_lines(-(-Sq // BQ), batch, idx_t),
          f"  const {T}* __restrict__ Qb = in0_p + bh * {Sq * D}u;",
          f"  const {T}* __restrict__ Kb = in1_p + bh * {Sk * D}u;",
          f"  const {T}* __restrict__ Vb = in2_p + bh * {Sk * Dv}u;",
          f"  {T}* __restrict__ Ob = out0_p + bh * {Sq * Dv}u;",
-         f"  const unsigned int qrow = qt * {BQ}u + wave * 32u + col;",
-         f"  const unsigned int qc = qrow < {Sq}u ? qrow : {Sq - 1}u;",
-         # Q as the B operand of S^T = K Q^T: chunk c holds Q[q][c*16 + g*8 .. +8]
-         f"  {opvec} qf[{D // 16}];",
+         # query tile q of this wave: rows qrow0 + q*32 .. +31, one per lane column
+         f"  const unsigned int qrow0 = qt * {BQ}u + wave * {32 * QT}u + col;",
+         # Q as the B operand of S^T = K Q^T: chunk c holds Q[row][c*16 + g*8 .. +8]
+         f"  {opvec} qf[{QT}][{D // 16}];",
+         f"  tj_f32x16 o[{QT}][{Dv // 32}];",
+         f"  float m_run[{QT}], l_run[{QT}];",
          "#pragma unroll",
-         f"  for (int c = 0; c < {D // 16}; ++c) qf[c] = *(const {opvec}*)&Qb[qc * {D}u + c * 16 + g * 8u];",
-         f"  tj_f32x16 o[{Dv // 32}];",
+         f"  for (int q = 0; q < {QT}; ++q) {{",
+         f"    const unsigned int qc = qrow0 + q * 32u < {Sq}u ? qrow0 + q * 32u : {Sq - 1}u;",
          "#pragma unroll",
-         f"  for (int u = 0; u < {Dv // 32}; ++u) o[u] = (tj_f32x16)(0.0f);",
-         "  float m_run = -__builtin_inff(), l_run = 0.0f;",
+         f"    for (int c = 0; c < {D // 16}; ++c) qf[q][c] = *(const {opvec}*)&Qb[qc * {D}u + c * 16 + g * 8u];",
+         "#pragma unroll",
+         f"    for (int u = 0; u < {Dv // 32}; ++u) o[q][u] = (tj_f32x16)(0.0f);",
+         "    m_run[q] = -__builtin_inff();",
+         "    l_run[q] = 0.0f;",
+         "  }",
          f"  tj_u32x4 rk[{KC}], rv[{VC}];"]
+    if pingpong:
+        L.append("  const unsigned int gq = wave / 4u, gtid = tid % 256u;")
 
     def k_load(blk: str) -> list[str]:
         out_l = ["#pragma unroll", f"for (int i = 0; i < {KC}; ++i) {{",
@@ -256,6 +274,26 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
             out_l.append(f"  key = key < {Sk}u ? key : {Sk - 1}u;")
         return out_l + [f"  rv[i] = *(const tj_u32x4*)&Vb[key * {Dv}u + d8];", "}"]
 
+    def half_load(which: str, blk: str) -> list[str]:
+        """This group's half (keys gq*32 .. +31) of a K or V block into rk / rv; the block
+        index is clamped so the loads past the last block stay in bounds (unused)."""
+        d, reg, base = (D, "rk", "Kb") if which == "k" else (Dv, "rv", "Vb")
+        n = (BKV // 2) * d // 8 // 256
+        out_l = ["#pragma unroll", f"for (int i = 0; i < {n}; ++i) {{",
+                 f"  const unsigned int c = i * 256u + gtid, row = gq * {BKV // 2}u + c / {d // 8}u, d8 = (c % {d // 8}u) * 8u;",
+                 f"  const unsigned int b_ = ({blk}) < {KB}u ? ({blk}) : {KB - 1}u;",
+                 f"  unsigned int key = b_ * {BKV}u + row;"]
+        if ragged:
+            out_l.append(f"  key = key < {Sk}u ? key : {Sk - 1}u;")
+        return out_l + [f"  {reg}[i] = *(const tj_u32x4*)&{base}[key * {d}u + d8];", "}"]
+
+    def half_store(which: str, stage: str) -> list[str]:
+        d, reg, arr = (D, "rk", "Ks") if which == "k" else (Dv, "rv", "Vs")
+        n = (BKV // 2) * d // 8 // 256
+        return ["#pragma unroll", f"for (int i = 0; i < {n}; ++i) {{",
+                f"  const unsigned int c = i * 256u + gtid, row = gq * {BKV // 2}u + c / {d // 8}u, d8 = (c % {d // 8}u) * 8u;",
+                f"  *(tj_u32x4*)&{arr}[{stage}][row][d8] = {reg}[i];", "}"]
+
     def k_store(stage: int) -> list[str]:
         return ["#pragma unroll", f"for (int i = 0; i < {KC}; ++i) {{",
                 f"  const unsigned int c = i * {THREADS}u + tid, row = c / {D // 8}u, d8 = (c % {D // 8}u) * 8u;",
@@ -268,10 +306,14 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
 
     def scores(dst: str, stage: int) -> list[str]:
         """S^T = K Q^T over D in 16-wide chunks: tile t covers keys t*32 .. t*32+31."""
-        return ["#pragma unroll", f"for (int t = 0; t < {BKV // 32}; ++t) {dst}[t] = (tj_f32x16)(0.0f);",
-                "#pragma unroll", f"for (int c = 0; c < {D // 16}; ++c)", "#pragma unroll",
-                f"  for (int t = 0; t < {BKV // 32}; ++t)",
-                f"    {dst}[t] = {mfma}(*(const {opvec}*)&Ks[{stage}][t * 32 + col][c * 16 + g * 8u], qf[c], {dst}[t], 0, 0, 0);"]
+        return ["#pragma unroll", f"for (int q = 0; q < {QT}; ++q)", "#pragma unroll",
+                f"  for (int t = 0; t < {BKV // 32}; ++t) {dst}[q][t] = (tj_f32x16)(0.0f);",
+                "#pragma unroll", f"for (int c = 0; c < {D // 16}; ++c) {{", "#pragma unroll",
+                f"  for (int t = 0; t < {BKV // 32}; ++t) {{",
+                f"    const {opvec} kf = *(const {opvec}*)&Ks[{stage}][t * 32 + col][c * 16 + g * 8u];",
+                "#pragma unroll",
+                f"    for (int q = 0; q < {QT}; ++q) {dst}[q][t] = {mfma}(kf, qf[q][c], {dst}[q][t], 0, 0, 0);",
+                "  }", "}"]
 
     # online softmax, one query column per lane (its 32 keys here + lane ^ 32's 32).
     # The extreme is taken on the raw scores (max(s*cs) = cs*max(s) for cs > 0, min for
@@ -282,36 +324,51 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         ("fminf", "__builtin_inff()", "__builtin_inff()")
 
     def block_max(sc: str, j: int | None) -> list[str]:
-        out_l = [f"float mx = {ext_init};", "#pragma unroll", f"for (int t = 0; t < {BKV // 32}; ++t)",
-                 "#pragma unroll", "  for (int r = 0; r < 16; ++r) {"]
+        mask = None
         if ragged and j == KB - 1:
-            out_l.append(f"    if ({j * BKV} + t * 32 + (r / 4) * 8 + (int)g * 4 + r % 4 >= {Sk}) {sc}[t][r] = {masked};")
-        out_l += [f"    mx = {ext}(mx, {sc}[t][r]);", "  }",
-                  f"mx = {ext}(mx, __shfl_xor(mx, 32, 64));",
-                  f"const float mb = mx * {cs!r}f;",
-                  "if (__builtin_amdgcn_ballot_w64(mb > m_run + 8.0f)) {",
-                  "  const float m_new = fmaxf(m_run, mb);",
-                  "  const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);",
-                  "  l_run *= alpha;",
+            mask = f"{j * BKV}"
+        elif ragged and j is None and pingpong:
+            mask = "(int)jj"
+            mask = f"{mask} * {BKV}"
+        out_l = [f"float mb[{QT}];", "bool grow = false;", "#pragma unroll", f"for (int q = 0; q < {QT}; ++q) {{",
+                 f"  float mx = {ext_init};", "#pragma unroll", f"  for (int t = 0; t < {BKV // 32}; ++t)",
+                 "#pragma unroll", "    for (int r = 0; r < 16; ++r) {"]
+        if mask is not None:
+            out_l.append(f"      if ({mask} + t * 32 + (r / 4) * 8 + (int)g * 4 + r % 4 >= {Sk}) {sc}[q][t][r] = {masked};")
+        out_l += [f"      mx = {ext}(mx, {sc}[q][t][r]);", "    }",
+                  f"  mx = {ext}(mx, __shfl_xor(mx, 32, 64));",
+                  f"  mb[q] = mx * {cs!r}f;",
+                  "  grow = grow || mb[q] > m_run[q] + 8.0f;",
+                  "}",
+                  "if (__builtin_amdgcn_ballot_w64(grow)) {",
                   "#pragma unroll",
-                  f"  for (int u = 0; u < {Dv // 32}; ++u) o[u] *= alpha;",
-                  "  m_run = m_new;",
+                  f"  for (int q = 0; q < {QT}; ++q) {{",
+                  "    const float m_new = fmaxf(m_run[q], mb[q]);",
+                  "    const float alpha = __builtin_amdgcn_exp2f(m_run[q] - m_new);",
+                  "    l_run[q] *= alpha;",
+                  "#pragma unroll",
+                  f"    for (int u = 0; u < {Dv // 32}; ++u) o[q][u] *= alpha;",
+                  "    m_run[q] = m_new;",
+                  "  }",
                   "}"]
         return out_l
 
     def probs(sc: str) -> list[str]:
-        """exp2 of the block's scores, their sum, and the P^T operands (chunk 2t+h)."""
+        """exp2 of the block's scores, the running sums, and the P^T operands (chunk 2t+h)."""
         cvt = ("tj_f2bf2({0}, {1})" if dt == DType.bf16 else "tj_f2h({0}) | (tj_f2h({1}) << 16)")
-        return ["float rs = 0.0f;", "#pragma unroll", f"for (int t = 0; t < {BKV // 32}; ++t)",
-                "#pragma unroll", "  for (int h = 0; h < 2; ++h) {",
-                "    tj_u32x4 pw;", "#pragma unroll", "    for (int w = 0; w < 4; ++w) {",
-                f"      const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[t][8 * h + 2 * w], {cs!r}f, -m_run));",
-                f"      const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[t][8 * h + 2 * w + 1], {cs!r}f, -m_run));",
-                "      rs += e0 + e1;",
-                "      pw[w] = " + cvt.format("e0", "e1") + ";",
+        return ["#pragma unroll", f"for (int q = 0; q < {QT}; ++q) {{",
+                "  float rs = 0.0f;", "#pragma unroll", f"  for (int t = 0; t < {BKV // 32}; ++t)",
+                "#pragma unroll", "    for (int h = 0; h < 2; ++h) {",
+                "      tj_u32x4 pw;", "#pragma unroll", "      for (int w = 0; w < 4; ++w) {",
+                f"        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[q][t][8 * h + 2 * w], {cs!r}f, -m_run[q]));",
+                f"        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[q][t][8 * h + 2 * w + 1], {cs!r}f, -m_run[q]));",
+                "        rs += e0 + e1;",
+                "        pw[w] = " + cvt.format("e0", "e1") + ";",
+                "      }",
+                f"      pf[q][2 * t + h] = __builtin_bit_cast({opvec}, pw);",
                 "    }",
-                f"    pf[2 * t + h] = __builtin_bit_cast({opvec}, pw);",
-                "  }"]
+                "  l_run[q] += rs + __shfl_xor(rs, 32, 64);",
+                "}"]
 
     def pv(stage: int) -> list[str]:
         """O^T += V^T P^T.  The V^T fragment of chunk ch holds keys ch*16 + g*4 + 0..3 then
@@ -323,8 +380,9 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 "    const unsigned int vcol = u * 32 + ((lane / 16u) % 2u) * 16u + (lane % 4u) * 4u;",
                 f"    tj_i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)&Vs[{stage}][vrow][vcol]);",
                 f"    tj_i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)&Vs[{stage}][vrow + 8u][vcol]);",
-                "    tj_i16x8 vv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);",
-                f"    o[u] = {mfma}(__builtin_bit_cast({opvec}, vv), pf[ch], o[u], 0, 0, 0);",
+                f"    const {opvec} vv = __builtin_bit_cast({opvec}, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));",
+                "#pragma unroll",
+                f"    for (int q = 0; q < {QT}; ++q) o[q][u] = {mfma}(vv, pf[q][ch], o[q][u], 0, 0, 0);",
                 "  }", "}"]
 
     def iteration(j: str, jc: int | None, par: int, has_next: bool, store_k: bool, store_v: bool,
@@ -337,7 +395,6 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         if has_next:
             out_l += scores(sn, 1 - par)
         out_l += probs(sc)
-        out_l += ["l_run += rs + __shfl_xor(rs, 32, 64);"]
         out_l += pv(par)
         if store_k:
             out_l += k_store(par)
@@ -350,47 +407,107 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         out_l.append("__syncthreads();")
         return out_l
 
-    L += [f"  tj_f32x16 sA[{BKV // 32}], sB[{BKV // 32}];", f"  {opvec} pf[{BKV // 16}];"]
-    # prologue: K(0), K(1), V(0) into LDS, S(0), then K(2) and V(1) into registers
-    L += ["  " + x for x in k_load("0u") + k_store(0)]
-    if KB > 1:
-        L += ["  " + x for x in k_load("1u") + k_store(1)]
-    L += ["  " + x for x in v_load("0u") + v_store(0)]
-    L.append("  __syncthreads();")
-    L += ["  " + x for x in scores("sA", 0)]
-    L.append("  __syncthreads();   // every wave has read Ks[0] before K(2) replaces it")
-    if KB > 2:
-        L += ["  " + x for x in k_load("2u")]
-    if KB > 1:
-        L += ["  " + x for x in v_load("1u")]
-    # blocks 0 .. KB-4 have every step; run them in even/odd pairs, then peel the rest
-    npair = max(0, KB - 3) // 2
-    if npair:
-        L.append(f"  for (unsigned int j = 0; j < {2 * npair}u; j += 2u) {{")
-        L += ["    {"] + ["      " + x for x in iteration("j", None, 0, True, True, True, True, True)] + ["    }"]
-        L += ["    {"] + ["      " + x for x in iteration("j + 1u", None, 1, True, True, True, True, True)] + ["    }"]
-        L.append("  }")
-    for j in range(2 * npair, KB):
-        L.append(f"  {{  // block {j}")
-        L += ["    " + x for x in iteration(f"{j}u", j, j % 2, j + 1 < KB, j + 2 < KB, j + 1 < KB, j + 3 < KB,
-                                            j + 2 < KB)]
-        L.append("  }")
-    # O = O^T / l: lane holds 4 consecutive dv per (u, r/4) for its query
-    L += [f"  if (qrow < {Sq}u) {{",
-          "    const float inv = 1.0f / l_run;",
-          "#pragma unroll",
-          f"    for (int u = 0; u < {Dv // 32}; ++u)",
-          "#pragma unroll",
-          "      for (int r4 = 0; r4 < 4; ++r4) {",
-          "        const unsigned int dv = u * 32 + r4 * 8 + g * 4u;",
-          "        *(unsigned long*)&Ob[qrow * " + f"{Dv}u + dv] = "
-          + pack4.format("o[u][r4 * 4] * inv", "o[u][r4 * 4 + 1] * inv", "o[u][r4 * 4 + 2] * inv",
-                         "o[u][r4 * 4 + 3] * inv") + ";",
-          "      }",
-          "  }",
-          "}"]
-    lds = 2 * BKV * (DP + VP) * dt.itemsize
+    def double_buffer_body() -> list[str]:
+        """All waves in step; one barrier per block (2 LDS stages)."""
+        out = []
+        # prologue: K(0), K(1), V(0) into LDS, S(0), then K(2) and V(1) into registers
+        out += ["  " + x for x in k_load("0u") + k_store(0)]
+        if KB > 1:
+            out += ["  " + x for x in k_load("1u") + k_store(1)]
+        out += ["  " + x for x in v_load("0u") + v_store(0)]
+        out.append("  __syncthreads();")
+        out += ["  " + x for x in scores("sA", 0)]
+        out.append("  __syncthreads();   // every wave has read Ks[0] before K(2) replaces it")
+        if KB > 2:
+            out += ["  " + x for x in k_load("2u")]
+        if KB > 1:
+            out += ["  " + x for x in v_load("1u")]
+        # blocks 0 .. KB-4 have every step; run them in even/odd pairs, then peel the rest
+        npair = max(0, KB - 3) // 2
+        if npair:
+            out.append(f"  for (unsigned int j = 0; j < {2 * npair}u; j += 2u) {{")
+            out += ["    {"] + ["      " + x for x in iteration("j", None, 0, True, True, True, True, True)] + ["    }"]
+            out += ["    {"] + ["      " + x for x in iteration("j + 1u", None, 1, True, True, True, True, True)] + ["    }"]
+            out.append("  }")
+        for j in range(2 * npair, KB):
+            out.append(f"  {{  // block {j}")
+            out += ["    " + x for x in iteration(f"{j}u", j, j % 2, j + 1 < KB, j + 2 < KB, j + 1 < KB, j + 3 < KB,
+                                                  j + 2 < KB)]
+            out.append("  }")
+        return out
+
+    def pp_iteration(jj: str, par: int) -> list[str]:
+        """One block for one wave group, as two phases separated by workgroup barriers.
+        Phase A: softmax of S(j) with the MFMAs of S(j+1) (K(j+1) in stage (j+1)%3).
+        Phase B: O += P(j) V(j) (stage j%3); this group's halves of K(j+3) and V(j+1) go
+        to LDS, the loads of K(j+4) and V(j+2) are issued.  The other group runs the
+        opposite phase meanwhile.  With group 1 one phase behind, a K block is written
+        (phases 2j+1 and 2j+2) two phases before its first read (2j+4) and a V block
+        (same phases) one phase before (2j+3); the stages they overwrite were last read
+        in phase 2j-1 (K) and 2j-2 (V)."""
+        sc, sn = ("sA", "sB") if par == 0 else ("sB", "sA")
+        out = block_max(sc, None)
+        # S(j+1) unconditionally: past the last block it reads a stale stage, unused
+        out += scores(sn, f"(({jj}) + 1u) % 3u")
+        out += probs(sc)
+        out += ["__syncthreads();"]
+        out += pv(f"({jj}) % 3u")
+        # stores past the last block write stages no later block reads; loads are clamped
+        out += half_store("k", f"({jj}) % 3u") + half_store("v", f"(({jj}) + 1u) % 3u")
+        out += half_load("k", f"({jj}) + 4u") + half_load("v", f"({jj}) + 2u")
+        out.append("__syncthreads();")
+        return out
+
+    def pingpong_body() -> list[str]:
+        out = []
+        # prologue (all waves): K(0..2), V(0) into LDS, S(0); then this group's halves
+        # of K(3) and V(1) into registers; group 1 waits one extra barrier
+        for b in range(min(3, KB)):
+            out += ["  " + x for x in k_load(f"{b}u") + k_store(b)]
+        out += ["  " + x for x in v_load("0u") + v_store(0)]
+        out.append("  __syncthreads();")
+        out += ["  " + x for x in scores("sA", 0)]
+        out += ["  " + x for x in half_load("k", "3u") + half_load("v", "1u")]
+        out.append("  if (gq == 1u) __syncthreads();")
+        npair = KB // 2
+        if npair:
+            out.append(f"  for (unsigned int jj = 0; jj < {2 * npair}u; jj += 2u) {{")
+            out += ["    {"] + ["      " + x for x in pp_iteration("jj", 0)] + ["    }"]
+            out += ["    {"] + ["      const unsigned int jj1 = jj + 1u;"] + \
+                   ["      " + x.replace("(int)jj *", "(int)jj1 *") for x in pp_iteration("jj1", 1)] + ["    }"]
+            out.append("  }")
+        if KB % 2:
+            out.append(f"  {{  const unsigned int jj = {KB - 1}u;")
+            out += ["    " + x for x in pp_iteration("jj", (KB - 1) % 2)]
+            out.append("  }")
+        out.append("  if (gq == 0u) __syncthreads();")
+        return out
+
+    def epilogue_lines() -> list[str]:
+        # O = O^T / l: lane holds 4 consecutive dv per (u, r/4) for its query
+        return ["#pragma unroll", f"  for (int q = 0; q < {QT}; ++q) {{",
+                "    const unsigned int qrow = qrow0 + q * 32u;",
+                f"    if (qrow < {Sq}u) {{",
+                "      const float inv = 1.0f / l_run[q];",
+                "#pragma unroll",
+                f"      for (int u = 0; u < {Dv // 32}; ++u)",
+                "#pragma unroll",
+                "        for (int r4 = 0; r4 < 4; ++r4) {",
+                "          const unsigned int dv = u * 32 + r4 * 8 + g * 4u;",
+                "          *(unsigned long*)&Ob[qrow * " + f"{Dv}u + dv] = "
+                + pack4.format("o[q][u][r4 * 4] * inv", "o[q][u][r4 * 4 + 1] * inv", "o[q][u][r4 * 4 + 2] * inv",
+                               "o[q][u][r4 * 4 + 3] * inv") + ";",
+                "        }",
+                "    }",
+                "  }",
+                "}"]
+
+    L += [f"  tj_f32x16 sA[{QT}][{BKV // 32}], sB[{QT}][{BKV // 32}];", f"  {opvec} pf[{QT}][{BKV // 16}];"]
+    L += pingpong_body() if pingpong else double_buffer_body()
+    L += epilogue_lines()
+    lds = NST * BKV * (DP + VP) * dt.itemsize
     flops = 2.0 * batch * Sq * Sk * (D + Dv)
     meta = {"family": "attention", "dtype": dt.value, "batch": batch, "Sq": Sq, "Sk": Sk, "D": D, "Dv": Dv,
-            "scale": scale, "lds_bytes": lds, "flops": flops}
+            "scale": scale, "lds_bytes": lds, "flops": flops,
+            "schedule": "pingpong" if pingpong else "double-buffer"}
     return "\n".join(L), Launch(fname, (-(-Sq // BQ) * batch, 1, 1), (THREADS, 1, 1), 0, meta)

@@ -89,8 +89,10 @@ def test_flash_kernel_compiles_for_gfx950(shapes, dtype, tj_env):
     f = fuse_attention(lowered(attn, shapes, dtype))
     src, launches = hb.generate(f)
     (l,) = launches
-    waves = 8 if shapes[0][-1] % 64 == 0 and shapes[2][-1] % 64 == 0 and shapes[0][-2] >= 512 else 4
+    from tensorjit.backends.hip_attention import attention_layout
+
+    waves, tiles = attention_layout(shapes[0][-2], shapes[0][-1], shapes[2][-1])
     assert "attention" in l.name and l.block == (64 * waves, 1, 1)
-    assert l.grid == (-(-shapes[0][-2] // (32 * waves)) * l.meta["batch"], 1, 1)
+    assert l.grid == (-(-shapes[0][-2] // (32 * waves * tiles)) * l.meta["batch"], 1, 1)
     code = hb.compile_source(src, "gfx950")
     assert len(code) > 1000
