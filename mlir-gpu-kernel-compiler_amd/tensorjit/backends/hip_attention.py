@@ -126,6 +126,34 @@ def match_attention(program: Program, i3: int) -> dict | None:
             "nodes": k1.nodes + k2.nodes + k3.nodes}
 
 
+def _bshd_source(program: Program, t: Node, users_ok: set[int], outs: set[int]) -> tuple[int, Node] | None:
+    """If ``t`` is a copy kernel's ``transpose(perm=(0,2,1,3))`` of a contiguous
+    [B, S, H, D] value used only inside the fused chain, return (kernel index, source):
+    the attention kernel can read the source through strides instead."""
+    if t.op != "transpose" or tuple(t.attrs.get("perm", ())) != (0, 2, 1, 3) or len(t.shape) != 4:
+        return None
+    if id(t) in outs or not all(id(u) in users_ok for u in t.users):
+        return None
+    for i, k in enumerate(program.kernels):
+        if k.kind == "copy" and k.nodes == [t] and k.outputs == [t]:
+            return i, t.inputs[0]
+    return None
+
+
+def _bshd_sink(program: Program, o: Node, outs: set[int]) -> tuple[int, Node] | None:
+    """If the attention output's only user is a copy kernel's transpose back to
+    [B, S, H, D], return (kernel index, that transpose): the kernel writes it directly."""
+    if id(o) in outs or len(o.users) != 1:
+        return None
+    t = o.users[0]
+    if t.op != "transpose" or tuple(t.attrs.get("perm", ())) != (0, 2, 1, 3) or len(t.shape) != 4:
+        return None
+    for i, k in enumerate(program.kernels):
+        if k.kind == "copy" and k.nodes == [t] and k.outputs == [t] and k.inputs == [o]:
+            return i, t
+    return None
+
+
 def fuse_attention(program: Program) -> Program:
     """Replace every fusable attention chain by one ``attention`` kernel at the PV
     product's position (its inputs are live there; the scores and probabilities
@@ -141,14 +169,37 @@ def fuse_attention(program: Program) -> Program:
         if m is None:
             i3 += 1
             continue
-        fused = Kernel("attention", nodes=m["nodes"], anchor=m["out"], inputs=[m["q"], m["k"], m["v"]],
-                       outputs=list(kernels[i3].outputs))
-        fused.attn = {"scale": m["scale"]}  # type: ignore[attr-defined]
+        # head transposes on either side: read q/k/v from, and write o to, [B, S, H, D]
+        outs = {id(cur.resolve(o)) for o in program.graph.outputs}
+        fused_ids = {id(n) for n in m["nodes"]}
+        drop = [m["i1"], m["i2"]]
+        ins, layouts, nodes, seen = [], [], list(m["nodes"]), {}
+        for x in (m["q"], m["k"], m["v"]):
+            src = seen.get(id(x)) or _bshd_source(cur, x, fused_ids, outs)
+            if src is not None:
+                seen[id(x)] = src
+                if src[0] not in drop:
+                    drop.append(src[0])
+                    nodes.insert(0, x)
+                ins.append(src[1])
+                layouts.append("bshd")
+            else:
+                ins.append(x)
+                layouts.append("bhsd")
+        out, out_layout = m["out"], "bhsd"
+        sink = _bshd_sink(cur, m["out"], outs)
+        if sink is not None:
+            drop.append(sink[0])
+            out, out_layout = sink[1], "bshd"
+            nodes.append(sink[1])
+        fused = Kernel("attention", nodes=nodes, anchor=m["out"], inputs=ins, outputs=[out])
+        fused.attn = {"scale": m["scale"], "layouts": layouts, "out_layout": out_layout}  # type: ignore[attr-defined]
         kernels[i3] = fused
-        for i in sorted((m["i1"], m["i2"]), reverse=True):
+        for i in sorted(drop, reverse=True):
             del kernels[i]
-        i3 -= 2
+        i3 = kernels.index(fused) + 1
         changed = True
+        continue
     return Program(program.graph, kernels, program.aliases) if changed else program
 
 
@@ -190,11 +241,32 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     q, kk, v = k.inputs
     out = k.outputs[0]
     scale = k.attn["scale"]  # type: ignore[attr-defined]
+    layouts = k.attn.get("layouts", ["bhsd"] * 3)  # type: ignore[attr-defined]
+    out_layout = k.attn.get("out_layout", "bhsd")  # type: ignore[attr-defined]
+
+    def logical(n: Node, layout: str) -> tuple[tuple, int, int]:
+        """(batch dims, rows, row length) of an operand as [.., rows, d]."""
+        if layout == "bshd":
+            B, S_, H, d = n.shape
+            return (B, H), S_, d
+        return tuple(n.shape[:-2]), n.shape[-2], n.shape[-1]
+
+    qb_dims, Sq, D = logical(q, layouts[0])
+    _, Sk, _ = logical(kk, layouts[1])
+    _, _, Dv = logical(v, layouts[2])
     dt = q.dtype
     T = CTYPE[dt]
-    batch = math.prod(q.shape[:-2]) if len(q.shape) > 2 else 1
-    Sq, D = q.shape[-2:]
-    Sk, Dv = kk.shape[-2], v.shape[-1]
+    batch = math.prod(qb_dims) if qb_dims else 1
+
+    def base_stride(layout: str, rows: int, d: int, n: Node) -> tuple[str, int]:
+        """Offset of (batch*head ``bh``)'s [rows, d] matrix and its row stride."""
+        if layout == "bshd":
+            H = n.shape[2]
+            return f"(bh / {H}u) * {rows * H * d}u + (bh % {H}u) * {d}u", H * d
+        return f"bh * {rows * d}u", d
+
+    (qoff, qst), (koff, kst) = base_stride(layouts[0], Sq, D, q), base_stride(layouts[1], Sk, D, kk)
+    (voff, vst), (ooff, ost) = base_stride(layouts[2], Sk, Dv, v), base_stride(out_layout, Sq, Dv, out)
     NW, QT = attention_layout(Sq, D, Dv)
     assert QT == 1, "one query tile per wave"
     THREADS = NW * 64
@@ -213,8 +285,9 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     VC = BKV * Dv // 8 // THREADS
     assert KC * THREADS * 8 == BKV * D and VC * THREADS * 8 == BKV * Dv
     idx_t = "unsigned long" if batch * max(Sq, Sk) * max(D, Dv) >= 2**31 else "unsigned int"
+    assert batch * max(Sq, Sk) * max(D, Dv) < 2**32, "32-bit element offsets"
     ragged = Sk % BKV != 0
-    bdims = "x".join(str(d) for d in q.shape[:-2]) or "1"
+    bdims = "x".join(str(d) for d in qb_dims) or "1"
     fname = f"tj{idx}_attention_{bdims}x{Sq}x{Sk}x{D}_{dt.value}_flash"
     cs = scale * 1.4426950408889634            # scores scaled into exp2's domain
     if dt == DType.bf16:
@@ -234,10 +307,10 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
          "  const unsigned int tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;",
          "  const unsigned int g = lane / 32u, col = lane % 32u;",
          *_tile_lines(-(-Sq // BQ), batch, idx_t),
-         f"  const {T}* __restrict__ Qb = in0_p + bh * {Sq * D}u;",
-         f"  const {T}* __restrict__ Kb = in1_p + bh * {Sk * D}u;",
-         f"  const {T}* __restrict__ Vb = in2_p + bh * {Sk * Dv}u;",
-         f"  {T}* __restrict__ Ob = out0_p + bh * {Sq * Dv}u;",
+         f"  const {T}* __restrict__ Qb = in0_p + ({qoff});",
+         f"  const {T}* __restrict__ Kb = in1_p + ({koff});",
+         f"  const {T}* __restrict__ Vb = in2_p + ({voff});",
+         f"  {T}* __restrict__ Ob = out0_p + ({ooff});",
          # query tile q of this wave: rows qrow0 + q*32 .. +31, one per lane column
          f"  const unsigned int qrow0 = qt * {BQ}u + wave * {32 * QT}u + col;",
          # Q as the B operand of S^T = K Q^T: chunk c holds Q[row][c*16 + g*8 .. +8]
@@ -248,7 +321,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
          f"  for (int q = 0; q < {QT}; ++q) {{",
          f"    const unsigned int qc = qrow0 + q * 32u < {Sq}u ? qrow0 + q * 32u : {Sq - 1}u;",
          "#pragma unroll",
-         f"    for (int c = 0; c < {D // 16}; ++c) qf[q][c] = *(const {opvec}*)&Qb[qc * {D}u + c * 16 + g * 8u];",
+         f"    for (int c = 0; c < {D // 16}; ++c) qf[q][c] = *(const {opvec}*)&Qb[qc * {qst}u + c * 16 + g * 8u];",
          "#pragma unroll",
          f"    for (int u = 0; u < {Dv // 32}; ++u) o[q][u] = (tj_f32x16)(0.0f);",
          "    m_run[q] = -__builtin_inff();",
@@ -264,7 +337,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                  f"  unsigned int key = ({blk}) * {BKV}u + row;"]
         if ragged:
             out_l.append(f"  key = key < {Sk}u ? key : {Sk - 1}u;")
-        return out_l + [f"  rk[i] = *(const tj_u32x4*)&Kb[key * {D}u + d8];", "}"]
+        return out_l + [f"  rk[i] = *(const tj_u32x4*)&Kb[key * {kst}u + d8];", "}"]
 
     def v_load(blk: str) -> list[str]:
         out_l = ["#pragma unroll", f"for (int i = 0; i < {VC}; ++i) {{",
@@ -272,12 +345,12 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                  f"  unsigned int key = ({blk}) * {BKV}u + row;"]
         if ragged:
             out_l.append(f"  key = key < {Sk}u ? key : {Sk - 1}u;")
-        return out_l + [f"  rv[i] = *(const tj_u32x4*)&Vb[key * {Dv}u + d8];", "}"]
+        return out_l + [f"  rv[i] = *(const tj_u32x4*)&Vb[key * {vst}u + d8];", "}"]
 
     def half_load(which: str, blk: str) -> list[str]:
         """This group's half (keys gq*32 .. +31) of a K or V block into rk / rv; the block
         index is clamped so the loads past the last block stay in bounds (unused)."""
-        d, reg, base = (D, "rk", "Kb") if which == "k" else (Dv, "rv", "Vb")
+        d, reg, base, st = (D, "rk", "Kb", kst) if which == "k" else (Dv, "rv", "Vb", vst)
         n = (BKV // 2) * d // 8 // 256
         out_l = ["#pragma unroll", f"for (int i = 0; i < {n}; ++i) {{",
                  f"  const unsigned int c = i * 256u + gtid, row = gq * {BKV // 2}u + c / {d // 8}u, d8 = (c % {d // 8}u) * 8u;",
@@ -285,7 +358,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                  f"  unsigned int key = b_ * {BKV}u + row;"]
         if ragged:
             out_l.append(f"  key = key < {Sk}u ? key : {Sk - 1}u;")
-        return out_l + [f"  {reg}[i] = *(const tj_u32x4*)&{base}[key * {d}u + d8];", "}"]
+        return out_l + [f"  {reg}[i] = *(const tj_u32x4*)&{base}[key * {st}u + d8];", "}"]
 
     def half_store(which: str, stage: str) -> list[str]:
         d, reg, arr = (D, "rk", "Ks") if which == "k" else (Dv, "rv", "Vs")
@@ -494,7 +567,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 "#pragma unroll",
                 "        for (int r4 = 0; r4 < 4; ++r4) {",
                 "          const unsigned int dv = u * 32 + r4 * 8 + g * 4u;",
-                "          *(unsigned long*)&Ob[qrow * " + f"{Dv}u + dv] = "
+                "          *(unsigned long*)&Ob[qrow * " + f"{ost}u + dv] = "
                 + pack4.format("o[q][u][r4 * 4] * inv", "o[q][u][r4 * 4 + 1] * inv", "o[q][u][r4 * 4 + 2] * inv",
                                "o[q][u][r4 * 4 + 3] * inv") + ";",
                 "        }",

@@ -77,7 +77,12 @@ def test_config5_block_fuses_its_attention():
     p = lowered(bench._fn_block, shapes)
     assert len(p.kernels) == 16
     f = fuse_attention(p)
-    assert len(f.kernels) == 14 and [k.kind for k in f.kernels].count("attention") == 1
+    # the attention chain and the four head transposes around it are one kernel
+    assert len(f.kernels) == 10 and [k.kind for k in f.kernels].count("attention") == 1
+    (att,) = [k for k in f.kernels if k.kind == "attention"]
+    assert att.attn["layouts"] == ["bshd"] * 3 and att.attn["out_layout"] == "bshd"
+    assert [i.shape for i in att.inputs] == [(4, 2048, 32, 128)] * 3 and att.outputs[0].shape == (4, 2048, 32, 128)
+    assert all(k.kind != "copy" for k in f.kernels)
     # the 1 GiB score and probability buffers are gone from the arena (2.25 GiB -> 428 MiB)
     assert plan_memory(f).arena_bytes < plan_memory(p).arena_bytes - 1.5 * 2**30
 
@@ -96,3 +101,36 @@ def test_flash_kernel_compiles_for_gfx950(shapes, dtype, tj_env):
     assert l.grid == (-(-shapes[0][-2] // (32 * waves * tiles)) * l.meta["batch"], 1, 1)
     code = hb.compile_source(src, "gfx950")
     assert len(code) > 1000
+
+
+def mha(x, wq, wk, wv, heads=2):
+    B, S, Dm = x.shape
+    d = Dm // heads
+    q = tj.linear(x, wq).reshape(B, S, heads, d).transpose(1, 2)
+    k = tj.linear(x, wk).reshape(B, S, heads, d).transpose(1, 2)
+    v = tj.linear(x, wv).reshape(B, S, heads, d).transpose(1, 2)
+    o = tj.matmul(tj.softmax(tj.matmul(q, k.transpose(-1, -2)) * (1.0 / d ** 0.5)), v)
+    return o.transpose(1, 2).reshape(B, S, Dm)
+
+
+def test_head_transposes_are_folded_into_strided_attention(tj_env):
+    p = lowered(mha, [(2, 200, 128), (128, 128), (128, 128), (128, 128)])
+    assert [k.kind for k in p.kernels].count("copy") == 4
+    f = fuse_attention(p)
+    assert [k.kind for k in f.kernels] == ["matmul", "matmul", "matmul", "attention"]
+    src, launches = hb.generate(f)
+    assert "(bh / 2u) * 25600u + (bh % 2u) * 64u" in src       # [B, S, H, D] addressing
+    hb.compile_source(src, "gfx950")
+
+
+def test_transpose_with_another_user_is_not_folded():
+    def fn(x, wq, wk, wv):
+        B, S, Dm = x.shape
+        q = tj.linear(x, wq).reshape(B, S, 2, 64).transpose(1, 2)
+        k = tj.linear(x, wk).reshape(B, S, 2, 64).transpose(1, 2)
+        v = tj.linear(x, wv).reshape(B, S, 2, 64).transpose(1, 2)
+        o = tj.matmul(tj.softmax(tj.matmul(q, k.transpose(-1, -2)) * 0.125), v)
+        return o, q * 2.0
+    f = fuse_attention(lowered(fn, [(2, 200, 128), (128, 128), (128, 128), (128, 128)]))
+    (att,) = [k for k in f.kernels if k.kind == "attention"]
+    assert att.attn["layouts"] == ["bhsd", "bshd", "bshd"] and att.attn["out_layout"] == "bhsd"

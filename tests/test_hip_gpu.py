@@ -266,6 +266,32 @@ def test_fused_attention_vs_oracle_and_unfused_plan(shapes, dt, monkeypatch):
     close_lowp(out, out3, tol=2e-2)
 
 
+def _mha(x, wq, wk, wv, heads):
+    B, S, Dm = x.shape
+    d = Dm // heads
+    q = tj.linear(x, wq).reshape(B, S, heads, d).transpose(1, 2)
+    k = tj.linear(x, wk).reshape(B, S, heads, d).transpose(1, 2)
+    v = tj.linear(x, wv).reshape(B, S, heads, d).transpose(1, 2)
+    o = tj.matmul(tj.softmax(tj.matmul(q, k.transpose(-1, -2)) * (1.0 / d ** 0.5)), v)
+    return o.transpose(1, 2).reshape(B, S, Dm)
+
+
+@pytest.mark.parametrize("B,S,Dm,heads", [(2, 200, 128, 2), (1, 600, 256, 4)], ids=["4_waves", "pingpong"])
+def test_fused_attention_reads_and_writes_head_interleaved_layout(B, S, Dm, heads):
+    """Multi-head attention with the head transposes folded into the flash kernel's
+    strided loads and stores (no copy kernels), against the fp32 oracle."""
+    torch.manual_seed(0)
+    x = torch.randn(B, S, Dm, device=DEV).bfloat16()
+    ws = [(torch.randn(Dm, Dm, device=DEV) / Dm ** 0.5).bfloat16() for _ in range(3)]
+    fn = lambda x, a, b, c: _mha(x, a, b, c, heads)  # noqa: E731
+    f = tj.jit(fn)
+    out = f(x, *ws)
+    cp = f.compiled(x, *ws)
+    assert [l.meta["family"] for l in cp.launches].count("attention") == 1 and cp.num_kernels == 4
+    (ref,) = oracle.run(fn, *[t.float().cpu() for t in (x, *ws)])
+    close_lowp(out, ref, tol=2e-2)
+
+
 def test_fused_attention_large_logits_and_unit_scale():
     """Scores of magnitude ~100 (online max subtraction must keep exp2 in range) and
     no scale multiply in the chain."""
