@@ -529,6 +529,27 @@ def test_config4_gemm_full_size_bf16_rows_vs_oracle():
     close_lowp(out, ref, tol=2e-2)
 
 
+def test_config5_block_with_fused_attention_vs_oracle():
+    """Config 5's layer at head dim 64 (so the attention chain and its head transposes
+    fuse into one flash kernel: 10 kernels), bf16 vs the fp32 oracle of the reference
+    plan, and hipGraph replays equal to eager launches."""
+    import bench
+
+    torch.manual_seed(0)
+    args = bench.block_inputs(torch, torch.device(DEV), B=1, S=256, D=2048, F=512)
+    f = tj.jit(bench._fn_block)
+    out = f(*args)
+    cp = f.compiled(*args)
+    assert cp.num_kernels == 10 and any("attention" in l.name for l in cp.launches)
+    (ref,) = oracle.run(bench._fn_block, *[a.float().cpu() for a in args])
+    close_lowp(out, ref, tol=3e-2)
+    eager = cp(*args)[0].clone()
+    cp.use_graph = True
+    for _ in range(3):
+        assert torch.equal(cp(*args)[0], eager)
+    cp.use_graph = False
+
+
 def test_config5_transformer_block_small_bf16_vs_oracle():
     """Config 5's layer (RMSNorm, q/k/v, attention with materialised scores, out-proj +
     residual, RMSNorm, gelu MLP + residual) at a small shape, bf16 vs the fp32 oracle."""
