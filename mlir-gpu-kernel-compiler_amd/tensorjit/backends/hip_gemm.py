@@ -80,6 +80,22 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
         return ok
     if cfg.INTERLEAVE and (cfg.PINGPONG or (cfg.TK // ki) % 2):
         return False
+    if cfg.DIRECT:
+        # direct-to-LDS tiles: 16-bit operands, 128-byte K rows (TK 64), 32x32 MFMAs
+        # with 128-row wave tiles (the LDS swizzle assumes row bases that are
+        # multiples of 32), 8-row DMA blocks per wave and no other schedule
+        ok = (dt in (DType.bf16, DType.f16) and cfg.TK == 64 and cfg.MI == 32 and not cfg.PINGPONG
+              and not cfg.INTERLEAVE and cfg.SPLIT_K == 1 and cfg.WM * cfg.WN == cfg.num_warps
+              and cfg.TM % (cfg.WM * 32) == 0 and cfg.TN % (cfg.WN * 32) == 0
+              and cfg.TM % (8 * cfg.num_warps) == 0 and cfg.TN % (8 * cfg.num_warps) == 0
+              and 2 * (cfg.TM + cfg.TN) * 128 <= 160 * 1024)
+        if ok and mm is not None:
+            M, N, K, tb = matmul_dims(mm)
+            a, b = mm.inputs
+            # buffer descriptors: byte offsets (rows padded to the tile) and ranges in int32
+            ok = (tb and K % 64 == 0 and a.dtype == b.dtype == dt
+                  and (M + cfg.TM) * K * 2 < 2**31 and (N + cfg.TN) * K * 2 < 2**31)
+        return ok
     if cfg.PINGPONG:
         ks = cfg.TK // ki
         if cfg.num_warps % 2 or cfg.PINGPONG > 3 or (cfg.PINGPONG == 3 and ks % 2):
@@ -386,9 +402,10 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {fname}({g.params()}) {{']
     a_bytes = 2 * BM * LDK * esz
     lds_bytes = a_bytes + 2 * BN * LDK * esz
-    L.append(f"  __shared__ __attribute__((aligned(16))) char tj_lds[{lds_bytes}];")
-    L.append(f"  {lds_t} (*As)[{BM}][{LDK}] = ({lds_t} (*)[{BM}][{LDK}])tj_lds;")
-    L.append(f"  {lds_t} (*Bs)[{BN}][{LDK}] = ({lds_t} (*)[{BN}][{LDK}])(tj_lds + {a_bytes});")
+    if not cfg.DIRECT:
+        L.append(f"  __shared__ __attribute__((aligned(16))) char tj_lds[{lds_bytes}];")
+        L.append(f"  {lds_t} (*As)[{BM}][{LDK}] = ({lds_t} (*)[{BM}][{LDK}])tj_lds;")
+        L.append(f"  {lds_t} (*Bs)[{BN}][{LDK}] = ({lds_t} (*)[{BN}][{LDK}])(tj_lds + {a_bytes});")
     L.append("  const unsigned int tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;")
     L.append(f"  const unsigned int wm = wave / {WN}u, wn = wave % {WN}u;")
     ntm, ntn = -(-M // BM), -(-N // BN)
@@ -420,6 +437,12 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         bidx = []
         L.append(f"  const {CTYPE[a.dtype]}* __restrict__ Ab = {A}_p;")
         L.append(f"  const {CTYPE[b.dtype]}* __restrict__ Bb = {B}_p;")
+
+    if cfg.DIRECT:
+        L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, guard_m, guard_n, idx_t,
+                               CTYPE[a.dtype], CTYPE[b.dtype])
+        return _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW,
+                              TNW, NACC, THREADS, 0, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
 
     # ---- global -> register staging ------------------------------------------------
     def plan_k_major(rows: int, vec: bool):
@@ -832,6 +855,186 @@ def interleaved_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, lo
     for kt in range(2 * npair, KT):
         L.append(f"  {{  // K tile {kt}")
         L += tile(str(kt), kt % 2, kt + 1 < KT, kt + 2 < KT, kt + 1 < KT, "    ")
+        L.append("  }")
+    return L
+
+
+# direct-to-LDS load split: (loads of tile kt+2 issued in tile kt's region B, region-A
+# sub-steps of tile kt+1 over which the rest are spread)
+DIRECT_SPLIT = (8, 1)
+
+
+def _vmcnt_only(n: int) -> str:
+    """s_waitcnt immediate for gfx9 that waits until at most ``n`` vector-memory
+    operations are outstanding (vmcnt split over bits 3:0 and 15:14; expcnt and
+    lgkmcnt at their maxima, i.e. not waited on)."""
+    assert 0 <= n < 64
+    return hex((n & 15) | ((n >> 4) << 14) | 0x0F70)
+
+
+def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, guard_m, guard_n, idx_t,
+                      a_ct, b_ct) -> list[str]:
+    """Main loop for one wave per SIMD with tiles loaded straight into LDS (``DIRECT``).
+
+    ``global_load_lds_dwordx4`` moves 16 bytes per lane from HBM/L2 into LDS without
+    passing through registers: no staging VGPRs and no LDS store instructions, so the
+    wave's issue slots go to its MFMAs and fragment reads.  One instruction writes
+    1 KiB of LDS contiguously (lane i at byte 16 i), i.e. eight 128-byte K rows of a
+    64-deep tile.  Rows are not padded; instead the 16-byte chunk ``c`` of tile row
+    ``r`` is stored at position ``c ^ f(r)`` with ``f(r) = (r & 7) ^ ((r >> 3) & 3)``,
+    applied by choosing which chunk each lane fetches (the 8 lanes of a row still
+    cover one whole 128-byte line).  Sixteen lanes of an MFMA fragment read (16
+    consecutive rows, one chunk) then land on 16 distinct 16-byte bank groups.
+
+    Two LDS stages, each operand and stage its own ``__shared__`` array so the
+    compiler can tell the stage being filled from the stage being read and does not
+    wait for the loads in flight before each fragment read.  Tile kt (stage kt & 1):
+    region A issues the loads of tile kt+1 into the other stage, then runs the MFMAs
+    of sub-steps 0 .. KS-2 with the fragment reads of the next sub-steps threaded
+    between them; a barrier (which waits for this wave's loads) publishes tile kt+1;
+    region B runs the last sub-step's MFMAs with the reads of tile kt+1's first
+    fragments."""
+    nw = cfg.num_warps
+    KS = 4                                  # 64-deep tile, 16 per 32x32x16 MFMA
+    # Barrier that publishes a stage filled by DMA: each wave first waits for its own
+    # DMA loads (vmcnt 0; expcnt and lgkmcnt left at their maxima).  A workgroup-scope
+    # fence does not cover loads that write LDS, and the compiler's own vmcnt wait is
+    # placed after the barrier (it only orders this wave's reads), so without this
+    # wait another wave can read a block whose DMA is still landing.
+    publish = ["__builtin_amdgcn_s_waitcnt(0x0F70);", "__syncthreads();"]
+    a_cnt, b_cnt = BM // (8 * nw), BN // (8 * nw)
+    nmm = TMW * TNW
+    L = [f"  __shared__ __attribute__((aligned(1024))) char As0[{BM * 128}];",
+         f"  __shared__ __attribute__((aligned(1024))) char As1[{BM * 128}];",
+         f"  __shared__ __attribute__((aligned(1024))) char Bs0[{BN * 128}];",
+         f"  __shared__ __attribute__((aligned(1024))) char Bs1[{BN * 128}];",
+         "  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave);",
+         "  const unsigned int drow = lane >> 3;",
+         f"  {'tj_f32x16'} acc[{TMW}][{TNW}];",
+         "#pragma unroll",
+         f"  for (int x = 0; x < {TMW}; ++x)",
+         "#pragma unroll",
+         f"    for (int y = 0; y < {TNW}; ++y) acc[x][y] = (tj_f32x16)(0.0f);",
+         # fragment addresses: row (wave base + lane % 32), logical chunk 2 ks + lane / 32
+         "  const unsigned int fr = lane & 31u, fh = lane >> 5;",
+         "  const unsigned int fsw = (fr & 7u) ^ ((fr >> 3) & 3u);",
+         f"  const unsigned int arow = (wm * {BM // cfg.WM}u + fr) * 128u;",
+         f"  const unsigned int brow = (wn * {BN // cfg.WN}u + fr) * 128u;",
+         "  unsigned int fofs[4];",
+         "#pragma unroll",
+         "  for (int ks = 0; ks < 4; ++ks) fofs[ks] = ((2u * ks + fh) ^ fsw) * 16u;"]
+
+    # Loads go through buffer resources (buffer_load_dwordx4 ... lds): a 32-bit lane
+    # offset that does not change over K (row and swizzled chunk), the tile's K position
+    # in a scalar offset, and the descriptor's range check, which returns zeros for rows
+    # past M or N (no clamping).  The global_load_lds form would also work, but the
+    # compiler treats it as a flat access that may touch LDS and then waits for every
+    # outstanding LDS read (lgkmcnt 0) wherever one fragment is needed.
+    L.append(f"  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, {M * K * 2}, 0x00020000);")
+    L.append(f"  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, {N * K * 2}, 0x00020000);")
+    for op, cnt, rows in (("A", a_cnt, "m0"), ("B", b_cnt, "n0")):
+        L.append(f"  unsigned int vo{op}[{cnt}];")
+        for i in range(cnt):
+            q = f"({i * nw}u + wv)"
+            L.append(f"  vo{op}[{i}] = (({rows} + {q} * 8u + drow) * {K}u + ((lane & 7u) ^ drow ^ ({q} & 3u)) * 8u) * 2u;")
+
+    def dma(kt: str, stage: int) -> list[list[str]]:
+        """The DMA loads of tile ``kt`` into ``stage``, one statement block per load."""
+        blocks = []
+        for op, cnt in (("A", a_cnt), ("B", b_cnt)):
+            for i in range(cnt):
+                q = f"({i * nw}u + wv)"
+                blocks.append([f"__builtin_amdgcn_raw_ptr_buffer_load_lds(rs{op}, (__attribute__((address_space(3))) void*)"
+                               f"({op}s{stage} + {q} * 1024u), 16, vo{op}[{i}], (int)(({kt}) * 128u), 0, 0);"])
+        return blocks
+
+    def frag_reads(buf: int, stage: int, ks: int) -> list[str]:
+        """Fragment reads in the order the MFMAs consume them (row-major over (x, y):
+        fa[0], fb[0..], fa[1], ...), so each MFMA waits only for its own operands."""
+        a_rd = [f"fa[{buf}][{x}] = *(const {opvec}*)(As{stage} + arow + fofs[{ks}] + {x * 32 * 128}u);"
+                for x in range(TMW)]
+        b_rd = [f"fb[{buf}][{y}] = *(const {opvec}*)(Bs{stage} + brow + fofs[{ks}] + {y * 32 * 128}u);"
+                for y in range(TNW)]
+        return [a_rd[0]] + b_rd + a_rd[1:]
+
+    def mfmas(buf: int) -> list[str]:
+        return [f"acc[{x}][{y}] = {builtin}(fa[{buf}][{x}], fb[{buf}][{y}], acc[{x}][{y}], 0, 0, 0);"
+                for x in range(TMW) for y in range(TNW)]
+
+    def pattern(n_mfma: int, mem: list[int]) -> list[str]:
+        out = []
+        per = -(-len(mem) // max(n_mfma, 1)) if mem else 0
+        for i in range(n_mfma):
+            out.append(f"__builtin_amdgcn_sched_group_barrier({SG_MFMA}, 1, 0);")
+            for m in mem[i * per:(i + 1) * per]:
+                out.append(f"__builtin_amdgcn_sched_group_barrier({m}, 1, 0);")
+        return out
+
+    n_batch = a_cnt + b_cnt
+    n_b = min(DIRECT_SPLIT[0], n_batch)          # loads issued in region B
+    a_steps = max(1, min(DIRECT_SPLIT[1], KS - 1))  # region-A sub-steps taking the rest
+
+    def tile(kt: str, stage: int, carry: bool, do_load: bool, last: bool, ind: str) -> list[str]:
+        """Tile kt from LDS stage ``stage``.  The loads of tile kt+2 (into this stage,
+        released by this tile's barrier) start in region B; ``carry``: the rest of tile
+        kt+1's loads (begun in the previous tile's region B) go into region A here,
+        still ahead of the barrier that publishes tile kt+1.  Splitting a tile's loads
+        over both regions keeps the texture unit (about 16 cycles per 1 KiB load, four
+        waves per CU) from backing up into MFMA issue.  ``last``: no tile follows."""
+        out = []
+        rest = dma(f"({kt}) + 1", 1 - stage)[n_b:] if carry else []
+        # region A: sub-steps 0 .. KS-2 with the fragment reads of the next sub-steps
+        for ks in range(KS - 1):
+            mine = rest[len(rest) * ks // a_steps:len(rest) * (ks + 1) // a_steps] if ks < a_steps else []
+            for blk in mine:
+                out += blk
+            out += mfmas(ks % 2)
+            out += frag_reads((ks + 1) % 2, stage, ks + 1)
+            out += pattern(nmm, [SG_DS_READ] * (TMW + TNW) + [SG_VMEM_READ] * len(mine))
+            out.append("__builtin_amdgcn_sched_barrier(0);")
+        if not last:
+            out += publish + ["__builtin_amdgcn_sched_barrier(0);"]
+        # region B: last sub-step, with the first fragments of tile kt+1 and the first
+        # loads of tile kt+2
+        out += mfmas((KS - 1) % 2)
+        mem = []
+        if not last:
+            out += frag_reads(0, 1 - stage, 0)
+            mem += [SG_DS_READ] * (TMW + TNW)
+        if do_load:
+            blocks = dma(f"({kt}) + 2", stage)[:n_b]
+            for blk in blocks:
+                out += blk
+            mem += [SG_VMEM_READ] * len(blocks)
+        out += pattern(nmm, mem)
+        out.append("__builtin_amdgcn_sched_barrier(0);")
+        return [ind + x for x in out]
+
+    # prologue: tiles 0 and 1 in flight, wait for tile 0 only (the 2nd batch may
+    # stay outstanding: vmcnt <= its load count)
+    L += ["  " + x for blk in dma("0", 0) for x in blk]
+    if KT > 1:
+        L += ["  " + x for blk in dma("1", 1) for x in blk]
+        L.append(f"  __builtin_amdgcn_s_waitcnt({_vmcnt_only(n_batch)});")
+        L.append("  __syncthreads();")
+    else:
+        L += ["  " + x for x in publish]
+    L.append(f"  {opvec} fa[2][{TMW}], fb[2][{TNW}];")
+    L += ["  " + x for x in frag_reads(0, 0, 0)]
+    # tile 0 (nothing to carry: the prologue loaded tile 1 whole), then (odd, even)
+    # pairs of tiles that all carry and load, then the tail
+    L.append("  {  // K tile 0")
+    L += tile("0", 0, False, 2 < KT, KT == 1, "    ")
+    L.append("  }")
+    npair = max(0, KT - 3) // 2
+    if npair:
+        L.append(f"  for (unsigned int kt = 1; kt < {1 + 2 * npair}u; kt += 2) {{")
+        L += tile("kt", 1, True, True, False, "    ")
+        L += tile("kt + 1u", 0, True, True, False, "    ")
+        L.append("  }")
+    for kt in range(1 + 2 * npair, KT):
+        L.append(f"  {{  // K tile {kt}")
+        L += tile(str(kt), kt % 2, kt + 1 < KT, kt + 2 < KT, kt + 1 == KT, "    ")
         L.append("  }")
     return L
 

@@ -59,21 +59,24 @@ class MatmulConfig:
     GROUP_M: int = 8        # tile rows per group of the XCD-aware tile order (0 = plain row-major order)
     PINGPONG: int = 0       # two wave groups alternate MFMA and memory phases: 1/2 = loads 2/3 K steps ahead, 3 = K-split tiles
     INTERLEAVE: int = 0     # 1: one wave per SIMD, memory instructions threaded between its MFMAs
+    DIRECT: int = 0         # 1: one wave per SIMD, tiles loaded straight into LDS (global_load_lds_dwordx4)
 
     def as_dict(self) -> dict:
         return {"TM": self.TM, "TN": self.TN, "TK": self.TK, "num_warps": self.num_warps,
                 "WM": self.WM, "WN": self.WN, "MI": self.MI, "SPLIT_K": self.SPLIT_K, "GROUP_M": self.GROUP_M,
-                "PINGPONG": self.PINGPONG, "INTERLEAVE": self.INTERLEAVE}
+                "PINGPONG": self.PINGPONG, "INTERLEAVE": self.INTERLEAVE, "DIRECT": self.DIRECT}
 
     @staticmethod
     def from_dict(d: dict) -> "MatmulConfig":
         return MatmulConfig(d["TM"], d["TN"], d.get("TK", 0), d.get("num_warps", 4), d.get("WM", 2),
                             d.get("WN", 2), d.get("MI", 32), d.get("SPLIT_K", 1), d.get("GROUP_M", 8),
-                            d.get("PINGPONG", 0), d.get("INTERLEAVE", 0))
+                            d.get("PINGPONG", 0), d.get("INTERLEAVE", 0), d.get("DIRECT", 0))
 
 
 # bf16 / fp16 candidates (MFMA 32x32x16 or 16x16x32)
 HIP_CANDIDATES: list[MatmulConfig] = [
+    MatmulConfig(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
+    MatmulConfig(256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
     MatmulConfig(256, 256, 64, 8, 2, 4, 32, 1, 8, 3),
     MatmulConfig(256, 256, 64, 8, 4, 2, 32, 1, 8, 3),
     MatmulConfig(256, 256, 32, 8, 2, 4, 32, 1, 8, 2),
@@ -134,7 +137,10 @@ def _skinny_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: in
 
 def _sched_factor(cfg: MatmulConfig) -> float:
     """Relative MFMA-phase cost of a loop schedule, from bf16 8192^3 runs on MI355X
-    (ping-pong with K-split tiles fastest; plain double-buffered loop ~9% slower)."""
+    (direct-to-LDS loads 3-7% ahead of ping-pong with K-split tiles; plain
+    double-buffered loop ~9% behind it)."""
+    if cfg.DIRECT:
+        return 0.95
     if cfg.INTERLEAVE:
         return 1.15
     return {3: 1.0, 2: 1.04, 1: 1.05}.get(cfg.PINGPONG, 1.09)
@@ -153,7 +159,7 @@ def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) 
         return math.inf
     acc = tm * tn / (64 * waves) * (cfg.SPLIT_K if cfg.SPLIT_K > 1 else 1)
     frags = 2 * (tm / cfg.WM + tn / cfg.WN) / cfg.MI * (4 if elem == 2 else 1)  # double-buffered
-    staging = (tm + tn) * tk * elem / (64 * waves * 4)  # staged K step per lane, 4 B per VGPR
+    staging = 0 if cfg.DIRECT else (tm + tn) * tk * elem / (64 * waves * 4)  # staged K step per lane, 4 B per VGPR
     regs = acc + frags + staging + 32
     if regs > 512:
         return math.inf
