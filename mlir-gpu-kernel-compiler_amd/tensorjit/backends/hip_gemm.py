@@ -252,6 +252,48 @@ def _batch_strides(t: Node, batch_shape: tuple) -> tuple[int, ...]:
     return tuple(st)
 
 
+def _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, ve, cs) -> list[str]:
+    """Epilogue of one run of ``ve`` consecutive outputs at (i, j) (both defined by the
+    caller), the accumulators being ``cs`` with ``q`` the position in the run: extra
+    inputs loaded as vectors where contiguous, outputs stored as vectors."""
+    L = []
+    full_idx = list(bidx) + ["i", "j"]
+    L.append(f"    float acc_v[{ve}];")
+    L.append("#pragma unroll")
+    L.append(f"    for (int q = 0; q < {ve}; ++q) acc_v[q] = {cs};")
+    local = {id(mm): "acc_v[q]"}
+    for n in epi_inputs:
+        consumer = next((c for c in epilogue if n in c.inputs), epilogue[0] if epilogue else mm)
+        st = access_strides(n, consumer, out_shape)
+        terms = [v if s_ == 1 else f"{v} * {s_}u" for v, s_ in zip(full_idx, st) if s_]
+        off = " + ".join(terms) if terms else "0u"
+        nm = g.names[id(n)]
+        L.append(f"    float {nm}_v[{ve}];")
+        inner = st[-1]
+        if ve > 1 and inner == 1 and 16 // n.dtype.itemsize == ve:
+            L.append(f"    tj_ldv({nm}_p + ({off}), {nm}_v);")
+        elif inner == 0:
+            L.append(f"    {{ const float s_ = tj_ld({nm}_p[{off}]); for (int q = 0; q < {ve}; ++q) {nm}_v[q] = s_; }}")
+        else:
+            L.append(f"    for (int q = 0; q < {ve}; ++q) {nm}_v[q] = tj_ld({nm}_p[({off}) + q * {inner}u]);")
+        local[id(n)] = f"{nm}_v[q]"
+    for jj in range(len(k.outputs)):
+        L.append(f"    float o{jj}_v[{ve}];")
+    L.append("#pragma unroll")
+    L.append(f"    for (int q = 0; q < {ve}; ++q) {{")
+    for n in epilogue:
+        L.append(f"      const float {g.names[id(n)]} = {emit_expr(n, local)};")
+        local[id(n)] = g.names[id(n)]
+    for jj, o in enumerate(k.outputs):
+        L.append(f"      o{jj}_v[q] = {local[id(o)]};")
+    L.append("    }")
+    obase = f"bi * {M * N}u + " if batch_shape else ""
+    for jj in range(len(k.outputs)):
+        dst = f"out{jj}_p + {obase}i * {N}u + j"
+        L.append(f"    tj_stv({dst}, o{jj}_v);" if ve > 1 else f"    tj_st({dst}, o{jj}_v[0]);")
+    return L
+
+
 def staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, BM, BN, WM, WN, MI,
                           TMW, TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t):
     """Epilogue through LDS: the accumulators are written to LDS in row-major order
@@ -298,39 +340,46 @@ def staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch
         conds = ([f"i < {M}u"] if guard_m else []) + ([f"j < {N}u"] if guard_n else [])
         if conds:
             L.append(f"    if (!({' && '.join(conds)})) continue;")
-        L.append(f"    float acc_v[{ve}];")
+        L += _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, ve,
+                        f"Cs[lr * {ldc}u + cc + q]")
+        L.append("  }")
+    return L
+
+
+def direct_staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, BM, BN, WM, WN,
+                                 TMW, TNW, NACC, guard_m, guard_n, idx_t, cfg) -> list[str] | None:
+    """Staged epilogue of the direct-to-LDS schedule.  The four K-stage arrays are free
+    once every wave has finished its last fragment reads (one barrier); wave w then
+    owns array w and stages its sub-tile through it 32 rows (one MFMA row block) at a
+    time, with no further workgroup barriers: a wave's LDS accesses complete in order.
+    Each pass turns the 32 x 32 MFMA layout into 16-byte runs of output rows, as in
+    the shared staged epilogue.  Returns None where the arrays do not fit a pass."""
+    out_dt = k.outputs[0].dtype
+    if cfg.num_warps != 4 or any(o.dtype != out_dt for o in k.outputs):
+        return None
+    ve = 16 // out_dt.itemsize if N % (16 // out_dt.itemsize) == 0 else 1
+    cols = TNW * 32
+    ldc = cols + 4
+    if 32 * ldc * 4 > min(BM, BN) * 128 or cols % ve:
+        return None
+    per_row = cols // ve
+    L = ["  __syncthreads();",
+         "  float* Cw = (float*)(wave == 0u ? As0 : wave == 1u ? As1 : wave == 2u ? Bs0 : Bs1);"]
+    for x in range(TMW):
         L.append("#pragma unroll")
-        L.append(f"    for (int q = 0; q < {ve}; ++q) acc_v[q] = Cs[lr * {ldc}u + cc + q];")
-        local = {id(mm): "acc_v[q]"}
-        for n in epi_inputs:
-            consumer = next((c for c in epilogue if n in c.inputs), epilogue[0] if epilogue else mm)
-            st = access_strides(n, consumer, out_shape)
-            terms = [v if s_ == 1 else f"{v} * {s_}u" for v, s_ in zip(full_idx, st) if s_]
-            off = " + ".join(terms) if terms else "0u"
-            nm = g.names[id(n)]
-            L.append(f"    float {nm}_v[{ve}];")
-            inner = st[-1]
-            if ve > 1 and inner == 1 and 16 // n.dtype.itemsize == ve:
-                L.append(f"    tj_ldv({nm}_p + ({off}), {nm}_v);")
-            elif inner == 0:
-                L.append(f"    {{ const float s_ = tj_ld({nm}_p[{off}]); for (int q = 0; q < {ve}; ++q) {nm}_v[q] = s_; }}")
-            else:
-                L.append(f"    for (int q = 0; q < {ve}; ++q) {nm}_v[q] = tj_ld({nm}_p[({off}) + q * {inner}u]);")
-            local[id(n)] = f"{nm}_v[q]"
-        for jj in range(len(k.outputs)):
-            L.append(f"    float o{jj}_v[{ve}];")
+        L.append(f"  for (int y = 0; y < {TNW}; ++y)")
         L.append("#pragma unroll")
-        L.append(f"    for (int q = 0; q < {ve}; ++q) {{")
-        for n in epilogue:
-            L.append(f"      const float {g.names[id(n)]} = {emit_expr(n, local)};")
-            local[id(n)] = g.names[id(n)]
-        for jj, o in enumerate(k.outputs):
-            L.append(f"      o{jj}_v[q] = {local[id(o)]};")
-        L.append("    }")
-        obase = f"bi * {M * N}u + " if batch_shape else ""
-        for jj in range(len(k.outputs)):
-            dst = f"out{jj}_p + {obase}i * {N}u + j"
-            L.append(f"    tj_stv({dst}, o{jj}_v);" if ve > 1 else f"    tj_st({dst}, o{jj}_v[0]);")
+        L.append(f"  for (int r = 0; r < {NACC}; ++r)")
+        L.append(f"    Cw[((r / 4) * 8 + (lane / 32u) * 4 + (r % 4)) * {ldc}u + y * 32u + lane % 32u] = acc[{x}][y][r];")
+        L.append(f"  for (unsigned int c = lane; c < {32 * per_row}u; c += 64u) {{")
+        L.append(f"    const unsigned int lr = c / {per_row}u, cc = (c % {per_row}u) * {ve}u;")
+        L.append(f"    const {idx_t} i = m0 + wm * {BM // WM}u + {x * 32}u + lr;")
+        L.append(f"    const {idx_t} j = n0 + wn * {BN // WN}u + cc;")
+        conds = ([f"i < {M}u"] if guard_m else []) + ([f"j < {N}u"] if guard_n else [])
+        if conds:
+            L.append(f"    if (!({' && '.join(conds)})) continue;")
+        L += _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, ve,
+                        f"Cw[lr * {ldc}u + cc + q]")
         L.append("  }")
     return L
 
@@ -1044,8 +1093,12 @@ def _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K,
     a, b = mm.inputs
     # ---- epilogue on accumulators ------------------------------------------------------
     epi_inputs = [i for i in k.inputs if i is not a and i is not b]
-    staged = staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, BM, BN, WM, WN,
-                                   MI, TMW, TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t)
+    if cfg.DIRECT:
+        staged = direct_staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, BM,
+                                              BN, WM, WN, TMW, TNW, NACC, guard_m, guard_n, idx_t, cfg)
+    else:
+        staged = staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, BM, BN, WM,
+                                       WN, MI, TMW, TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t)
     if staged is not None:
         L += staged
         L.append("}")
