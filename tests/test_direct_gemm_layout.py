@@ -1,0 +1,133 @@
+"""The direct-to-LDS GEMM schedule, checked on the CPU from its generated source.
+
+The kernel writes LDS through DMA (each load instruction places lane ``l``'s 16 bytes
+at byte ``16 l`` of a 1 KiB block, so the swizzle lives in *which* global chunk each
+lane fetches) and reads MFMA fragments with a different set of expressions.  These
+tests evaluate both sets of expressions exactly as generated, for every wave and
+lane, and check that (a) the DMA fills each LDS slot of a stage exactly once, (b)
+every fragment read returns the (row, k-chunk) the 32x32x16 MFMA expects in that
+lane, and (c) the 16 lanes that share an LDS access cycle hit 16 distinct 16-byte
+bank groups.  The wait-count immediate is pinned against the assembler's own
+decoding of a compiled kernel."""
+import re
+import shutil
+import subprocess
+
+import pytest
+
+import tensorjit as tj
+import tensorjit.compiler as C
+from tensorjit.backends import hip_backend as hb
+from tensorjit.backends import hip_gemm as hg
+from tensorjit.ir import DType, TensorType
+from tensorjit.runtime.autotune import MatmulConfig
+
+DIRECT = MatmulConfig(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1)
+DIRECT_N128 = MatmulConfig(256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1)
+
+
+def _source(cfg, M=256, N=256, K=64, epi="plain"):
+    fns = {"plain": (lambda x, w: tj.linear(x, w), [(M, K), (N, K)]),
+           "residual": (lambda x, w, r: tj.linear(x, w) + r, [(M, K), (N, K), (M, N)]),
+           "bias_gelu": (lambda x, w, b: tj.gelu(tj.linear(x, w, b)), [(M, K), (N, K), (N,)])}
+    fn, shapes = fns[epi]
+    p = C.lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    return hb.generate(p, {0: cfg})
+
+
+def _c_eval(expr: str, env: dict) -> int:
+    """Evaluate a generated unsigned-int C expression (literals with a u suffix,
+    + * ^ & >> and parentheses) in Python."""
+    py = re.sub(r"(\d+)u\b", r"\1", expr)
+    return int(eval(py, {}, dict(env))) & 0xFFFFFFFF
+
+
+@pytest.mark.parametrize("cfg", [DIRECT, DIRECT_N128], ids=["256x256", "256x128"])
+def test_dma_placement_and_fragment_reads_agree(cfg):
+    K = 64
+    src, launches = _source(cfg, N=cfg.TN, K=K)
+    nw, WM, WN = cfg.num_warps, cfg.WM, cfg.WN
+    for op, rows, wdim, rowdim in (("A", cfg.TM, WM, cfg.TM // WM), ("B", cfg.TN, WN, cfg.TN // WN)):
+        vo = dict(re.findall(rf"  vo{op}\[(\d+)\] = (.*);\n", src))
+        dst = re.findall(rf"raw_ptr_buffer_load_lds\(rs{op}, \(__attribute__\(\(address_space\(3\)\)\) void\*\)"
+                         rf"\({op}s0 \+ (.*?)\), 16, vo{op}\[(\d+)\], \(int\)\(\(0\) \* 128u\), 0, 0\);", src)
+        assert vo and dst and len({i for _, i in dst}) == len(vo), op
+        slots = {}
+        for wv in range(nw):
+            for lane in range(64):
+                env = {"m0": 0, "n0": 0, "wv": wv, "lane": lane, "drow": lane >> 3}
+                for lds_expr, i in dst:
+                    off = _c_eval(vo[i], env)                # global byte offset of this lane's 16 bytes
+                    g_row, g_col = divmod(off // 2, K)
+                    assert g_col % 8 == 0
+                    slot = (_c_eval(lds_expr, env) + lane * 16) // 16
+                    assert slot not in slots, (op, wv, lane, i)
+                    slots[slot] = (g_row, g_col // 8)
+        assert sorted(slots) == list(range(rows * K * 2 // 16)), op      # every 16-byte slot filled once
+        # fragment reads: lane l of wave (wm, wn), tile x / y, sub-step ks wants row base + 32 x + l % 32,
+        # 16-byte chunk 2 ks + l / 32 (8 bf16 of k per lane, 16 per MFMA)
+        fsw = re.search(r"const unsigned int fsw = (.*);", src).group(1)
+        base = re.search(rf"const unsigned int {'arow' if op == 'A' else 'brow'} = (.*);", src).group(1)
+        fofs = re.search(r"fofs\[ks\] = (.*);", src).group(1)
+        reads = re.findall(rf"f{'a' if op == 'A' else 'b'}\[\d\]\[(\d)\] = \*\(const tj_bf16x8\*\)\({op}s0 \+ "
+                           rf"{'arow' if op == 'A' else 'brow'} \+ fofs\[(\d)\] \+ (\d+)u\);", src)
+        assert reads, op
+        for w in range(wdim):
+            for lane in range(64):
+                env = {"fr": lane & 31, "fh": lane >> 5, "wm": w, "wn": w}
+                env["fsw"] = _c_eval(fsw, env)
+                for t, ks, xoff in set(reads):
+                    env["ks"] = int(ks)
+                    addr = _c_eval(base, env) + _c_eval(fofs, env) + int(xoff)
+                    want = (w * rowdim + int(t) * 32 + (lane & 31), 2 * int(ks) + (lane >> 5))
+                    assert slots[addr // 16] == want, (op, w, lane, t, ks)
+        # bank groups: lanes 16 g .. 16 g + 15 of one read touch 16 distinct 16-byte groups of a 256-byte row
+        for w in range(wdim):
+            for t, ks, xoff in set(reads):
+                for g in range(4):
+                    grp = []
+                    for lane in range(16 * g, 16 * g + 16):
+                        env = {"fr": lane & 31, "fh": lane >> 5, "wm": w, "wn": w, "ks": int(ks)}
+                        env["fsw"] = _c_eval(fsw, env)
+                        grp.append(((_c_eval(base, env) + _c_eval(fofs, env) + int(xoff)) // 16) % 16)
+                    assert len(set(grp)) == 16, (op, w, t, ks, g, grp)
+
+
+@pytest.mark.parametrize("epi", ["plain", "residual", "bias_gelu"])
+@pytest.mark.parametrize("shape", [(256, 256, 64), (300, 520, 192), (1024, 768, 4096)])
+def test_direct_kernels_compile_for_gfx950(epi, shape, tj_env):
+    M, N, K = shape
+    for cfg in (DIRECT, DIRECT_N128):
+        src, launches = _source(cfg, M, N, K, epi)
+        assert launches[0].meta["config"]["DIRECT"] == 1
+        assert launches[0].meta.get("epilogue") == "lds-staged"
+        assert "raw_ptr_buffer_load_lds" in src and "__builtin_amdgcn_s_waitcnt(0x0F70);" in src
+        hb.compile_source(src, "gfx950")
+
+
+def test_direct_config_rules():
+    p = C.lower(tj.trace(lambda x, w: tj.linear(x, w), [TensorType((512, 200), DType.bf16),
+                                                       TensorType((512, 200), DType.bf16)]), "hip")
+    mm = p.kernels[0].anchor
+    assert not hb.config_ok(DIRECT, DType.bf16, mm)                        # K not a multiple of 64
+    p = C.lower(tj.trace(lambda x, w: tj.matmul(x, w), [TensorType((512, 256), DType.bf16),
+                                                       TensorType((256, 512), DType.bf16)]), "hip")
+    assert not hb.config_ok(DIRECT, DType.bf16, p.kernels[0].anchor)       # NN layout
+    assert not hb.config_ok(DIRECT, DType.f32)                             # 16-bit operands only
+    assert not hb.config_ok(MatmulConfig(256, 256, 32, 4, 2, 2, 32, 1, 8, 0, 0, 1), DType.bf16)   # TK must be 64
+
+
+@pytest.mark.skipif(shutil.which("llvm-objdump") is None and not __import__("os").path.exists(
+    "/opt/rocm/llvm/bin/llvm-objdump"), reason="llvm-objdump not available")
+def test_vmcnt_immediate_decodes_as_intended(tmp_path):
+    ns = [0, 5, 15, 16, 24, 63]
+    # one wait per kernel: inside one kernel the compiler merges redundant waits
+    src = "\n".join(f'extern "C" __global__ void probe{n}() {{ __builtin_amdgcn_s_waitcnt({hg._vmcnt_only(n)}); }}'
+                    for n in ns)
+    code = hb.compile_source(src, "gfx950")
+    (tmp_path / "p.co").write_bytes(code)
+    objdump = shutil.which("llvm-objdump") or "/opt/rocm/llvm/bin/llvm-objdump"
+    dis = subprocess.run([objdump, "-d", "--mcpu=gfx950", str(tmp_path / "p.co")], capture_output=True,
+                         text=True, check=True).stdout
+    waits = [re.sub(r"\s*(expcnt\(7\)|lgkmcnt\(15\))", "", w).strip() for w in re.findall(r"s_waitcnt\s+([^\n/]*)", dis)]
+    assert waits == [f"vmcnt({n})" for n in ns], waits      # expcnt / lgkmcnt left at their maxima
