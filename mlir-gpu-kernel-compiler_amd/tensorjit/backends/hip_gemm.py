@@ -488,8 +488,7 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         L.append(f"  const {CTYPE[b.dtype]}* __restrict__ Bb = {B}_p;")
 
     if cfg.DIRECT:
-        L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, guard_m, guard_n, idx_t,
-                               CTYPE[a.dtype], CTYPE[b.dtype])
+        L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin)
         return _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW,
                               TNW, NACC, THREADS, 0, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
 
@@ -921,28 +920,29 @@ def _vmcnt_only(n: int) -> str:
     return hex((n & 15) | ((n >> 4) << 14) | 0x0F70)
 
 
-def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, guard_m, guard_n, idx_t,
-                      a_ct, b_ct) -> list[str]:
+def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> list[str]:
     """Main loop for one wave per SIMD with tiles loaded straight into LDS (``DIRECT``).
 
-    ``global_load_lds_dwordx4`` moves 16 bytes per lane from HBM/L2 into LDS without
-    passing through registers: no staging VGPRs and no LDS store instructions, so the
-    wave's issue slots go to its MFMAs and fragment reads.  One instruction writes
-    1 KiB of LDS contiguously (lane i at byte 16 i), i.e. eight 128-byte K rows of a
-    64-deep tile.  Rows are not padded; instead the 16-byte chunk ``c`` of tile row
-    ``r`` is stored at position ``c ^ f(r)`` with ``f(r) = (r & 7) ^ ((r >> 3) & 3)``,
-    applied by choosing which chunk each lane fetches (the 8 lanes of a row still
-    cover one whole 128-byte line).  Sixteen lanes of an MFMA fragment read (16
-    consecutive rows, one chunk) then land on 16 distinct 16-byte bank groups.
+    ``buffer_load_dwordx4 ... lds`` moves 16 bytes per lane from HBM/L2 into LDS
+    without passing through registers: no staging VGPRs and no LDS store
+    instructions, so each wave can hold a 128x128 accumulator tile (256 AGPRs) and its
+    issue slots go to MFMAs and fragment reads.  One instruction writes 1 KiB of LDS
+    contiguously (lane i at byte 16 i), i.e. eight 128-byte K rows of a 64-deep tile.
+    Rows are not padded; instead the 16-byte chunk ``c`` of tile row ``r`` is stored at
+    position ``c ^ f(r)`` with ``f(r) = (r & 7) ^ ((r >> 3) & 3)``, applied by choosing
+    which chunk each lane fetches (the 8 lanes of a row still cover one whole 128-byte
+    line).  Sixteen lanes of an MFMA fragment read (16 consecutive rows, one chunk)
+    then land on 16 distinct 16-byte bank groups.
 
     Two LDS stages, each operand and stage its own ``__shared__`` array so the
     compiler can tell the stage being filled from the stage being read and does not
     wait for the loads in flight before each fragment read.  Tile kt (stage kt & 1):
-    region A issues the loads of tile kt+1 into the other stage, then runs the MFMAs
-    of sub-steps 0 .. KS-2 with the fragment reads of the next sub-steps threaded
-    between them; a barrier (which waits for this wave's loads) publishes tile kt+1;
-    region B runs the last sub-step's MFMAs with the reads of tile kt+1's first
-    fragments."""
+    region A runs the MFMAs of sub-steps 0 .. KS-2 with the fragment reads of the next
+    sub-steps threaded between them, plus the second half of tile kt+1's loads; a
+    barrier (after each wave's wait for its own loads) publishes tile kt+1 and frees
+    stage kt & 1; region B runs the last sub-step's MFMAs with the reads of tile
+    kt+1's first fragments and the first half of tile kt+2's loads into the freed
+    stage.  Every load so gets a whole tile of MFMAs to land."""
     nw = cfg.num_warps
     KS = 4                                  # 64-deep tile, 16 per 32x32x16 MFMA
     # Barrier that publishes a stage filled by DMA: each wave first waits for its own
@@ -959,7 +959,7 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, guard_
          f"  __shared__ __attribute__((aligned(1024))) char Bs1[{BN * 128}];",
          "  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave);",
          "  const unsigned int drow = lane >> 3;",
-         f"  {'tj_f32x16'} acc[{TMW}][{TNW}];",
+         f"  tj_f32x16 acc[{TMW}][{TNW}];",
          "#pragma unroll",
          f"  for (int x = 0; x < {TMW}; ++x)",
          "#pragma unroll",
