@@ -183,7 +183,10 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     L.append(f"  {acc_t} acc[{NT}];")
     L.append("#pragma unroll")
     L.append(f"  for (int t = 0; t < {NT}; ++t) acc[t] = ({acc_t})(0.0f);")
-    L.append(f"  const unsigned int kw = wave * {steps_per_wave * KI}u;")
+    # the K slice of wave w in workgroup b is (w + b) mod SK: at any moment the
+    # workgroups read different parts of A (which every workgroup reads whole) instead
+    # of all requesting the same lines (27.7 vs 30.5 us for 16 x 8192 x 8192, TN 32)
+    L.append(f"  const unsigned int kw = ((wave + blockIdx.x) % {SK}u) * {steps_per_wave * KI}u;")
     L.append(f"  for (int it = 0; it < {iters}; ++it) {{")
     L.append(f"    tj_u32x4 ra[{U}], rb[{U}][{NT}];")
     L.append("#pragma unroll")
