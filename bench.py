@@ -129,15 +129,21 @@ def timed_steps(torch, fn, args, steps, warmup):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
-def kernel_ms(f, args, k=0, iters=20):
+def kernel_ms(f, args, k=None, iters=20):
+    """Device time of launch ``k``, or of all the program's launches (``k=None``: a
+    split-K GEMM is one kernel with two launches)."""
     cp = f.compiled(*args)
-    return cp.kernel_time_ms(k, *args, warmup=3, iters=iters)
+    ks = range(len(cp.launches)) if k is None else [k]
+    return sum(cp.kernel_time_ms(i, *args, warmup=3, iters=iters) for i in ks)
 
 
-def kernel_ms_settled(cp, args, k=0, rounds=3, iters=10):
+def kernel_ms_settled(cp, args, k=None, rounds=3, iters=10):
     """Best of ``rounds`` averages of ``iters`` launches after a warm-up long enough for
-    the clocks of an MFMA-bound kernel to settle (a cold first average reads 10-20% slow)."""
-    return min(cp.kernel_time_ms(k, *args, warmup=10 if r == 0 else 2, iters=iters) for r in range(rounds))
+    the clocks of an MFMA-bound kernel to settle (a cold first average reads 10-20% slow);
+    ``k=None`` sums all the program's launches."""
+    ks = range(len(cp.launches)) if k is None else [k]
+    return sum(min(cp.kernel_time_ms(i, *args, warmup=10 if r == 0 else 2, iters=iters) for r in range(rounds))
+               for i in ks)
 
 
 def load_traffic(workload: str):

@@ -75,7 +75,10 @@ def analytic_config(k: Kernel) -> MatmulConfig:
 # ---------------------------------------------------------------------------
 
 
-def generate_kernel(k: Kernel, idx: int, cfg: MatmulConfig | None = None) -> tuple[str, Launch]:
+def generate_kernel(k: Kernel, idx: int, cfg: MatmulConfig | None = None) -> tuple[str, Launch | list[Launch]]:
+    """HIP source of one fused kernel and its launch(es).  A GEMM whose K is split
+    across workgroups (``KSPLIT``) has two: partial products into a workspace, then
+    the sum of the partials with the fused epilogue."""
     g = KernelGen.of(k, idx)
     if k.kind == "elementwise":
         return gen_elementwise(g)
@@ -94,14 +97,46 @@ def generate_kernel(k: Kernel, idx: int, cfg: MatmulConfig | None = None) -> tup
 
 
 def generate(program: Program, configs: dict[int, MatmulConfig] | None = None) -> tuple[str, list[Launch]]:
-    """HIP source of the whole program (prelude + one ``extern "C"`` kernel per fused kernel)."""
+    """HIP source of the whole program (prelude + the ``extern "C"`` kernels of every fused
+    kernel) and its launches in order; ``meta["kernel"]`` is each launch's kernel index."""
     configs = configs or {}
     sources, launches = [PRELUDE], []
     for idx, k in enumerate(program.kernels):
-        src, launch = generate_kernel(k, idx, configs.get(idx))
+        src, ls = generate_kernel(k, idx, configs.get(idx))
         sources.append(src)
-        launches.append(launch)
+        for launch in ls if isinstance(ls, list) else [ls]:
+            launch.meta["kernel"] = idx
+            launches.append(launch)
     return "\n\n".join(sources), launches
+
+
+WS_ALIGN = 256
+
+
+def workspace_layout(launches: list[Launch], base: int) -> tuple[dict[int, int], int]:
+    """Arena offsets of the kernels' workspaces (split-K partials), placed after the
+    planned intermediates (``base`` bytes) in the same allocation, and the total size."""
+    off = -(-base // WS_ALIGN) * WS_ALIGN
+    ws: dict[int, int] = {}
+    for launch in launches:
+        need = launch.meta.get("workspace", 0)
+        if need:
+            ws[launch.meta["kernel"]] = off
+            off += -(-need // WS_ALIGN) * WS_ALIGN
+    return ws, (off if ws else base)
+
+
+def launch_args(launches: list[Launch], kernel_args: list[list], ws: dict[int, int]) -> list[list]:
+    """Per-launch pointer refs: the kernel's inputs and outputs, plus its workspace for
+    the launches that take one (``meta["ws_arg"]``)."""
+    out = []
+    for launch in launches:
+        idx = launch.meta["kernel"]
+        refs = list(kernel_args[idx])
+        if launch.meta.get("ws_arg"):
+            refs.append((rt.ARENA, ws[idx]))
+        out.append(refs)
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -175,7 +210,8 @@ class HipProgram:
                 self.matmul_configs[idx] = self._pick_config(k, idx, tune)
         self.source, self.launches = generate(program, self.matmul_configs)
         self.code = compile_source(self.source, self.arch)
-        self._native = self._load(self.code, self.launches, self._args)
+        self._workspace, self.arena_bytes = workspace_layout(self.launches, self.plan.arena_bytes)
+        self._native = self._load(self.code, self.launches, launch_args(self.launches, self._args, self._workspace))
 
         self.pool = BufferPool()
         # hipGraph replay is opt-in: on ROCm a graph launch costs more host time
@@ -199,7 +235,7 @@ class HipProgram:
     def _load(self, code: bytes, launches: list[Launch], args) -> rt.NativeHipProgram:
         return rt.NativeHipProgram(self.device_index, code, [l.name for l in launches],
                                    [(l.grid, l.block, l.shared) for l in launches], args,
-                                   self.plan.arena_bytes, len(self.program.graph.inputs), len(self._out_nodes))
+                                   self.arena_bytes, len(self.program.graph.inputs), len(self._out_nodes))
 
     def _pick_config(self, k: Kernel, idx: int, tune: bool) -> MatmulConfig:
         store = AutotuneStore()
@@ -228,12 +264,16 @@ class HipProgram:
         stream = torch.cuda.current_stream(dev).cuda_stream
 
         def build(cfg: MatmulConfig):
-            src, launch = generate(single, {0: cfg})
+            src, launches = generate(single, {0: cfg})
             code = compile_source(src, self.arch)
-            prog = rt.NativeHipProgram(self.device_index, code, [launch[0].name], [(launch[0].grid, launch[0].block, 0)],
-                                       args, 0, len(ins), len(outs))
+            ws, arena = workspace_layout(launches, 0)
+            prog = rt.NativeHipProgram(self.device_index, code, [l.name for l in launches],
+                                       [(l.grid, l.block, 0) for l in launches], launch_args(launches, args, ws),
+                                       arena, len(ins), len(outs))
             ip, op = [t.data_ptr() for t in ins], [t.data_ptr() for t in outs]
-            return lambda warmup, iters: prog.kernel_time(0, ip, op, stream, warmup, iters)
+            # a split-K kernel is timed as the sum of its two launches
+            return lambda warmup, iters: sum(prog.kernel_time(i, ip, op, stream, warmup, iters)
+                                             for i in range(len(launches)))
 
         def timer(run, warmup, iters):
             # enough launches for ~2 ms of device time per measurement (>= 3)
@@ -247,7 +287,8 @@ class HipProgram:
     # -- protocol ---------------------------------------------------------------
     @property
     def num_kernels(self) -> int:
-        return len(self.launches)
+        """Fused kernels of the plan (a split-K GEMM is one kernel with two launches)."""
+        return len(self.program.kernels)
 
     @property
     def native(self) -> rt.NativeHipProgram:

@@ -69,6 +69,16 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
     if (dt, cfg.MI) not in MFMA:
         return False
     _, ki, _, _, _ = MFMA[(dt, cfg.MI)]
+    if cfg.KSPLIT > 1:
+        # K split over workgroups: the plain double-buffered schedule or the skinny
+        # kernel, every split an equal whole number of K steps (no K edge inside a split)
+        if cfg.PINGPONG or cfg.INTERLEAVE or cfg.DIRECT or cfg.KSPLIT > 16:
+            return False
+        if mm is not None:
+            K = matmul_dims(mm)[2]
+            step = cfg.KSPLIT * (cfg.SPLIT_K * ki if cfg.SPLIT_K > 1 else cfg.TK)
+            if K % step:
+                return False
     if cfg.SPLIT_K > 1:
         # skinny kernel: one MI x MI tile per workgroup, K split over its waves (NT, bf16/fp16)
         ok = (dt in (DType.bf16, DType.f16) and cfg.TM == cfg.MI and cfg.TN % cfg.MI == 0
@@ -136,14 +146,17 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     out_shape = tuple(mm.shape)
     batch_shape = out_shape[:-2]
     batch = math.prod(batch_shape) if batch_shape else 1
-    steps_total = -(-K // KI)
+    S = cfg.KSPLIT                                   # workgroups along K (partials summed by a 2nd launch)
+    Kw = K // S                                      # this workgroup's K range
+    steps_total = -(-Kw // KI)
     steps_per_wave = -(-steps_total // SK)
     iters = -(-steps_per_wave // U)
-    k_guard = steps_per_wave * SK * KI != K or iters * U != steps_per_wave
+    k_guard = steps_per_wave * SK * KI != Kw or iters * U != steps_per_wave
     A, B = g.names[id(a)], g.names[id(b)]
     epilogue = [n for n in k.nodes if n is not mm]
     fname = g.fname
-    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {fname}({g.params()}) {{']
+    ws_param = ", float* __restrict__ ws_p" if S > 1 else ""
+    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {fname}({g.params()}{ws_param}) {{']
     L.append(f"  __shared__ float red[{SK}][{MI}][{TN + 1}];")
     L.append("  const unsigned int tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;")
     L.append(f"  const unsigned int n0 = blockIdx.x * {TN}u;")
@@ -186,7 +199,8 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     # the K slice of wave w in workgroup b is (w + b) mod SK: at any moment the
     # workgroups read different parts of A (which every workgroup reads whole) instead
     # of all requesting the same lines (27.7 vs 30.5 us for 16 x 8192 x 8192, TN 32)
-    L.append(f"  const unsigned int kw = ((wave + blockIdx.x) % {SK}u) * {steps_per_wave * KI}u;")
+    L.append(f"  const unsigned int kw = {'blockIdx.y * ' + str(Kw) + 'u + ' if S > 1 else ''}"
+             f"((wave + blockIdx.x) % {SK}u) * {steps_per_wave * KI}u;")
     L.append(f"  for (int it = 0; it < {iters}; ++it) {{")
     L.append(f"    tj_u32x4 ra[{U}], rb[{U}][{NT}];")
     L.append("#pragma unroll")
@@ -222,6 +236,17 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     L.append("    float s = 0.0f;")
     L.append("#pragma unroll")
     L.append(f"    for (int w = 0; w < {SK}; ++w) s += red[w][i][jj];")
+    if S > 1:
+        # this workgroup's K-range partial; the second launch sums and applies the epilogue
+        bi = "bi" if batch_shape else "0u"
+        L += [f"    ws_p[(({bi} * {S}u + blockIdx.y) * {M}u + i) * {N}u + j] = s;", "  }", "}"]
+        grid = (-(-N // TN), S, batch)
+        meta = {"family": "matmul_skinny", "config": cfg.as_dict(), "dtype": dt.value, "M": M, "N": N, "K": K,
+                "batch": batch, "trans_b": tb, "lds_bytes": SK * MI * (TN + 1) * 4, "flops": 2.0 * M * N * K * batch,
+                "workspace": batch * S * M * N * 4, "ws_arg": True}
+        epi_inputs = [i for i in k.inputs if i is not a and i is not b]
+        src2, sum_launch = gen_ksplit_sum(g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, S, fname)
+        return "\n".join(L) + "\n\n" + src2, [Launch(fname, grid, (THREADS, 1, 1), 0, meta), sum_launch]
     L.append(f"    const float {g.names[id(mm)]} = s;")
     local = {id(mm): g.names[id(mm)]}
     full_idx = list(bidx) + ["i", "j"]
@@ -451,7 +476,9 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     epilogue = [n for n in k.nodes if n is not mm]
     idx_t = "unsigned long" if batch * M * N >= 2**31 or batch * max(M, N) * K >= 2**31 else "unsigned int"
 
-    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {fname}({g.params()}) {{']
+    S = cfg.KSPLIT
+    ws_param = ", float* __restrict__ ws_p" if S > 1 else ""
+    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {fname}({g.params()}{ws_param}) {{']
     a_bytes = 2 * BM * LDK * esz
     lds_bytes = a_bytes + 2 * BN * LDK * esz
     if not cfg.DIRECT:
@@ -464,7 +491,7 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     L += tile_order_lines(ntm, ntn, cfg.GROUP_M, BM, BN)
     # batch offsets
     if batch_shape:
-        L.append(f"  const {idx_t} bi = blockIdx.z;")
+        L.append(f"  const {idx_t} bi = blockIdx.z / {S}u;" if S > 1 else f"  const {idx_t} bi = blockIdx.z;")
         bst = contiguous_strides(batch_shape)
         bidx = []
         rem = "bi"
@@ -494,6 +521,12 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin)
         return _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW,
                               TNW, NACC, THREADS, 0, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
+
+    # K split over workgroups: this workgroup's K steps are [ksp * KTs, (ksp + 1) * KTs)
+    KTs = KT // S
+    if S > 1:
+        L.append(f"  const unsigned int ksp = blockIdx.z % {S}u, kbase = ksp * {KTs * BK}u;")
+    kb = "kbase + " if S > 1 else ""
 
     # ---- global -> register staging ------------------------------------------------
     def plan_k_major(rows: int, vec: bool):
@@ -699,21 +732,21 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     # the MFMAs on LDS[kt & 1], then writes the registers (tile kt+1, loaded one full
     # MFMA phase earlier) to LDS[(kt+1) & 1], then issues the global loads of tile kt+2
     # so their latency hides behind the next step's MFMAs; one barrier per step.
-    L.append("  unsigned int k0 = 0;")
+    L.append(f"  unsigned int k0 = {kb}0u;")
     L += load_lines()
     L += store_lines("0")
-    if KT > 1:
-        L.append(f"  k0 = {BK}u;")
+    if KTs > 1:
+        L.append(f"  k0 = {kb}{BK}u;")
         L += load_lines()
     L.append("  __syncthreads();")
-    L.append(f"  for (int kt = 0; kt < {KT}; ++kt) {{")
+    L.append(f"  for (int kt = 0; kt < {KTs}; ++kt) {{")
     L.append("    const int cur = kt & 1;")
     L += ["  " + s for s in compute_lines("cur")]
-    L.append(f"    if (kt + 1 < {KT}) {{")
+    L.append(f"    if (kt + 1 < {KTs}) {{")
     L += ["    " + s for s in store_lines("cur ^ 1")]
     L.append("    }")
-    L.append(f"    if (kt + 2 < {KT}) {{")
-    L.append(f"      k0 = (kt + 2) * {BK}u;")
+    L.append(f"    if (kt + 2 < {KTs}) {{")
+    L.append(f"      k0 = {kb}(kt + 2) * {BK}u;")
     L += ["    " + s for s in load_lines()]
     L.append("    }")
     L.append("    __syncthreads();")
@@ -1091,11 +1124,88 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
     return L
 
 
+def _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW, TNW,
+                   NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname):
+    """K split over workgroups: each workgroup stores its fp32 partial tile into the
+    workspace ``[batch][KSPLIT][M][N]``; a second launch sums the partials and applies
+    the fused epilogue (``gen_ksplit_sum``)."""
+    S = cfg.KSPLIT
+    if MI == 32:
+        row_of, col_of = "(r / 4) * 8 + (lane / 32u) * 4 + (r % 4)", "lane % 32u"
+    else:
+        row_of, col_of = "(lane / 16u) * 4 + r", "lane % 16u"
+    bi = "bi" if batch_shape else "0u"
+    L += ["#pragma unroll", f"  for (int x = 0; x < {TMW}; ++x)", "#pragma unroll", f"  for (int y = 0; y < {TNW}; ++y)",
+          "#pragma unroll", f"  for (int r = 0; r < {NACC}; ++r) {{",
+          f"    const {idx_t} i = m0 + wm * {BM // WM}u + x * {MI}u + {row_of};",
+          f"    const {idx_t} j = n0 + wn * {BN // WN}u + y * {MI}u + {col_of};"]
+    conds = ([f"i < {M}u"] if guard_m else []) + ([f"j < {N}u"] if guard_n else [])
+    if conds:
+        L.append(f"    if ({' && '.join(conds)})")
+    L += [f"    ws_p[(({bi} * {S}u + ksp) * {M}u + i) * {N}u + j] = acc[x][y][r];", "  }", "}"]
+    grid = (-(-N // BN), -(-M // BM), batch * S)
+    ws_bytes = batch * S * M * N * 4
+    meta = {"family": "matmul", "config": cfg.as_dict(), "dtype": dt.value, "M": M, "N": N, "K": K, "batch": batch,
+            "trans_b": tb, "lds_bytes": lds_bytes, "flops": 2.0 * M * N * K * batch, "workspace": ws_bytes,
+            "ws_arg": True, "epilogue": "k-split partials"}
+    partial = Launch(fname, grid, (THREADS, 1, 1), 0, meta)
+    src2, sum_launch = gen_ksplit_sum(g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, S, fname)
+    return "\n".join(L) + "\n\n" + src2, [partial, sum_launch]
+
+
+def gen_ksplit_sum(g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, S, fname) -> tuple[str, Launch]:
+    """Second launch of a K-split GEMM: out = epilogue(sum over the S partials), one lane
+    per run of ``ve`` outputs (16-byte output stores, 16-byte partial loads)."""
+    out_dt = k.outputs[0].dtype
+    ve = 16 // out_dt.itemsize if N % (16 // out_dt.itemsize) == 0 else 1
+    if any(o.dtype.itemsize != out_dt.itemsize for o in k.outputs):
+        ve = 1
+    batch = math.prod(batch_shape) if batch_shape else 1
+    runs = batch * M * N // ve
+    idx_t = "unsigned long" if batch * M * N >= 2**31 else "unsigned int"
+    name = fname + "_ksum"
+    L = [f'extern "C" __global__ __launch_bounds__(256) void {name}({g.params()}, const float* __restrict__ ws_p) {{',
+         f"  const {idx_t} t = ({idx_t})blockIdx.x * 256u + threadIdx.x;",
+         f"  if (t >= {runs}u) return;",
+         f"  const {idx_t} e = t * {ve}u, bi = e / {M * N}u, rem = e % {M * N}u, i = rem / {N}u, j = rem % {N}u;"]
+    bidx = []
+    if batch_shape:
+        rem = "bi"
+        for d, cst in enumerate(contiguous_strides(batch_shape)):
+            v = f"b{d}"
+            if d == len(batch_shape) - 1:
+                L.append(f"  const {idx_t} {v} = {rem};")
+            else:
+                L.append(f"  const {idx_t} {v} = {rem} / {cst}u, br{d} = {rem} % {cst}u;")
+                rem = f"br{d}"
+            bidx.append(v)
+    L.append(f"  float sm[{ve}];")
+    L.append("#pragma unroll")
+    L.append(f"  for (int q = 0; q < {ve}; ++q) sm[q] = 0.0f;")
+    L.append("#pragma unroll")
+    L.append(f"  for (int s = 0; s < {S}; ++s) {{")
+    L.append(f"    const float* src = ws_p + ((bi * {S}u + s) * {M}u + i) * {N}u + j;")
+    if ve % 4 == 0:
+        L += ["#pragma unroll", f"    for (int q4 = 0; q4 < {ve // 4}; ++q4) {{",
+              "      const tj_f32x4 x = *(const tj_f32x4*)(src + q4 * 4);",
+              "      sm[q4 * 4] += x[0]; sm[q4 * 4 + 1] += x[1]; sm[q4 * 4 + 2] += x[2]; sm[q4 * 4 + 3] += x[3];", "    }"]
+    else:
+        L.append(f"    for (int q = 0; q < {ve}; ++q) sm[q] += src[q];")
+    L.append("  }")
+    L += _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, ve, "sm[q]")
+    L.append("}")
+    meta = {"family": "ksplit_sum", "splits": S, "ws_arg": True, "numel": batch * M * N}
+    return "\n".join(L), Launch(name, (-(-runs // 256), 1, 1), (256, 1, 1), 0, meta)
+
+
 def _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW, TNW, NACC,
                    THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname):
     a, b = mm.inputs
     # ---- epilogue on accumulators ------------------------------------------------------
     epi_inputs = [i for i in k.inputs if i is not a and i is not b]
+    if cfg.KSPLIT > 1:
+        return _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, K, BM, BN, WM, WN, MI,
+                              TMW, TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
     if cfg.DIRECT:
         staged = direct_staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, BM,
                                               BN, WM, WN, TMW, TNW, NACC, guard_m, guard_n, idx_t, cfg)

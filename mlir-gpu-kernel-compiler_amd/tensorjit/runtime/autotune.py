@@ -59,18 +59,19 @@ class MatmulConfig:
     GROUP_M: int = 8        # tile rows per group of the XCD-aware tile order (0 = plain row-major order)
     PINGPONG: int = 0       # two wave groups alternate MFMA and memory phases: 1/2 = loads 2/3 K steps ahead, 3 = K-split tiles
     INTERLEAVE: int = 0     # 1: one wave per SIMD, memory instructions threaded between its MFMAs
-    DIRECT: int = 0         # 1: one wave per SIMD, tiles loaded straight into LDS (global_load_lds_dwordx4)
+    DIRECT: int = 0         # 1: one wave per SIMD, tiles loaded straight into LDS (buffer_load_dwordx4 ... lds)
+    KSPLIT: int = 1         # > 1: K split over that many workgroups, partials summed by a second launch
 
     def as_dict(self) -> dict:
         return {"TM": self.TM, "TN": self.TN, "TK": self.TK, "num_warps": self.num_warps,
                 "WM": self.WM, "WN": self.WN, "MI": self.MI, "SPLIT_K": self.SPLIT_K, "GROUP_M": self.GROUP_M,
-                "PINGPONG": self.PINGPONG, "INTERLEAVE": self.INTERLEAVE, "DIRECT": self.DIRECT}
+                "PINGPONG": self.PINGPONG, "INTERLEAVE": self.INTERLEAVE, "DIRECT": self.DIRECT, "KSPLIT": self.KSPLIT}
 
     @staticmethod
     def from_dict(d: dict) -> "MatmulConfig":
         return MatmulConfig(d["TM"], d["TN"], d.get("TK", 0), d.get("num_warps", 4), d.get("WM", 2),
                             d.get("WN", 2), d.get("MI", 32), d.get("SPLIT_K", 1), d.get("GROUP_M", 8),
-                            d.get("PINGPONG", 0), d.get("INTERLEAVE", 0), d.get("DIRECT", 0))
+                            d.get("PINGPONG", 0), d.get("INTERLEAVE", 0), d.get("DIRECT", 0), d.get("KSPLIT", 1))
 
 
 # bf16 / fp16 candidates (MFMA 32x32x16 or 16x16x32)
@@ -121,6 +122,11 @@ HIP_F32_CANDIDATES: list[MatmulConfig] = [
     MatmulConfig(32, 64, 32, 4, 2, 2, 16),
     MatmulConfig(64, 32, 32, 4, 2, 2, 16),
     MatmulConfig(32, 32, 64, 4, 2, 2, 16),
+    # K split over workgroups (few output tiles, long K: config 1's 512x768x3072)
+    MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 8),
+    MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 4),
+    MatmulConfig(32, 32, 64, 4, 2, 2, 16, 1, 8, 0, 0, 0, 4),
+    MatmulConfig(32, 64, 64, 4, 2, 2, 16, 1, 8, 0, 0, 0, 4),
 ]
 
 
@@ -165,7 +171,9 @@ def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) 
         return math.inf
     # workgroups per CU: LDS, and registers (a SIMD holds 512 per lane; waves spread over 4 SIMDs)
     occ = max(1, min(LDS_BYTES_PER_CU // lds, int(512 // regs) * 4 // waves, 32 // waves))
-    tiles = -(-M // tm) * -(-N // tn) * batch
+    S = cfg.KSPLIT
+    tiles = -(-M // tm) * -(-N // tn) * batch * S                  # a K split multiplies the workgroups
+    kt = K / S                                                     # ... each over 1/S of K
     slots = CU_COUNT * occ
     rounds = -(-tiles // slots)
     fill = tiles / (rounds * slots)
@@ -175,15 +183,17 @@ def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) 
     peak = (MFMA_FLOP_PER_CLK_BF16 if elem == 2 else MFMA_FLOP_PER_CLK_F32) * CU_COUNT * CLOCK_HZ
     t_mfma = flops / (peak * max(fill, 1e-3) * max(busy_cus, 1e-3) * edge) * _sched_factor(cfg)
     # LDS: per K step each wave reads (tm/WM + tn/WN) x tk elements; per CU per tile
-    lds_bytes_tile = waves * (tm / cfg.WM + tn / cfg.WN) * K * elem
-    lds_bytes_tile += (tm + tn) * K * elem                         # the global->LDS writes
+    lds_bytes_tile = waves * (tm / cfg.WM + tn / cfg.WN) * kt * elem
+    lds_bytes_tile += (tm + tn) * kt * elem                        # the global->LDS writes
     t_lds = tiles * lds_bytes_tile / (LDS_BYTES_PER_CLK * CLOCK_HZ * min(CU_COUNT, tiles))
-    t_l2 = tiles * (tm + tn) * K * elem / L2_BYTES_PER_S
+    t_l2 = tiles * (tm + tn) * kt * elem / L2_BYTES_PER_S
     t_hbm = (M * K + N * K + M * N) * batch * elem / HBM_BYTES_PER_S
     # a workgroup writes its output tile after its K loop; with one workgroup per CU
     # nothing overlaps that store, which matters when the output dominates (small K)
-    t_out = M * N * batch * elem / HBM_BYTES_PER_S / occ
-    t = max(t_mfma, t_lds, t_l2, t_hbm) + t_out
+    t_out = M * N * batch * (4 * S if S > 1 else elem) / HBM_BYTES_PER_S / occ
+    # split K: the second launch reads the S fp32 partials, writes the output, and costs a launch
+    t_sum = ((S * 4 + elem) * M * N * batch / HBM_BYTES_PER_S + 4e-6) if S > 1 else 0.0
+    t = max(t_mfma, t_lds, t_l2, t_hbm) + t_out + t_sum
     return t * 1e6
 
 

@@ -124,3 +124,24 @@ def test_tile_order_is_a_bijection_when_compiled_for_the_host(tmp_path):
     exe = tmp_path / "order"
     subprocess.run(["gcc", "-O1", "-o", str(exe), str(c)], check=True)
     assert subprocess.run([str(exe)]).returncode == 0
+
+
+def test_k_split_gemm_has_a_partial_and_a_sum_launch():
+    """K split over workgroups: the partial-product launch owns a workspace of
+    batch x splits x M x N fp32 values (placed after the planned intermediates in the
+    arena) and both launches take it as their last argument."""
+    fn = lambda x, w, b: tj.gelu(tj.linear(x, w, b))
+    p = C.lower(tj.trace(fn, [TensorType(s, DType.f32) for s in [(512, 3072), (768, 3072), (768,)]]), "hip")
+    cfg = MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 8)
+    assert hb.config_ok(cfg, DType.f32, p.kernels[0].anchor)
+    src, launches = hb.generate(p, {0: cfg})
+    assert [l.meta["kernel"] for l in launches] == [0, 0]
+    assert launches[0].grid == (12, 8, 8) and launches[0].meta["workspace"] == 8 * 512 * 768 * 4
+    assert launches[1].meta["family"] == "ksplit_sum" and launches[1].grid == (384, 1, 1)
+    ws, arena = hb.workspace_layout(launches, 1000)
+    assert ws == {0: 1024} and arena == 1024 + 8 * 512 * 768 * 4
+    refs = hb.launch_args(launches, [[("in", 0), ("in", 1), ("in", 2), ("out", 0)]], ws)
+    assert all(r[-1] == (hb.rt.ARENA, 1024) for r in refs)
+    hb.compile_source(src, "gfx950")
+    # splits must divide K into whole K steps
+    assert not hb.config_ok(MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 7), DType.f32, p.kernels[0].anchor)

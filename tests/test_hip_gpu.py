@@ -584,8 +584,9 @@ def _run_with_config(fn, args, cfg):
     code = hb.compile_source(src, hb.arch_of(0))
     out = torch.empty(k.outputs[0].shape, device=DEV, dtype=args[0].dtype)
     refs = [[(rt.INPUT, j) for j in range(len(args))] + [(rt.OUTPUT, 0)]]
-    prog = rt.NativeHipProgram(0, code, [launches[0].name], [(launches[0].grid, launches[0].block, 0)], refs, 0,
-                               len(args), 1)
+    ws, arena = hb.workspace_layout(launches, 0)          # split-K GEMMs: partials + a sum launch
+    prog = rt.NativeHipProgram(0, code, [l.name for l in launches], [(l.grid, l.block, 0) for l in launches],
+                               hb.launch_args(launches, refs, ws), arena, len(args), 1)
     prog.run([a.data_ptr() for a in args], [out.data_ptr()], torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     return out
@@ -613,6 +614,49 @@ def test_every_bf16_tile_config_is_exact_on_integer_data(tb):
             assert torch.equal(out, ref), (m, n, kk, tb, cfg)
             tried += 1
         assert tried >= (3 if m > 16 else 1)
+
+
+@pytest.mark.parametrize("case", ["f32_residual", "f32_ragged_gelu", "bf16_batched", "skinny_bias_gelu"])
+def test_k_split_gemm_matches_reference(case):
+    """K split over workgroups: fp32 partial tiles in the arena workspace, summed (in a
+    fixed order) by a second launch that applies the fused epilogue; compared with an
+    fp32 reference, twice (the workspace is reused without clearing)."""
+    from tensorjit.runtime.autotune import MatmulConfig
+
+    torch.manual_seed(0)
+    if case == "f32_residual":
+        x, w, r = torch.randn(512, 3072, device=DEV), 0.02 * torch.randn(768, 3072, device=DEV), torch.randn(512, 768, device=DEV)
+        fn, args = (lambda a, b, c: tj.linear(a, b) + c), [x, w, r]
+        ref, tol = x @ w.t() + r, 1e-5
+        cfgs = [(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 8), (32, 32, 64, 4, 2, 2, 16, 1, 8, 0, 0, 0, 4)]
+    elif case == "f32_ragged_gelu":
+        x, w, b = torch.randn(200, 1024, device=DEV), 0.05 * torch.randn(300, 1024, device=DEV), torch.randn(300, device=DEV)
+        fn, args = (lambda a, bb, c: tj.gelu(tj.linear(a, bb, c))), [x, w, b]
+        ref, tol = torch.nn.functional.gelu(x @ w.t() + b), 1e-5
+        cfgs = [(32, 64, 64, 4, 2, 2, 16, 1, 8, 0, 0, 0, 4), (64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 8)]
+    elif case == "bf16_batched":
+        a = torch.randn(3, 136, 512, device=DEV).bfloat16()
+        b = torch.randn(3, 200, 512, device=DEV).bfloat16()
+        fn, args = (lambda p, q: tj.matmul(p, tj.transpose(q, 1, 2))), [a, b]
+        ref, tol = a.float() @ b.float().transpose(1, 2).contiguous(), 2e-2
+        cfgs = [(64, 64, 64, 4, 2, 2, 16, 1, 8, 0, 0, 0, 4), (128, 128, 32, 4, 2, 2, 32, 1, 8, 0, 0, 0, 2)]
+    else:
+        x, w, b = torch.randn(16, 8192, device=DEV).bfloat16(), (0.02 * torch.randn(4096, 8192, device=DEV)).bfloat16(), \
+            torch.randn(4096, device=DEV).bfloat16()
+        fn, args = (lambda a, bb, c: tj.gelu(tj.linear(a, bb, c))), [x, w, b]
+        ref, tol = torch.nn.functional.gelu(x.float() @ w.float().t() + b.float()), 2e-2
+        cfgs = [(16, 64, 256, 8, 1, 1, 16, 8, 0, 0, 0, 0, 4), (16, 32, 256, 8, 1, 1, 16, 8, 0, 0, 0, 0, 2)]
+    for vals in cfgs:
+        cfg = MatmulConfig(*vals)
+        first = None
+        for _ in range(2):
+            out = _run_with_config(fn, args, cfg).float()
+            err = float(((out - ref).abs() - tol * ref.abs()).max() / ref.abs().max())
+            assert err < tol, (case, vals, err)
+            if first is None:
+                first = out
+            else:
+                assert torch.equal(out, first), (case, vals)      # fixed summation order
 
 
 DIRECT_CFGS = [(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1)]
