@@ -91,10 +91,10 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
     if cfg.INTERLEAVE and (cfg.PINGPONG or (cfg.TK // ki) % 2):
         return False
     if cfg.DIRECT:
-        # direct-to-LDS tiles: 16-bit operands, 128-byte K rows (TK 64), 32x32 MFMAs
-        # with 128-row wave tiles (the LDS swizzle assumes row bases that are
-        # multiples of 32), 8-row DMA blocks per wave and no other schedule
-        ok = (dt in (DType.bf16, DType.f16) and cfg.TK == 64 and cfg.MI == 32 and not cfg.PINGPONG
+        # direct-to-LDS tiles: 16-bit operands, 128-byte K rows (TK 64), 32x32x16 or
+        # 16x16x32 MFMAs with wave tiles whose row bases are multiples of 32 (the LDS
+        # swizzle's period), 8-row DMA blocks per wave and no other schedule
+        ok = (dt in (DType.bf16, DType.f16) and cfg.TK == 64 and cfg.MI in (16, 32) and not cfg.PINGPONG
               and not cfg.INTERLEAVE and cfg.SPLIT_K == 1 and cfg.WM * cfg.WN == cfg.num_warps
               and cfg.TM % (cfg.WM * 32) == 0 and cfg.TN % (cfg.WN * 32) == 0
               and cfg.TM % (8 * cfg.num_warps) == 0 and cfg.TN % (8 * cfg.num_warps) == 0
@@ -378,30 +378,37 @@ def direct_staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx
                                  TMW, TNW, NACC, guard_m, guard_n, idx_t, cfg) -> list[str] | None:
     """Staged epilogue of the direct-to-LDS schedule.  The four K-stage arrays are free
     once every wave has finished its last fragment reads (one barrier); wave w then
-    owns array w and stages its sub-tile through it 32 rows (one MFMA row block) at a
-    time, with no further workgroup barriers: a wave's LDS accesses complete in order.
-    Each pass turns the 32 x 32 MFMA layout into 16-byte runs of output rows, as in
-    the shared staged epilogue.  Returns None where the arrays do not fit a pass."""
+    owns array w and stages its sub-tile through it 32 rows (one 32x32 or two 16x16
+    MFMA row blocks) at a time, with no further workgroup barriers: a wave's LDS
+    accesses complete in order.  Each pass turns the MFMA layout into 16-byte runs of
+    output rows, as in the shared staged epilogue.  Returns None where the arrays do
+    not fit a pass."""
     out_dt = k.outputs[0].dtype
     if cfg.num_warps != 4 or any(o.dtype != out_dt for o in k.outputs):
         return None
+    MI = cfg.MI
     ve = 16 // out_dt.itemsize if N % (16 // out_dt.itemsize) == 0 else 1
-    cols = TNW * 32
+    cols = TNW * MI
     ldc = cols + 4
-    if 32 * ldc * 4 > min(BM, BN) * 128 or cols % ve:
+    if 32 * ldc * 4 > min(BM, BN) * 128 or cols % ve or (TMW * MI) % 32:
         return None
     per_row = cols // ve
     L = ["  __syncthreads();",
          "  float* Cw = (float*)(wave == 0u ? As0 : wave == 1u ? As1 : wave == 2u ? Bs0 : Bs1);"]
-    for x in range(TMW):
-        L.append("#pragma unroll")
-        L.append(f"  for (int y = 0; y < {TNW}; ++y)")
-        L.append("#pragma unroll")
-        L.append(f"  for (int r = 0; r < {NACC}; ++r)")
-        L.append(f"    Cw[((r / 4) * 8 + (lane / 32u) * 4 + (r % 4)) * {ldc}u + y * 32u + lane % 32u] = acc[{x}][y][r];")
+    tiles = 32 // MI                      # MFMA row blocks per 32-row pass
+    for p_ in range(TMW // tiles):
+        for xl in range(tiles):
+            x = p_ * tiles + xl
+            row = ("(r / 4) * 8 + (lane / 32u) * 4 + (r % 4)" if MI == 32
+                   else f"{xl * 16}u + (lane / 16u) * 4 + r")
+            L.append("#pragma unroll")
+            L.append(f"  for (int y = 0; y < {TNW}; ++y)")
+            L.append("#pragma unroll")
+            L.append(f"  for (int r = 0; r < {NACC}; ++r)")
+            L.append(f"    Cw[({row}) * {ldc}u + y * {MI}u + lane % {MI}u] = acc[{x}][y][r];")
         L.append(f"  for (unsigned int c = lane; c < {32 * per_row}u; c += 64u) {{")
         L.append(f"    const unsigned int lr = c / {per_row}u, cc = (c % {per_row}u) * {ve}u;")
-        L.append(f"    const {idx_t} i = m0 + wm * {BM // WM}u + {x * 32}u + lr;")
+        L.append(f"    const {idx_t} i = m0 + wm * {BM // WM}u + {p_ * 32}u + lr;")
         L.append(f"    const {idx_t} j = n0 + wn * {BN // WN}u + cc;")
         conds = ([f"i < {M}u"] if guard_m else []) + ([f"j < {N}u"] if guard_n else [])
         if conds:
@@ -943,9 +950,12 @@ def interleaved_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, lo
     return L
 
 
-# direct-to-LDS load split: (loads of tile kt+2 issued in tile kt's region B, region-A
-# sub-steps of tile kt+1 over which the rest are spread)
-DIRECT_SPLIT = (8, 1)
+# direct-to-LDS load split per MFMA size: (loads of tile kt+2 issued in tile kt's
+# region B, region-A sub-steps of tile kt+1 over which the rest are spread)
+DIRECT_SPLIT = {32: (8, 1), 16: (8, 1)}
+# 32x32 schedule: DMA loads from the first MFMA of a region on, reads in between
+# (True), or the reads first and the loads after them (False)
+DIRECT_EARLY_LOADS = True
 
 
 def _vmcnt_only(n: int) -> str:
@@ -974,13 +984,25 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
     compiler can tell the stage being filled from the stage being read and does not
     wait for the loads in flight before each fragment read.  Tile kt (stage kt & 1):
     region A runs the MFMAs of sub-steps 0 .. KS-2 with the fragment reads of the next
-    sub-steps threaded between them, plus the second half of tile kt+1's loads; a
+    sub-steps placed between them, plus the second part of tile kt+1's loads; a
     barrier (after each wave's wait for its own loads) publishes tile kt+1 and frees
     stage kt & 1; region B runs the last sub-step's MFMAs with the reads of tile
-    kt+1's first fragments and the first half of tile kt+2's loads into the freed
-    stage.  Every load so gets a whole tile of MFMAs to land."""
+    kt+1's first fragments and the first part of tile kt+2's loads into the freed
+    stage.  Every load so gets at least a sub-step of MFMAs to land.
+
+    MFMA shapes: 32x32x16 (four 16-deep sub-steps per tile, 16 MFMAs each, both
+    fragment sets double-buffered) or 16x16x32 (two 32-deep sub-steps, 64 MFMAs each;
+    the A fragment of row tile x is re-read for the next sub-step right after the
+    sub-step's last MFMA on that row, so only B is double-buffered: 96 fragment VGPRs
+    instead of 128).  Each memory instruction has a fixed slot after one MFMA: DMA
+    loads one per 64 MFMA cycles of a wave (about what the texture unit passes for
+    four waves at ~16 cycles per 1 KiB load), fragment reads in the slots between."""
     nw = cfg.num_warps
-    KS = 4                                  # 64-deep tile, 16 per 32x32x16 MFMA
+    MI = cfg.MI
+    KI = 16 if MI == 32 else 32               # K per MFMA
+    KS = 64 // KI                             # sub-steps per 64-deep tile
+    NACC = MI * MI // 64
+    dsp = 64 // MI                            # MFMAs per 64 cycles: 32x32x16 takes 32, 16x16x32 16
     # Barrier that publishes a stage filled by DMA: each wave first waits for its own
     # DMA loads (vmcnt 0; expcnt and lgkmcnt left at their maxima).  A workgroup-scope
     # fence does not cover loads that write LDS, and the compiler's own vmcnt wait is
@@ -995,19 +1017,30 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
          f"  __shared__ __attribute__((aligned(1024))) char Bs1[{BN * 128}];",
          "  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave);",
          "  const unsigned int drow = lane >> 3;",
-         f"  tj_f32x16 acc[{TMW}][{TNW}];",
+         f"  tj_f32x{NACC} acc[{TMW}][{TNW}];",
          "#pragma unroll",
          f"  for (int x = 0; x < {TMW}; ++x)",
          "#pragma unroll",
-         f"    for (int y = 0; y < {TNW}; ++y) acc[x][y] = (tj_f32x16)(0.0f);",
-         # fragment addresses: row (wave base + lane % 32), logical chunk 2 ks + lane / 32
-         "  const unsigned int fr = lane & 31u, fh = lane >> 5;",
+         f"    for (int y = 0; y < {TNW}; ++y) acc[x][y] = (tj_f32x{NACC})(0.0f);",
+         # fragment addresses: row (wave base + MI x + lane % MI), logical chunk
+         # (KI / 8) ks + lane / MI of the 64-deep tile
+         f"  const unsigned int fr = lane & {MI - 1}u, fh = lane >> {MI.bit_length() - 1};",
          "  const unsigned int fsw = (fr & 7u) ^ ((fr >> 3) & 3u);",
          f"  const unsigned int arow = (wm * {BM // cfg.WM}u + fr) * 128u;",
-         f"  const unsigned int brow = (wn * {BN // cfg.WN}u + fr) * 128u;",
-         "  unsigned int fofs[4];",
-         "#pragma unroll",
-         "  for (int ks = 0; ks < 4; ++ks) fofs[ks] = ((2u * ks + fh) ^ fsw) * 16u;"]
+         f"  const unsigned int brow = (wn * {BN // cfg.WN}u + fr) * 128u;"]
+    if MI == 32:
+        # row tiles start at multiples of 32: f(r) is that of the row within the tile
+        nofs = KS
+        L.append(f"  unsigned int fofs[{nofs}];")
+        L += [f"  fofs[{ks}] = (({2 * ks}u + fh) ^ fsw) * 16u;" for ks in range(KS)]
+        fofs = lambda ks, t: ks                                          # noqa: E731
+    else:
+        # a 16-row tile at an odd multiple of 16 has bit 1 of (r >> 3) & 3 set
+        nofs = 2 * KS
+        L.append(f"  unsigned int fofs[{nofs}];")
+        L += [f"  fofs[{2 * ks + par}] = (({4 * ks}u + fh) ^ fsw ^ {2 * par}u) * 16u;"
+              for ks in range(KS) for par in range(2)]
+        fofs = lambda ks, t: 2 * ks + (t & 1)                            # noqa: E731
 
     # Loads go through buffer resources (buffer_load_dwordx4 ... lds): a 32-bit lane
     # offset that does not change over K (row and swizzled chunk), the tile's K position
@@ -1023,89 +1056,95 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
             q = f"({i * nw}u + wv)"
             L.append(f"  vo{op}[{i}] = (({rows} + {q} * 8u + drow) * {K}u + ((lane & 7u) ^ drow ^ ({q} & 3u)) * 8u) * 2u;")
 
-    def dma(kt: str, stage: int) -> list[list[str]]:
-        """The DMA loads of tile ``kt`` into ``stage``, one statement block per load."""
-        blocks = []
+    def dma(kt: str, stage: int) -> list[str]:
+        """The DMA loads of tile ``kt`` into ``stage``, one statement per load."""
+        out = []
         for op, cnt in (("A", a_cnt), ("B", b_cnt)):
             for i in range(cnt):
                 q = f"({i * nw}u + wv)"
-                blocks.append([f"__builtin_amdgcn_raw_ptr_buffer_load_lds(rs{op}, (__attribute__((address_space(3))) void*)"
-                               f"({op}s{stage} + {q} * 1024u), 16, vo{op}[{i}], (int)(({kt}) * 128u), 0, 0);"])
-        return blocks
-
-    def frag_reads(buf: int, stage: int, ks: int) -> list[str]:
-        """Fragment reads in the order the MFMAs consume them (row-major over (x, y):
-        fa[0], fb[0..], fa[1], ...), so each MFMA waits only for its own operands."""
-        a_rd = [f"fa[{buf}][{x}] = *(const {opvec}*)(As{stage} + arow + fofs[{ks}] + {x * 32 * 128}u);"
-                for x in range(TMW)]
-        b_rd = [f"fb[{buf}][{y}] = *(const {opvec}*)(Bs{stage} + brow + fofs[{ks}] + {y * 32 * 128}u);"
-                for y in range(TNW)]
-        return [a_rd[0]] + b_rd + a_rd[1:]
-
-    def mfmas(buf: int) -> list[str]:
-        return [f"acc[{x}][{y}] = {builtin}(fa[{buf}][{x}], fb[{buf}][{y}], acc[{x}][{y}], 0, 0, 0);"
-                for x in range(TMW) for y in range(TNW)]
-
-    def pattern(n_mfma: int, mem: list[int]) -> list[str]:
-        out = []
-        per = -(-len(mem) // max(n_mfma, 1)) if mem else 0
-        for i in range(n_mfma):
-            out.append(f"__builtin_amdgcn_sched_group_barrier({SG_MFMA}, 1, 0);")
-            for m in mem[i * per:(i + 1) * per]:
-                out.append(f"__builtin_amdgcn_sched_group_barrier({m}, 1, 0);")
+                out.append(f"__builtin_amdgcn_raw_ptr_buffer_load_lds(rs{op}, (__attribute__((address_space(3))) void*)"
+                           f"({op}s{stage} + {q} * 1024u), 16, vo{op}[{i}], (int)(({kt}) * 128u), 0, 0);")
         return out
 
+    def fa_ref(buf: int, x: int) -> str:
+        return f"fa[{buf}][{x}]" if MI == 32 else f"fa[{x}]"
+
+    def frag_reads(buf: int, stage: int, ks: int) -> list[tuple[int, str]]:
+        """(slot, statement) of the fragment reads of sub-step ``ks`` from ``stage``
+        into set ``buf``.  32x32: in consumption order (fa[0], fb[0..], fa[1], ...),
+        one per slot from ``rd0`` on.  16x16: B fragments early (every 4th MFMA of the
+        first half), A fragment of row tile x right after the last MFMA of row x."""
+        a_rd = [f"{fa_ref(buf, x)} = *(const {opvec}*)(As{stage} + arow + fofs[{fofs(ks, x)}] + {x * MI * 128}u);"
+                for x in range(TMW)]
+        b_rd = [f"fb[{buf}][{y}] = *(const {opvec}*)(Bs{stage} + brow + fofs[{fofs(ks, y)}] + {y * MI * 128}u);"
+                for y in range(TNW)]
+        if MI == 32:
+            return list(enumerate([a_rd[0]] + b_rd + a_rd[1:]))
+        return [(4 * y + 2, r) for y, r in enumerate(b_rd)] + [(x * TNW + TNW - 1, r) for x, r in enumerate(a_rd)]
+
+    def mfmas(buf: int) -> list[str]:
+        return [f"acc[{x}][{y}] = {builtin}({fa_ref(buf, x)}, fb[{buf}][{y}], acc[{x}][{y}], 0, 0, 0);"
+                for x in range(TMW) for y in range(TNW)]
+
+    def region(buf: int, reads: list[tuple[int, str]], loads: list[str]) -> list[str]:
+        """One sub-step: its MFMAs with the memory statements placed after their
+        slots (DMA loads from slot 0, one per ``dsp`` MFMAs; reads as given; with
+        loads present the 32x32 reads move to the odd slots), then the matching
+        sched_group_barrier sequence."""
+        early = DIRECT_EARLY_LOADS or MI == 16
+        slots: dict[int, list[tuple[int, str]]] = {}
+        for i, ld in enumerate(loads):
+            s = i * dsp if early else len(reads) + i
+            slots.setdefault(min(s, nmm - 1), []).append((SG_VMEM_READ, ld))
+        for s, rd in reads:
+            if MI == 32 and loads and early:
+                s = 2 * s + 1
+            slots.setdefault(min(s, nmm - 1), []).append((SG_DS_READ, rd))
+        code, sched = [], []
+        for i, mf in enumerate(mfmas(buf)):
+            code.append(mf)
+            sched.append(f"__builtin_amdgcn_sched_group_barrier({SG_MFMA}, 1, 0);")
+            for mask, stmt in slots.get(i, []):
+                code.append(stmt)
+                sched.append(f"__builtin_amdgcn_sched_group_barrier({mask}, 1, 0);")
+        return code + sched + ["__builtin_amdgcn_sched_barrier(0);"]
+
     n_batch = a_cnt + b_cnt
-    n_b = min(DIRECT_SPLIT[0], n_batch)          # loads issued in region B
-    a_steps = max(1, min(DIRECT_SPLIT[1], KS - 1))  # region-A sub-steps taking the rest
+    split = DIRECT_SPLIT[MI]
+    n_b = min(split[0], n_batch)                  # loads issued in region B
+    a_steps = max(1, min(split[1], KS - 1))      # region-A sub-steps taking the rest
 
     def tile(kt: str, stage: int, carry: bool, do_load: bool, last: bool, ind: str) -> list[str]:
         """Tile kt from LDS stage ``stage``.  The loads of tile kt+2 (into this stage,
         released by this tile's barrier) start in region B; ``carry``: the rest of tile
         kt+1's loads (begun in the previous tile's region B) go into region A here,
-        still ahead of the barrier that publishes tile kt+1.  Splitting a tile's loads
-        over both regions keeps the texture unit (about 16 cycles per 1 KiB load, four
-        waves per CU) from backing up into MFMA issue.  ``last``: no tile follows."""
+        still ahead of the barrier that publishes tile kt+1.  ``last``: no tile follows."""
         out = []
         rest = dma(f"({kt}) + 1", 1 - stage)[n_b:] if carry else []
         # region A: sub-steps 0 .. KS-2 with the fragment reads of the next sub-steps
         for ks in range(KS - 1):
             mine = rest[len(rest) * ks // a_steps:len(rest) * (ks + 1) // a_steps] if ks < a_steps else []
-            for blk in mine:
-                out += blk
-            out += mfmas(ks % 2)
-            out += frag_reads((ks + 1) % 2, stage, ks + 1)
-            out += pattern(nmm, [SG_DS_READ] * (TMW + TNW) + [SG_VMEM_READ] * len(mine))
-            out.append("__builtin_amdgcn_sched_barrier(0);")
+            out += region(ks % 2, frag_reads((ks + 1) % 2, stage, ks + 1), mine)
         if not last:
             out += publish + ["__builtin_amdgcn_sched_barrier(0);"]
         # region B: last sub-step, with the first fragments of tile kt+1 and the first
         # loads of tile kt+2
-        out += mfmas((KS - 1) % 2)
-        mem = []
-        if not last:
-            out += frag_reads(0, 1 - stage, 0)
-            mem += [SG_DS_READ] * (TMW + TNW)
-        if do_load:
-            blocks = dma(f"({kt}) + 2", stage)[:n_b]
-            for blk in blocks:
-                out += blk
-            mem += [SG_VMEM_READ] * len(blocks)
-        out += pattern(nmm, mem)
-        out.append("__builtin_amdgcn_sched_barrier(0);")
+        reads = frag_reads(0, 1 - stage, 0) if not last else []
+        loads = dma(f"({kt}) + 2", stage)[:n_b] if do_load else []
+        out += region((KS - 1) % 2, reads, loads)
         return [ind + x for x in out]
 
     # prologue: tiles 0 and 1 in flight, wait for tile 0 only (the 2nd batch may
     # stay outstanding: vmcnt <= its load count)
-    L += ["  " + x for blk in dma("0", 0) for x in blk]
+    L += ["  " + x for x in dma("0", 0)]
     if KT > 1:
-        L += ["  " + x for blk in dma("1", 1) for x in blk]
+        L += ["  " + x for x in dma("1", 1)]
         L.append(f"  __builtin_amdgcn_s_waitcnt({_vmcnt_only(n_batch)});")
         L.append("  __syncthreads();")
     else:
         L += ["  " + x for x in publish]
-    L.append(f"  {opvec} fa[2][{TMW}], fb[2][{TNW}];")
-    L += ["  " + x for x in frag_reads(0, 0, 0)]
+    L.append(f"  {opvec} fa[2][{TMW}], fb[2][{TNW}];" if MI == 32 else f"  {opvec} fa[{TMW}], fb[2][{TNW}];")
+    L += ["  " + r for _, r in frag_reads(0, 0, 0)]
     # tile 0 (nothing to carry: the prologue loaded tile 1 whole), then (odd, even)
     # pairs of tiles that all carry and load, then the tail
     L.append("  {  // K tile 0")

@@ -76,6 +76,8 @@ class MatmulConfig:
 
 # bf16 / fp16 candidates (MFMA 32x32x16 or 16x16x32)
 HIP_CANDIDATES: list[MatmulConfig] = [
+    MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1),
+    MatmulConfig(256, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1),
     MatmulConfig(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
     MatmulConfig(256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
     MatmulConfig(256, 256, 64, 8, 2, 4, 32, 1, 8, 3),
@@ -143,10 +145,11 @@ def _skinny_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: in
 
 def _sched_factor(cfg: MatmulConfig) -> float:
     """Relative MFMA-phase cost of a loop schedule, from bf16 8192^3 runs on MI355X
-    (direct-to-LDS loads 3-7% ahead of ping-pong with K-split tiles; plain
-    double-buffered loop ~9% behind it)."""
+    (direct-to-LDS loads 3-7% ahead of ping-pong with K-split tiles, and another ~10%
+    with 16x16x32 MFMAs, which hold a higher clock on random data than 32x32x16;
+    plain double-buffered loop ~9% behind ping-pong)."""
     if cfg.DIRECT:
-        return 0.95
+        return 0.86 if cfg.MI == 16 else 0.95
     if cfg.INTERLEAVE:
         return 1.15
     return {3: 1.0, 2: 1.04, 1: 1.05}.get(cfg.PINGPONG, 1.09)
@@ -165,6 +168,8 @@ def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) 
         return math.inf
     acc = tm * tn / (64 * waves) * (cfg.SPLIT_K if cfg.SPLIT_K > 1 else 1)
     frags = 2 * (tm / cfg.WM + tn / cfg.WN) / cfg.MI * (4 if elem == 2 else 1)  # double-buffered
+    if cfg.DIRECT and cfg.MI == 16:
+        frags -= tm / cfg.WM / cfg.MI * 4                                   # A re-read in place
     staging = 0 if cfg.DIRECT else (tm + tn) * tk * elem / (64 * waves * 4)  # staged K step per lane, 4 B per VGPR
     regs = acc + frags + staging + 32
     if regs > 512:

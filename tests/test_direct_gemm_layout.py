@@ -6,8 +6,9 @@ lane fetches) and reads MFMA fragments with a different set of expressions.  The
 tests evaluate both sets of expressions exactly as generated, for every wave and
 lane, and check that (a) the DMA fills each LDS slot of a stage exactly once, (b)
 every fragment read returns the (row, k-chunk) the 32x32x16 MFMA expects in that
-lane, and (c) the 16 lanes that share an LDS access cycle hit 16 distinct 16-byte
-bank groups.  The wait-count immediate is pinned against the assembler's own
+lane (32x32x16: row l % 32, chunk 2 ks + l / 32; 16x16x32: row l % 16, chunk
+4 ks + l / 16), and (c) the 16 lanes that share an LDS access cycle hit 16 distinct
+16-byte bank groups.  The wait-count immediate is pinned against the assembler's own
 decoding of a compiled kernel."""
 import re
 import shutil
@@ -24,6 +25,10 @@ from tensorjit.runtime.autotune import MatmulConfig
 
 DIRECT = MatmulConfig(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1)
 DIRECT_N128 = MatmulConfig(256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1)
+DIRECT16 = MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1)
+DIRECT16_N128 = MatmulConfig(256, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1)
+ALL_DIRECT = [DIRECT, DIRECT_N128, DIRECT16, DIRECT16_N128]
+DIRECT_IDS = ["256x256", "256x128", "256x256_mi16", "256x128_mi16"]
 
 
 def _source(cfg, M=256, N=256, K=64, epi="plain"):
@@ -42,11 +47,14 @@ def _c_eval(expr: str, env: dict) -> int:
     return int(eval(py, {}, dict(env))) & 0xFFFFFFFF
 
 
-@pytest.mark.parametrize("cfg", [DIRECT, DIRECT_N128], ids=["256x256", "256x128"])
+@pytest.mark.parametrize("cfg", ALL_DIRECT, ids=DIRECT_IDS)
 def test_dma_placement_and_fragment_reads_agree(cfg):
     K = 64
     src, launches = _source(cfg, N=cfg.TN, K=K)
-    nw, WM, WN = cfg.num_warps, cfg.WM, cfg.WN
+    nw, WM, WN, MI = cfg.num_warps, cfg.WM, cfg.WN, cfg.MI
+    kc = 2 if MI == 32 else 4                     # 16-byte chunks of K per MFMA
+    fofs = {int(i): e for i, e in re.findall(r"  fofs\[(\d+)\] = (.*);\n", src)}
+    assert sorted(fofs) == list(range(4))
     for op, rows, wdim, rowdim in (("A", cfg.TM, WM, cfg.TM // WM), ("B", cfg.TN, WN, cfg.TN // WN)):
         vo = dict(re.findall(rf"  vo{op}\[(\d+)\] = (.*);\n", src))
         dst = re.findall(rf"raw_ptr_buffer_load_lds\(rs{op}, \(__attribute__\(\(address_space\(3\)\)\) void\*\)"
@@ -64,40 +72,50 @@ def test_dma_placement_and_fragment_reads_agree(cfg):
                     assert slot not in slots, (op, wv, lane, i)
                     slots[slot] = (g_row, g_col // 8)
         assert sorted(slots) == list(range(rows * K * 2 // 16)), op      # every 16-byte slot filled once
-        # fragment reads: lane l of wave (wm, wn), tile x / y, sub-step ks wants row base + 32 x + l % 32,
-        # 16-byte chunk 2 ks + l / 32 (8 bf16 of k per lane, 16 per MFMA)
+        # fragment reads: lane l of wave (wm, wn), tile t, sub-step ks wants row base + MI t + l % MI,
+        # 16-byte chunk kc ks + l / MI (8 bf16 of k per lane)
         fsw = re.search(r"const unsigned int fsw = (.*);", src).group(1)
         base = re.search(rf"const unsigned int {'arow' if op == 'A' else 'brow'} = (.*);", src).group(1)
-        fofs = re.search(r"fofs\[ks\] = (.*);", src).group(1)
-        reads = re.findall(rf"f{'a' if op == 'A' else 'b'}\[\d\]\[(\d)\] = \*\(const tj_bf16x8\*\)\({op}s0 \+ "
+        reads = re.findall(rf"f{'a' if op == 'A' else 'b'}(?:\[\d\])?\[(\d)\] = \*\(const tj_bf16x8\*\)\({op}s0 \+ "
                            rf"{'arow' if op == 'A' else 'brow'} \+ fofs\[(\d)\] \+ (\d+)u\);", src)
-        assert reads, op
+        # every (tile, sub-step) pair is read, each with its own offset register
+        assert len(set(reads)) == (rowdim // MI) * (64 // (8 * kc)), (op, sorted(set(reads)))
+
+        def lane_env(lane, w):
+            env = {"fr": lane & (MI - 1), "fh": lane // MI, "wm": w, "wn": w}
+            env["fsw"] = _c_eval(fsw, env)
+            return env
+
+        def sub_step(t, f):
+            if MI == 32:
+                return f
+            assert f % 2 == t % 2, (t, f)            # odd 16-row tiles take the odd offsets
+            return f // 2
+
         for w in range(wdim):
             for lane in range(64):
-                env = {"fr": lane & 31, "fh": lane >> 5, "wm": w, "wn": w}
-                env["fsw"] = _c_eval(fsw, env)
-                for t, ks, xoff in set(reads):
-                    env["ks"] = int(ks)
-                    addr = _c_eval(base, env) + _c_eval(fofs, env) + int(xoff)
-                    want = (w * rowdim + int(t) * 32 + (lane & 31), 2 * int(ks) + (lane >> 5))
-                    assert slots[addr // 16] == want, (op, w, lane, t, ks)
+                env = lane_env(lane, w)
+                for t, f, xoff in set(reads):
+                    t, f = int(t), int(f)
+                    addr = _c_eval(base, env) + _c_eval(fofs[f], env) + int(xoff)
+                    want = (w * rowdim + t * MI + (lane & (MI - 1)), kc * sub_step(t, f) + lane // MI)
+                    assert slots[addr // 16] == want, (op, w, lane, t, f)
         # bank groups: lanes 16 g .. 16 g + 15 of one read touch 16 distinct 16-byte groups of a 256-byte row
         for w in range(wdim):
-            for t, ks, xoff in set(reads):
+            for t, f, xoff in set(reads):
                 for g in range(4):
                     grp = []
                     for lane in range(16 * g, 16 * g + 16):
-                        env = {"fr": lane & 31, "fh": lane >> 5, "wm": w, "wn": w, "ks": int(ks)}
-                        env["fsw"] = _c_eval(fsw, env)
-                        grp.append(((_c_eval(base, env) + _c_eval(fofs, env) + int(xoff)) // 16) % 16)
-                    assert len(set(grp)) == 16, (op, w, t, ks, g, grp)
+                        env = lane_env(lane, w)
+                        grp.append(((_c_eval(base, env) + _c_eval(fofs[int(f)], env) + int(xoff)) // 16) % 16)
+                    assert len(set(grp)) == 16, (op, w, t, f, g, grp)
 
 
 @pytest.mark.parametrize("epi", ["plain", "residual", "bias_gelu"])
 @pytest.mark.parametrize("shape", [(256, 256, 64), (300, 520, 192), (1024, 768, 4096)])
 def test_direct_kernels_compile_for_gfx950(epi, shape, tj_env):
     M, N, K = shape
-    for cfg in (DIRECT, DIRECT_N128):
+    for cfg in ALL_DIRECT:
         src, launches = _source(cfg, M, N, K, epi)
         assert launches[0].meta["config"]["DIRECT"] == 1
         assert launches[0].meta.get("epilogue") == "lds-staged"

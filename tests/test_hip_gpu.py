@@ -659,7 +659,8 @@ def test_k_split_gemm_matches_reference(case):
                 assert torch.equal(out, first), (case, vals)      # fixed summation order
 
 
-DIRECT_CFGS = [(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1)]
+DIRECT_CFGS = [(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
+               (256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
