@@ -103,6 +103,10 @@ HIP_CANDIDATES: list[MatmulConfig] = [
     MatmulConfig(64, 64, 32, 4, 2, 2, 16),
     MatmulConfig(32, 64, 64, 4, 2, 2, 16),
     # skinny (M <= 16 / 32): one MI x MI tile per workgroup, K split over its waves
+    MatmulConfig(16, 32, 64, 4, 1, 1, 16, 4, 0),
+    MatmulConfig(16, 32, 128, 4, 1, 1, 16, 4, 0),
+    MatmulConfig(16, 32, 128, 2, 1, 1, 16, 2, 0),
+    MatmulConfig(32, 32, 64, 4, 1, 1, 32, 4, 0),
     MatmulConfig(16, 32, 256, 8, 1, 1, 16, 8, 0),
     MatmulConfig(16, 64, 256, 8, 1, 1, 16, 8, 0),
     MatmulConfig(16, 32, 128, 16, 1, 1, 16, 16, 0),
@@ -133,14 +137,19 @@ HIP_F32_CANDIDATES: list[MatmulConfig] = [
 
 
 def _skinny_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) -> float:
-    """Streaming kernel: the B panel once from HBM; needs enough waves in flight."""
+    """Streaming kernel: the B panel once from HBM, A re-read (from L2) by every
+    workgroup.  Measured on MI355X for 16 x 8192 x 8192 (TN 32, one workgroup per CU):
+    4 waves per workgroup stream B at 5.5 TB/s whatever the unroll depth (2-16 MFMA
+    steps ahead), 2 waves at 5.3, 8 waves at 4.9, 16 at 3.9; fewer workgroups than
+    CUs leave CUs idle (TN 64: 3.6 TB/s)."""
     if M > cfg.TM or elem != 2:
         return math.inf
     t_hbm = (M * K + N * K + M * N) * batch * elem / HBM_BYTES_PER_S
-    waves = -(-N // cfg.TN) * batch * cfg.SPLIT_K
-    fill = min(1.0, waves / (CU_COUNT * 8.0))           # ~8 streaming waves per CU saturate HBM
+    wgs = -(-N // cfg.TN) * batch
+    fill = min(1.0, wgs / CU_COUNT)
+    per_wave = {4: 1.0, 2: 1.04, 8: 1.13, 16: 1.4}.get(cfg.SPLIT_K, 1.5)
     a_reads = 1.0 + cfg.TM / cfg.TN * 0.5                # A panel re-read per TN columns (from L2)
-    return t_hbm / max(fill, 1e-3) * a_reads * 1e6
+    return t_hbm / max(fill, 1e-3) * per_wave * a_reads * 1e6
 
 
 def _sched_factor(cfg: MatmulConfig) -> float:
