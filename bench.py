@@ -118,7 +118,21 @@ def c2_inputs(torch, dt, dev):
     return [t.to(dt) for t in (x, a, b, c)]
 
 
-def timed_steps(torch, fn, args, steps, warmup):
+def ramp(torch, fn, args, seconds):
+    """Untimed calls for at least ``seconds`` of wall time: a GPU left idle while the
+    process starts can take tens of milliseconds to reach its clocks, which a fixed
+    count of warmup steps of a ~0.1 ms kernel does not cover."""
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(8):
+            fn(*args)
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return
+
+
+def timed_steps(torch, fn, args, steps, warmup, ramp_s=0.1):
+    ramp(torch, fn, args, ramp_s)
     for _ in range(warmup):
         fn(*args)
     torch.cuda.synchronize()
@@ -478,7 +492,7 @@ def main() -> int:
     cp = f.compiled(*args)
     assert cp.num_kernels == 1 and cp.backend == "hip"
     torch.cuda.synchronize()
-    ms_step = timed_steps(torch, f, args, a.steps, a.warmup)
+    ms_step = timed_steps(torch, f, args, a.steps, a.warmup, ramp_s=0.5)
     kms = kernel_ms(f, args, iters=max(20, a.steps))
     value = nbytes / (ms_step / 1e3) / 1e9
     achieved = nbytes / (kms / 1e3) / 1e9
