@@ -952,7 +952,7 @@ def interleaved_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, lo
 
 # direct-to-LDS load split per MFMA size: (loads of tile kt+2 issued in tile kt's
 # region B, region-A sub-steps of tile kt+1 over which the rest are spread)
-DIRECT_SPLIT = {32: (8, 1), 16: (8, 1)}
+DIRECT_SPLIT = {32: (8, 1), 16: (12, 1)}
 # 32x32 schedule: DMA loads from the first MFMA of a region on, reads in between
 # (True), or the reads first and the loads after them (False)
 DIRECT_EARLY_LOADS = True
@@ -1035,10 +1035,16 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
         L += [f"  fofs[{ks}] = (({2 * ks}u + fh) ^ fsw) * 16u;" for ks in range(KS)]
         fofs = lambda ks, t: ks                                          # noqa: E731
     else:
-        # a 16-row tile at an odd multiple of 16 has bit 1 of (r >> 3) & 3 set
+        # a 16-row tile at an odd multiple of 16 has bit 1 of (r >> 3) & 3 set.  K-group
+        # g of a sub-step reads chunk 4 ks + sigma(g), sigma swapping g's two bits (A and
+        # B alike, so each MFMA still pairs equal k): the LDS serves a 16-byte read to
+        # lanes 8j .. 8j+7 together with lanes 32+8j .. 32+8j+7, which hold k-groups g and
+        # g+2 of the same rows; chunks c and c+2 would put row r and row r^2 on one bank
+        # group (every read 2-way conflicted, measured), chunks an odd XOR apart do not
         nofs = 2 * KS
         L.append(f"  unsigned int fofs[{nofs}];")
-        L += [f"  fofs[{2 * ks + par}] = (({4 * ks}u + fh) ^ fsw ^ {2 * par}u) * 16u;"
+        L.append("  const unsigned int fg = ((fh & 1u) << 1) | (fh >> 1);")
+        L += [f"  fofs[{2 * ks + par}] = (({4 * ks}u + fg) ^ fsw ^ {2 * par}u) * 16u;"
               for ks in range(KS) for par in range(2)]
         fofs = lambda ks, t: 2 * ks + (t & 1)                            # noqa: E731
 
