@@ -509,7 +509,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
             out.append("  }")
         return out
 
-    def pp_iteration(jj: str, par: int) -> list[str]:
+    def pp_iteration(jj: str, par: int, has_next: bool = True) -> list[str]:
         """One block for one wave group, as two phases separated by workgroup barriers.
         Phase A: softmax of S(j) with the MFMAs of S(j+1) (K(j+1) in stage (j+1)%3).
         Phase B: O += P(j) V(j) (stage j%3); this group's halves of K(j+3) and V(j+1) go
@@ -517,11 +517,12 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         opposite phase meanwhile.  With group 1 one phase behind, a K block is written
         (phases 2j+1 and 2j+2) two phases before its first read (2j+4) and a V block
         (same phases) one phase before (2j+3); the stages they overwrite were last read
-        in phase 2j-1 (K) and 2j-2 (V)."""
+        in phase 2j-1 (K) and 2j-2 (V).  ``has_next``: S(j+1) exists (the last block
+        skips it; the barriers stay, so the groups keep their phase offset)."""
         sc, sn = ("sA", "sB") if par == 0 else ("sB", "sA")
         out = block_max(sc, None)
-        # S(j+1) unconditionally: past the last block it reads a stale stage, unused
-        out += scores(sn, f"(({jj}) + 1u) % 3u")
+        if has_next:
+            out += scores(sn, f"(({jj}) + 1u) % 3u")
         out += probs(sc)
         out += ["__syncthreads();"]
         out += pv(f"({jj}) % 3u")
@@ -542,16 +543,17 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         out += ["  " + x for x in scores("sA", 0)]
         out += ["  " + x for x in half_load("k", "3u") + half_load("v", "1u")]
         out.append("  if (gq == 1u) __syncthreads();")
-        npair = KB // 2
+        # pairs of blocks that all have a next block, then the last one or two peeled
+        npair = (KB - 1) // 2
         if npair:
             out.append(f"  for (unsigned int jj = 0; jj < {2 * npair}u; jj += 2u) {{")
             out += ["    {"] + ["      " + x for x in pp_iteration("jj", 0)] + ["    }"]
             out += ["    {"] + ["      const unsigned int jj1 = jj + 1u;"] + \
                    ["      " + x.replace("(int)jj *", "(int)jj1 *") for x in pp_iteration("jj1", 1)] + ["    }"]
             out.append("  }")
-        if KB % 2:
-            out.append(f"  {{  const unsigned int jj = {KB - 1}u;")
-            out += ["    " + x for x in pp_iteration("jj", (KB - 1) % 2)]
+        for j in range(2 * npair, KB):
+            out.append(f"  {{  const unsigned int jj = {j}u;")
+            out += ["    " + x for x in pp_iteration("jj", j % 2, j + 1 < KB)]
             out.append("  }")
         out.append("  if (gq == 0u) __syncthreads();")
         return out

@@ -244,8 +244,12 @@ ATTN = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)
 @pytest.mark.parametrize("shapes", [[(2, 4, 128, 64)] * 3, [(1, 100, 32), (1, 75, 32), (1, 75, 64)],
                                     [(1, 2, 300, 128), (1, 2, 1000, 128), (1, 2, 1000, 128)],
                                     [(1, 2, 600, 64), (1, 2, 1000, 64), (1, 2, 1000, 128)],
-                                    [(2, 8, 300, 64), (2, 8, 200, 64), (2, 8, 200, 64)]],
-                         ids=["even", "ragged_dv64", "multi_block_ragged", "eight_waves_ragged", "xcd_grouped_heads"])
+                                    [(2, 8, 300, 64), (2, 8, 200, 64), (2, 8, 200, 64)],
+                                    [(1, 2, 512, 64), (1, 2, 900, 64), (1, 2, 900, 64)],
+                                    [(1, 2, 512, 64), (1, 2, 128, 64), (1, 2, 128, 64)],
+                                    [(1, 2, 512, 64), (1, 2, 40, 64), (1, 2, 40, 64)]],
+                         ids=["even", "ragged_dv64", "multi_block_ragged", "eight_waves_ragged", "xcd_grouped_heads",
+                              "eight_waves_odd_blocks", "eight_waves_two_blocks", "eight_waves_one_ragged_block"])
 def test_fused_attention_vs_oracle_and_unfused_plan(shapes, dt, monkeypatch):
     """The flash kernel against the fp32 oracle (which runs the reference plan:
     materialised scores, softmax row kernel, PV product) and against this backend's
