@@ -587,7 +587,11 @@ def _run_with_config(fn, args, cfg):
     src, launches = hb.generate(p, {0: cfg})
     code = hb.compile_source(src, hb.arch_of(0))
     out = torch.empty(k.outputs[0].shape, device=DEV, dtype=args[0].dtype)
-    refs = [[(rt.INPUT, j) for j in range(len(args))] + [(rt.OUTPUT, 0)]]
+    # the kernel's parameters follow its own input order, not the traced function's
+    gin = {id(n): j for j, n in enumerate(p.graph.inputs)}
+    order = [gin[id(p.resolve(n))] for n in k.inputs]
+    assert [tuple(n.shape) for n in k.inputs] == [tuple(args[j].shape) for j in order]
+    refs = [[(rt.INPUT, j) for j in order] + [(rt.OUTPUT, 0)]]
     ws, arena = hb.workspace_layout(launches, 0)          # split-K GEMMs: partials + a sum launch
     prog = rt.NativeHipProgram(0, code, [l.name for l in launches], [(l.grid, l.block, 0) for l in launches],
                                hb.launch_args(launches, refs, ws), arena, len(args), 1)
