@@ -953,9 +953,6 @@ def interleaved_loop_lines(cfg, KT, KS, BK, TMW, TNW, MI, KI, opvec, builtin, lo
 # direct-to-LDS load split per MFMA size: (loads of tile kt+2 issued in tile kt's
 # region B, region-A sub-steps of tile kt+1 over which the rest are spread)
 DIRECT_SPLIT = {32: (8, 1), 16: (12, 1)}
-# 32x32 schedule: DMA loads from the first MFMA of a region on, reads in between
-# (True), or the reads first and the loads after them (False)
-DIRECT_EARLY_LOADS = True
 
 
 def _vmcnt_only(n: int) -> str:
@@ -1097,13 +1094,11 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
         slots (DMA loads from slot 0, one per ``dsp`` MFMAs; reads as given; with
         loads present the 32x32 reads move to the odd slots), then the matching
         sched_group_barrier sequence."""
-        early = DIRECT_EARLY_LOADS or MI == 16
         slots: dict[int, list[tuple[int, str]]] = {}
         for i, ld in enumerate(loads):
-            s = i * dsp if early else len(reads) + i
-            slots.setdefault(min(s, nmm - 1), []).append((SG_VMEM_READ, ld))
+            slots.setdefault(min(i * dsp, nmm - 1), []).append((SG_VMEM_READ, ld))
         for s, rd in reads:
-            if MI == 32 and loads and early:
+            if MI == 32 and loads:
                 s = 2 * s + 1
             slots.setdefault(min(s, nmm - 1), []).append((SG_DS_READ, rd))
         code, sched = [], []
