@@ -1034,10 +1034,10 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
     else:
         # a 16-row tile at an odd multiple of 16 has bit 1 of (r >> 3) & 3 set.  K-group
         # g of a sub-step reads chunk 4 ks + sigma(g), sigma swapping g's two bits (A and
-        # B alike, so each MFMA still pairs equal k): the LDS serves a 16-byte read to
-        # lanes 8j .. 8j+7 together with lanes 32+8j .. 32+8j+7, which hold k-groups g and
-        # g+2 of the same rows; chunks c and c+2 would put row r and row r^2 on one bank
-        # group (every read 2-way conflicted, measured), chunks an odd XOR apart do not
+        # B alike, so each MFMA still pairs equal k): the LDS serves a 16-byte read 32
+        # lanes at a time over 512 bytes of banks, and lanes 0-15 / 16-31 hold k-groups 0
+        # and 1 of the same 16 rows; in chunks c and c+1 rows r and r ^ 8 would share a
+        # bank group (every read 2-way conflicted, measured), in chunks c and c+2 none do
         nofs = 2 * KS
         L.append(f"  unsigned int fofs[{nofs}];")
         L.append("  const unsigned int fg = ((fh & 1u) << 1) | (fh >> 1);")

@@ -7,12 +7,15 @@ tests evaluate both sets of expressions exactly as generated, for every wave and
 lane, and check that (a) the DMA fills each LDS slot of a stage exactly once, (b)
 every fragment read returns the (row, k-chunk) the 32x32x16 MFMA expects in that
 lane (32x32x16: row l % 32, chunk 2 ks + l / 32; 16x16x32: row l % 16, chunk
-4 ks + sigma(l / 16), sigma swapping the two bits), and (c) the 16 lanes that share
-an LDS access cycle hit 16 distinct 16-byte bank groups.  The LDS serves a 16-byte
-read to lanes 8j .. 8j+7 together with lanes 32+8j .. 32+8j+7 (rocprofv3's
-SQ_LDS_BANK_CONFLICT: zero for the 32x32 layout, and exactly one extra pass per read
-for a 16x16 layout whose k-groups g and g+2 sat in chunks c and c+2, as this grouping
-predicts and a grouping of 16 consecutive lanes does not).  The wait-count immediate is pinned against the assembler's own
+4 ks + sigma(l / 16), sigma swapping the two bits), and (c) the 32 lanes the LDS
+serves in one pass hit 32 distinct 16-byte bank groups.  The model -- a 16-byte read
+served 32 lanes at a time (lanes 0-31, then 32-63) over 128 four-byte banks (512
+bytes) -- is the one that fits every rocprofv3 SQ_LDS_BANK_CONFLICT reading taken:
+zero for the 32x32 layout, one extra pass per read for a 16x16 layout with k-groups
+0 and 1 in chunks c and c+1 (rows r and r ^ 8 collide), zero once they sit in c and
+c+2, and zero for the flash-attention kernel's 272-byte row pitch (32 consecutive
+rows on 32 distinct groups).  Groupings of 16 consecutive lanes, or of 8 + 8 lanes,
+contradict at least one of these readings.  The wait-count immediate is pinned against the assembler's own
 decoding of a compiled kernel."""
 import re
 import shutil
@@ -110,16 +113,15 @@ def test_dma_placement_and_fragment_reads_agree(cfg):
                     addr = _c_eval(base, env) + _c_eval(fofs[f], env) + int(xoff)
                     want = (w * rowdim + t * MI + (lane & (MI - 1)), kc * sub_step(t, f) + kgroup(lane))
                     assert slots[addr // 16] == want, (op, w, lane, t, f)
-        # bank groups: the 16 lanes served together (8j .. 8j+7 and 32+8j .. 32+8j+7) touch 16
-        # distinct 16-byte groups of a 256-byte row
+        # bank groups: the 32 lanes served in one pass touch 32 distinct 16-byte groups of 512 bytes
         for w in range(wdim):
             for t, f, xoff in set(reads):
-                for g in range(4):
+                for half in range(2):
                     grp = []
-                    for lane in list(range(8 * g, 8 * g + 8)) + list(range(32 + 8 * g, 40 + 8 * g)):
+                    for lane in range(32 * half, 32 * half + 32):
                         env = lane_env(lane, w)
-                        grp.append(((_c_eval(base, env) + _c_eval(fofs[int(f)], env) + int(xoff)) // 16) % 16)
-                    assert len(set(grp)) == 16, (op, w, t, f, g, grp)
+                        grp.append(((_c_eval(base, env) + _c_eval(fofs[int(f)], env) + int(xoff)) // 16) % 32)
+                    assert len(set(grp)) == 32, (op, w, t, f, half, grp)
 
 
 @pytest.mark.parametrize("epi", ["plain", "residual", "bias_gelu"])
