@@ -134,10 +134,15 @@ def _load_lines(src: str, ctype_ptr: str, off: str, inner: int, vec: int, dst: s
 
 
 # 16-byte vectors per lane in the pointwise and copy families.  One vector
-# per lane and 256-lane workgroups measured fastest at every size (deeper
-# unrolling loses 3-8% on config 2 and on a plain copy: the extra loads in
-# flight per lane do not make up for fewer resident waves per CU).
+# per lane measured fastest at every size (deeper unrolling loses 3-8% on
+# config 2 and on a plain copy: the extra loads in flight per lane do not make
+# up for fewer resident waves per CU).
 POINTWISE_UNROLL = 1
+# Lanes per workgroup of the pointwise family: config 2 (two streamed inputs,
+# one output) ran 132.4 us in fp32 / 58.8 us in bf16 with 128-lane workgroups
+# against 136.2 / 59.6 us with 256 and 133.7 / 58.5 with 512 (same box,
+# interleaved, best of 8 rounds)
+POINTWISE_THREADS = 128
 
 
 def gen_pointwise(g: KernelGen, nodes: list[Node], iter_shape: tuple[int, ...]) -> tuple[str, Launch]:
@@ -149,20 +154,20 @@ def gen_pointwise(g: KernelGen, nodes: list[Node], iter_shape: tuple[int, ...]) 
     vec = _vec_for(row_len, numel, _kernel_dtype(k))
     nvec = numel // vec
     unroll = POINTWISE_UNROLL
-    per_block = THREADS * unroll
+    per_block = POINTWISE_THREADS * unroll
     grid = max(1, -(-nvec // per_block))
     idx_t = _index_type(numel)
     guard = nvec % per_block != 0
     inside = {id(n) for n in nodes}
 
-    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {g.fname}({g.params()}) {{',
+    L = [f'extern "C" __global__ __launch_bounds__({POINTWISE_THREADS}) void {g.fname}({g.params()}) {{',
          f"  const {idx_t} vbase = ({idx_t})blockIdx.x * {per_block}u + threadIdx.x;"]
     for n in k.inputs:
         L.append(f"  float {g.names[id(n)]}_v[{unroll}][{vec}];")
     # phase 1: issue every load of this lane
     L.append("#pragma unroll")
     L.append(f"  for (int u = 0; u < {unroll}; ++u) {{")
-    L.append(f"    const {idx_t} vi = vbase + u * {THREADS}u;")
+    L.append(f"    const {idx_t} vi = vbase + u * {POINTWISE_THREADS}u;")
     if guard:
         L.append(f"    if (vi >= {nvec}u) break;")
     L.append(f"    const {idx_t} e = vi * {vec}u;")
@@ -175,7 +180,7 @@ def gen_pointwise(g: KernelGen, nodes: list[Node], iter_shape: tuple[int, ...]) 
     # phase 2: compute and store
     L.append("#pragma unroll")
     L.append(f"  for (int u = 0; u < {unroll}; ++u) {{")
-    L.append(f"    const {idx_t} vi = vbase + u * {THREADS}u;")
+    L.append(f"    const {idx_t} vi = vbase + u * {POINTWISE_THREADS}u;")
     if guard:
         L.append(f"    if (vi >= {nvec}u) break;")
     L.append(f"    const {idx_t} e = vi * {vec}u;")
@@ -204,7 +209,7 @@ def gen_pointwise(g: KernelGen, nodes: list[Node], iter_shape: tuple[int, ...]) 
     L.append("  }")
     L.append("}")
     meta = {"family": "pointwise", "vec": vec, "unroll": unroll, "numel": numel}
-    return "\n".join(L), Launch(g.fname, (grid, 1, 1), (THREADS, 1, 1), 0, meta)
+    return "\n".join(L), Launch(g.fname, (grid, 1, 1), (POINTWISE_THREADS, 1, 1), 0, meta)
 
 
 def gen_elementwise(g: KernelGen) -> tuple[str, Launch]:
