@@ -974,8 +974,9 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
     Rows are not padded; instead the 16-byte chunk ``c`` of tile row ``r`` is stored at
     position ``c ^ f(r)`` with ``f(r) = (r & 7) ^ ((r >> 3) & 3)``, applied by choosing
     which chunk each lane fetches (the 8 lanes of a row still cover one whole 128-byte
-    line).  Sixteen lanes of an MFMA fragment read (16 consecutive rows, one chunk)
-    then land on 16 distinct 16-byte bank groups.
+    line).  The LDS serves a 16-byte read 32 lanes at a time over 512 bytes of banks;
+    the 32 lanes of a fragment read (32 rows, or 16 rows x 2 k-groups) then land on 32
+    distinct 16-byte bank groups.
 
     Two LDS stages, each operand and stage its own ``__shared__`` array so the
     compiler can tell the stage being filled from the stage being read and does not
