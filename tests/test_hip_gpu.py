@@ -672,7 +672,8 @@ DIRECT_CFGS = [(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("case", ["one_tile", "two_tiles", "three_tiles", "ragged", "batched", "bias_gelu", "residual"])
+@pytest.mark.parametrize("case", ["one_tile", "two_tiles", "three_tiles", "ragged", "batched", "shared_weight",
+                                  "bias_gelu", "residual"])
 def test_direct_lds_gemm_matches_reference(case, dtype):
     """The direct-to-LDS schedule (buffer loads straight into swizzled LDS, one wave per
     SIMD): the peeled prologue / tail for 1-3 K tiles, rows past M and N (zero-filled by
@@ -683,10 +684,16 @@ def test_direct_lds_gemm_matches_reference(case, dtype):
 
     torch.manual_seed(0)
     shapes = {"one_tile": (256, 256, 64), "two_tiles": (256, 512, 128), "three_tiles": (512, 256, 192),
-              "ragged": (300, 520, 320), "batched": (200, 136, 256), "bias_gelu": (384, 640, 448),
-              "residual": (520, 264, 256)}
+              "ragged": (300, 520, 320), "batched": (200, 136, 256), "shared_weight": (300, 392, 192),
+              "bias_gelu": (384, 640, 448), "residual": (520, 264, 256)}
     m, n, kk = shapes[case]
-    if case == "batched":
+    if case == "shared_weight":
+        # a batch of activations times one weight (batch stride 0 for B), as every projection of a layer
+        a = torch.randn(3, m, kk, device=DEV).to(dtype)
+        b = torch.randn(n, kk, device=DEV).to(dtype)
+        fn = lambda x, y: tj.linear(x, y)
+        args, ref = [a, b], a.float() @ b.float().t()
+    elif case == "batched":
         a = torch.randn(2, 3, m, kk, device=DEV).to(dtype)
         b = torch.randn(2, 3, n, kk, device=DEV).to(dtype)
         fn = lambda x, y: tj.matmul(x, tj.transpose(y, 2, 3))
