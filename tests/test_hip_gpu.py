@@ -533,6 +533,22 @@ def test_config4_gemm_full_size_bf16_rows_vs_oracle():
     close_lowp(out, ref, tol=2e-2)
 
 
+def test_config4_skinny_decode_full_size_vs_oracle():
+    """Config 4's decode shape, 16 x 8192 x 8192 bf16 + bias + gelu, through ``tj.jit`` on its
+    packaged tile (the streaming kernel, K split over the waves), against the oracle on the
+    whole output."""
+    torch.manual_seed(0)
+    x = torch.randn(16, 8192, device=DEV).bfloat16()
+    w = (0.02 * torch.randn(8192, 8192, device=DEV)).bfloat16()
+    bias = (0.02 * torch.randn(8192, device=DEV)).bfloat16()
+    fn = lambda x, w, b: tj.gelu(tj.linear(x, w, b))  # noqa: E731
+    f = tj.jit(fn)
+    out = f(x, w, bias)
+    assert f.compiled(x, w, bias).matmul_configs[0].SPLIT_K > 1
+    (orc,) = oracle.run(fn, x.float().cpu(), w.float().cpu(), bias.float().cpu())
+    close_lowp(out, orc, tol=2e-2)
+
+
 def test_config5_block_with_fused_attention_vs_oracle():
     """Config 5's layer at head dim 64 (so the attention chain and its head transposes
     fuse into one flash kernel: 10 kernels), bf16 vs the fp32 oracle of the reference
