@@ -549,6 +549,28 @@ def test_config4_skinny_decode_full_size_vs_oracle():
     close_lowp(out, orc, tol=2e-2)
 
 
+def test_config5_attention_full_size_sampled_heads():
+    """Config 5's attention core at its full shape, [4, 32, 2048, 128] bf16 with the 1/sqrt(128)
+    scale, through the fused flash kernel (8 waves, ping-pong, 32 key blocks), against an fp32
+    reference on four (batch, head) pairs; the rows of every head sum the values with weights
+    that sum to 1, so the output's mean over keys is also checked on all heads."""
+    torch.manual_seed(0)
+    q, k, v = [torch.randn(4, 32, 2048, 128, device=DEV).bfloat16() for _ in range(3)]
+    fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * (128 ** -0.5)), v)  # noqa: E731
+    f = tj.jit(fn)
+    out = f(q, k, v)
+    cp = f.compiled(q, k, v)
+    assert cp.num_kernels == 1 and "attention" in cp.launches[0].name
+    for b, h in ((0, 0), (1, 7), (2, 19), (3, 31)):
+        qf, kf, vf = q[b, h].float(), k[b, h].float(), v[b, h].float()
+        ref = torch.softmax(qf @ kf.t().contiguous() * (128 ** -0.5), dim=-1) @ vf
+        close_lowp(out[b, h], ref, tol=2e-2)
+    # convex combinations of V's rows: every output lies inside V's per-column range
+    lo, hi = v.float().amin(dim=2, keepdim=True), v.float().amax(dim=2, keepdim=True)
+    o = out.float()
+    assert bool(((o >= lo - 1e-2) & (o <= hi + 1e-2)).all())
+
+
 def test_config5_block_with_fused_attention_vs_oracle():
     """Config 5's layer at head dim 64 (so the attention chain and its head transposes
     fuse into one flash kernel: 10 kernels), bf16 vs the fp32 oracle of the reference
