@@ -571,6 +571,35 @@ def test_config5_attention_full_size_sampled_heads():
     assert bool(((o >= lo - 1e-2) & (o <= hi + 1e-2)).all())
 
 
+def test_config5_block_full_size_batch0_vs_fp32():
+    """Config 5's layer at its full shape ([4, 2048, 4096], 32 heads x 128, MLP 11008, bf16) on
+    the packaged tiles, against a float32 torch evaluation of the same layer for batch 0 (the
+    batches are independent)."""
+    import bench
+
+    args = bench.block_inputs(torch, torch.device(DEV))
+    f = tj.jit(bench._fn_block)
+    out = f(*args)
+    assert f.compiled(*args).num_kernels == 10
+    x, g1, wq, wk, wv, wo, g2, w1, w2 = [a.float() for a in args]
+    x = x[:1]
+    S, D, H = x.shape[1], x.shape[2], 32
+
+    def rms(t, g):
+        return t * torch.rsqrt((t * t).mean(-1, keepdim=True) + 1e-6) * g
+
+    def heads(t):
+        return t.reshape(1, S, H, D // H).transpose(1, 2).contiguous()
+
+    h = rms(x, g1)
+    q, k, v = heads(h @ wq.t().contiguous()), heads(h @ wk.t().contiguous()), heads(h @ wv.t().contiguous())
+    pr = torch.softmax(q @ k.transpose(-1, -2).contiguous() * (D // H) ** -0.5, dim=-1)
+    o = (pr @ v).transpose(1, 2).reshape(1, S, D)
+    x = x + o @ wo.t().contiguous()
+    ref = x + F.gelu(rms(x, g2) @ w1.t().contiguous()) @ w2.t().contiguous()
+    close_lowp(out[:1], ref, tol=3e-2)
+
+
 def test_config5_block_with_fused_attention_vs_oracle():
     """Config 5's layer at head dim 64 (so the attention chain and its head transposes
     fuse into one flash kernel: 10 kernels), bf16 vs the fp32 oracle of the reference
