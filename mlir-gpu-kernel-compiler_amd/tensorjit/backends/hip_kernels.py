@@ -10,9 +10,10 @@ vectors of the contiguous output.  A vector never crosses a row of the last
 dim, so every input is read with one offset per vector: a 16-byte load when
 its innermost stride is 1, one broadcast scalar when it is 0, a gather
 otherwise.  ``U`` vectors per lane are loaded before any is computed so
-several loads per lane are in flight.  Grid = one workgroup of 256 lanes per
-``256*U`` vectors (no grid-stride loop; HIP's dispatcher spreads workgroups
-over all XCDs round-robin).
+several loads per lane are in flight.  Grid = one workgroup of
+``POINTWISE_THREADS`` (128) lanes per ``128*U`` vectors (copies: 256 lanes; no
+grid-stride loop; HIP's dispatcher spreads workgroups over all XCDs
+round-robin).
 
 Family 2 (``row`` and stand-alone ``reduce``; reference template
 ``tensorjit/backends/cuda_backend.py:168-289``): one workgroup per row.  A
