@@ -117,6 +117,21 @@ def test_transpose_reshape_and_copies_are_bit_exact():
         assert torch.equal(h(y), y.permute(3, 0, 2, 1).contiguous())
 
 
+def test_int32_arithmetic_and_max_are_exact_below_2_24():
+    """int32 storage: pointwise ops evaluate in fp32, as the reference's expressions do, and
+    convert on store, so integer results below 2^24 in magnitude are exact -- a pointwise chain
+    with Python scalars, a maximum, and a row max (reduction from -inf) against torch's integer
+    arithmetic, bit for bit."""
+    g = torch.Generator(device=DEV).manual_seed(0)
+    x = torch.randint(-2 ** 20, 2 ** 20, (64, 1000), device=DEV, dtype=torch.int32, generator=g)
+    y = torch.randint(-2 ** 20, 2 ** 20, (64, 1000), device=DEV, dtype=torch.int32, generator=g)
+    f = tj.jit(lambda a, b: tj.maximum(a * 3 - b + 7, b))
+    out = f(x, y)
+    assert out.dtype == torch.int32 and torch.equal(out, torch.maximum(x * 3 - y + 7, y))
+    m = tj.jit(lambda a: tj.max(a))
+    assert torch.equal(m(x), x.amax(-1))
+
+
 # ------------------------------------------------------------------ reductions / rows
 
 
