@@ -75,10 +75,21 @@ def analytic_config(k: Kernel) -> MatmulConfig:
 # ---------------------------------------------------------------------------
 
 
+def reject_zero_size(nodes) -> None:
+    """Zero-size tensors are not supported: every generated kernel assumes a non-empty
+    iteration space (the pointwise family would run one unguarded workgroup), so such a
+    program is refused before any code is generated or memory allocated, with the
+    ``NotImplementedError`` that sends torch.compile back to eager."""
+    for n in nodes:
+        if any(d == 0 for d in n.shape):
+            raise NotImplementedError(f"{n.name}: zero-size tensor {tuple(n.shape)} is not supported by the hip backend")
+
+
 def generate_kernel(k: Kernel, idx: int, cfg: MatmulConfig | None = None) -> tuple[str, Launch | list[Launch]]:
     """HIP source of one fused kernel and its launch(es).  A GEMM whose K is split
     across workgroups (``KSPLIT``) has two: partial products into a workspace, then
     the sum of the partials with the fused epilogue."""
+    reject_zero_size(list(k.inputs) + list(k.nodes) + list(k.outputs))
     g = KernelGen.of(k, idx)
     if k.kind == "elementwise":
         return gen_elementwise(g)
@@ -178,6 +189,7 @@ class HipProgram:
 
     def __init__(self, program: Program, device: str | torch.device = "cuda", use_graph: bool | None = None,
                  tune: bool = True):
+        reject_zero_size(list(program.graph.inputs) + [n for k in program.kernels for n in k.nodes])
         # backend-level rewrite of the planned program: attention chains -> one kernel
         program = fuse_attention(program)
         self.program = program

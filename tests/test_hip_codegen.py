@@ -145,3 +145,21 @@ def test_k_split_gemm_has_a_partial_and_a_sum_launch():
     hb.compile_source(src, "gfx950")
     # splits must divide K into whole K steps
     assert not hb.config_ok(MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 7), DType.f32, p.kernels[0].anchor)
+
+
+@pytest.mark.parametrize("case", ["pointwise_0x4", "pointwise_3x0", "softmax_0x8", "softmax_4x0", "matmul_m0", "matmul_k0"])
+def test_zero_size_tensors_are_refused_before_codegen(case):
+    """Every kernel assumes a non-empty iteration space (a pointwise kernel over [0, 4] would run
+    one unguarded workgroup), so zero-size tensors raise NotImplementedError -- the signal that
+    sends torch.compile back to eager -- before any source is generated."""
+    fn, shapes = {
+        "pointwise_0x4": (lambda a: tj.exp(a) + 1.0, [(0, 4)]),
+        "pointwise_3x0": (lambda a: tj.exp(a) + 1.0, [(3, 0)]),
+        "softmax_0x8": (lambda a: tj.softmax(a), [(0, 8)]),
+        "softmax_4x0": (lambda a: tj.softmax(a), [(4, 0)]),
+        "matmul_m0": (lambda a, b: tj.matmul(a, b), [(0, 8), (8, 4)]),
+        "matmul_k0": (lambda a, b: tj.matmul(a, b), [(4, 0), (0, 4)]),
+    }[case]
+    p = C.lower(tj.trace(fn, [TensorType(s, DType.f32) for s in shapes]), "hip")
+    with pytest.raises(NotImplementedError, match="zero-size"):
+        hb.generate(p)

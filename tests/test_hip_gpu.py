@@ -431,6 +431,24 @@ def test_misaligned_input_view_is_handled():
     torch.testing.assert_close(f(x), torch.exp(x) * 2)
 
 
+def test_zero_size_inputs_are_refused_without_a_launch():
+    """An empty tensor never reaches a kernel: tj.jit raises NotImplementedError while
+    compiling, and torch.compile (not strict) falls back to eager for that graph."""
+    torch._dynamo.reset()
+    f = tj.jit(lambda a: tj.exp(a) + 1.0)
+    with pytest.raises(NotImplementedError, match="zero-size"):
+        f(torch.empty(0, 4, device=DEV))
+
+    def g(a):
+        return torch.exp(a) + 1.0
+
+    c = torch.compile(g, backend=tj.torch_compile_backend, dynamic=False)
+    x = torch.empty(0, 4, device=DEV)
+    out = c(x)
+    assert out.shape == (0, 4) and out.device == x.device
+    torch._dynamo.reset()
+
+
 def test_torch_compile_backend_matches_eager(monkeypatch):
     monkeypatch.setenv("TENSORJIT_STRICT", "1")
     torch.manual_seed(0)
