@@ -380,15 +380,39 @@ extern "C" __global__ __launch_bounds__(256) void mfma_probe(const unsigned shor
   for (int j = 0; j < 16; ++j) for (int i = 0; i < 16; ++i) s += c[j][i];
   out0_p[blockIdx.x * 256 + threadIdx.x] = s;
 }
+extern "C" __global__ __launch_bounds__(256) void mfma_probe16(const unsigned short* in0_p, float* out0_p) {
+  __shared__ float pad[25600];           // one workgroup (four waves, one per SIMD) per CU
+  tj_bf16x8 a[4], b[4];
+  const unsigned int base = (blockIdx.x * 256u + threadIdx.x) * 64u;
+  for (int f = 0; f < 4; ++f) {
+    a[f] = *(const tj_bf16x8*)(in0_p + base + f * 16u);
+    b[f] = *(const tj_bf16x8*)(in0_p + base + f * 16u + 8u);
+  }
+  tj_f32x4 c[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) c[j] = (tj_f32x4)(0.0f);
+  pad[threadIdx.x] = (float)threadIdx.x;
+  for (int it = 0; it < 4096; ++it) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) c[x * 4 + y] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[x], b[y], c[x * 4 + y], 0, 0, 0);
+  }
+  float s = pad[(threadIdx.x + 1) & 255];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) for (int i = 0; i < 4; ++i) s += c[j][i];
+  out0_p[blockIdx.x * 256 + threadIdx.x] = s;
+}
 """
 
 
 def mfma_sustained(torch) -> dict:
-    """Sustained bf16 MFMA rate of a register-only loop (32x32x16, 16 accumulators,
-    one wave per SIMD) on constant operands and on N(0,1) operands: the same
-    instruction stream, timed on the data a GEMM actually multiplies.  The card holds
-    a lower clock on random data, so the random-operand rate, not the 2.5 PF dense
-    figure, is the ceiling the GEMM fractions should be read against."""
+    """Sustained bf16 MFMA rate of a register-only loop (32x32x16 and 16x16x32, 16
+    accumulators, one wave per SIMD) on constant operands and on N(0,1) operands: the
+    same instruction stream, timed on the data a GEMM actually multiplies.  The card
+    holds a lower clock on random data, so the random-operand rate, not the 2.5 PF
+    dense figure, is the ceiling the GEMM fractions should be read against; the
+    16x16x32 stream holds a higher one."""
     from tensorjit.backends.hip_backend import compile_source, arch_of
     from tensorjit.backends.hip_prelude import PRELUDE
     from tensorjit.runtime import hip as rt
@@ -398,15 +422,20 @@ def mfma_sustained(torch) -> dict:
     n = nblk * 256 * 64
     s = torch.cuda.current_stream().cuda_stream
     res = {}
-    for name, data in (("constant_TFLOP/s", torch.ones(n, device="cuda")), ("randn_TFLOP/s", torch.randn(n, device="cuda"))):
-        inp = data.to(torch.bfloat16)
-        outp = torch.empty(nblk * 256, device="cuda")
-        prog = rt.NativeHipProgram(0, code, ["mfma_probe"], [((nblk, 1, 1), (256, 1, 1), 0)],
-                                   [[(rt.INPUT, 0), (rt.OUTPUT, 0)]], 0, 1, 1)
-        prog.kernel_time(0, [inp.data_ptr()], [outp.data_ptr()], s, 2, 3)
-        ms = min(prog.kernel_time(0, [inp.data_ptr()], [outp.data_ptr()], s, 1, 5) for _ in range(3))
-        res[name] = round(nblk * 4 * 2048 * 16 * 32 * 32 * 16 * 2 / ms / 1e9, 1)
+    # (kernel, key suffix, FLOP per launch): 16 MFMAs per iteration per wave, 4 waves per workgroup
+    probes = (("mfma_probe", "", nblk * 4 * 2048 * 16 * 32 * 32 * 16 * 2),
+              ("mfma_probe16", "_16x16x32", nblk * 4 * 4096 * 16 * 16 * 16 * 32 * 2))
+    for kname, suffix, flops in probes:
+        for name, data in (("constant", torch.ones(n, device="cuda")), ("randn", torch.randn(n, device="cuda"))):
+            inp = data.to(torch.bfloat16)
+            outp = torch.empty(nblk * 256, device="cuda")
+            prog = rt.NativeHipProgram(0, code, [kname], [((nblk, 1, 1), (256, 1, 1), 0)],
+                                       [[(rt.INPUT, 0), (rt.OUTPUT, 0)]], 0, 1, 1)
+            prog.kernel_time(0, [inp.data_ptr()], [outp.data_ptr()], s, 2, 3)
+            ms = min(prog.kernel_time(0, [inp.data_ptr()], [outp.data_ptr()], s, 1, 5) for _ in range(3))
+            res[f"{name}{suffix}_TFLOP/s"] = round(flops / ms / 1e9, 1)
     res["randn_frac_of_2.5PF"] = round(res["randn_TFLOP/s"] / BF16_PEAK_TFLOPS, 4)
+    res["randn_16x16x32_frac_of_2.5PF"] = round(res["randn_16x16x32_TFLOP/s"] / BF16_PEAK_TFLOPS, 4)
     return res
 
 
