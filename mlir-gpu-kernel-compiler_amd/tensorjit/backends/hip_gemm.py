@@ -361,6 +361,7 @@ def staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch
         L.append(f"    Cs[(wm * {XP * MI}u + (x - {p * XP}) * {MI}u + {row_of}) * {ldc}u + wn * {BN // WN}u + y * {MI}u + "
                  f"{col_of}] = acc[x][y][r];")
         L.append("  __syncthreads();")
+        L.append("#pragma unroll")
         L.append(f"  for (unsigned int c = tid; c < {chunks}u; c += {THREADS}u) {{")
         L.append(f"    const unsigned int lr = c / {BN // ve}u, cc = (c % {BN // ve}u) * {ve}u;")
         L.append(f"    const {idx_t} i = m0 + (lr / {XP * MI}u) * {BM // WM}u + {p * XP * MI}u + lr % {XP * MI}u;")
@@ -406,6 +407,7 @@ def direct_staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx
             L.append("#pragma unroll")
             L.append(f"  for (int r = 0; r < {NACC}; ++r)")
             L.append(f"    Cw[({row}) * {ldc}u + y * {MI}u + lane % {MI}u] = acc[{x}][y][r];")
+        L.append("#pragma unroll")
         L.append(f"  for (unsigned int c = lane; c < {32 * per_row}u; c += 64u) {{")
         L.append(f"    const unsigned int lr = c / {per_row}u, cc = (c % {per_row}u) * {ve}u;")
         L.append(f"    const {idx_t} i = m0 + wm * {BM // WM}u + {p_ * 32}u + lr;")
