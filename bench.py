@@ -171,6 +171,33 @@ def load_traffic(workload: str):
     return None if entry is None else entry.get("traffic_bytes")
 
 
+def host_cpus() -> dict:
+    """CPU counts of the host the baseline runs on: logical CPUs, the CPUs this process
+    may run on (its affinity mask: the box's share), physical cores (distinct
+    (package, core) pairs in /proc/cpuinfo), and the OpenMP threads the oracle uses
+    (``OMP_NUM_THREADS`` when set -- the GPU boxes set it to their CPU share -- else
+    libgomp's default, one per CPU in the affinity mask)."""
+    logical = os.cpu_count() or 1
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = logical
+    cores, pkg = set(), "0"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "physical id":
+                pkg = val
+            elif key == "core id":
+                cores.add((pkg, val))
+    except OSError:
+        pass
+    threads = int(os.environ.get("OMP_NUM_THREADS") or allowed)
+    return {"omp_threads": threads, "logical_cpus": logical, "affinity_cpus": allowed,
+            "physical_cores": len(cores) or None}
+
+
 def cpu_baseline(torch, args_gpu, nbytes, seconds):
     import oracle
 
@@ -185,11 +212,14 @@ def cpu_baseline(torch, args_gpu, nbytes, seconds):
         if el >= seconds or n >= 5000:
             break
     per = el / n
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    host = host_cpus()
+    cores = host["omp_threads"]
     return {"value": round(nbytes / per / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"full config-2 fp32 workload [16384,4096] x {n} calls ({el:.1f} s), "
-                      f"oracle C/OpenMP restatement of the reference c backend, {cores} threads",
-            "ms_per_call": round(per * 1e3, 3)}
+                      f"oracle C/OpenMP restatement of the reference c backend, {cores} OpenMP threads "
+                      f"(host: {host['physical_cores']} physical cores, {host['logical_cpus']} logical CPUs, "
+                      f"{host['affinity_cpus']} in this process's CPU share)",
+            "host": host, "ms_per_call": round(per * 1e3, 3)}
 
 
 def cpu_secondary(torch, seconds_cap: float = 20.0) -> dict:
@@ -199,7 +229,7 @@ def cpu_secondary(torch, seconds_cap: float = 20.0) -> dict:
     and config 4 on a 128-row sample of x scaled to the full 8192 rows."""
     import oracle
 
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    cores = host_cpus()["omp_threads"]
     gen = torch.Generator().manual_seed(0)
     out = {"kind": "port", "cores": cores, "dtype": "f32 (bf16 configs on fp32 copies)"}
     t_start = time.perf_counter()

@@ -25,6 +25,8 @@
  *                           Graph.__del__                 tensorjit/backends/cuda_driver.py:126-131,161-168
  *   tj_hip_last_error       CudaError message             tensorjit/backends/cuda_driver.py:22-23,54-72
  *   tj_hip_device_info      compute_capability()          tensorjit/backends/cuda_driver.py:75-76
+ *   tj_hip_toolchain_version  the toolchain part of the   tensorjit/runtime/native.py:38-41,
+ *                           reference's build-cache keys  tensorjit/backends/cuda_backend.py:474
  *   tj_hip_kernel_time      (no counterpart: hipEvent timing of one kernel of a program, used
  *                           by the autotuner and the benchmark)
  */
@@ -38,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TJ_HIP_ABI_VERSION 1
+#define TJ_HIP_ABI_VERSION 2
 
 /* Where a kernel argument points: caller input i, arena + offset, caller output j. */
 enum { TJ_ARG_INPUT = 0, TJ_ARG_ARENA = 1, TJ_ARG_OUTPUT = 2 };
@@ -47,6 +49,8 @@ typedef struct tj_argref {
   int32_t kind;   /* TJ_ARG_* */
   int32_t pad_;
   int64_t value;  /* input index, arena byte offset, or output index */
+  int64_t bytes;  /* ARENA: size of the buffer at that offset (offset + bytes <= arena_bytes);
+                     ignored for INPUT / OUTPUT */
 } tj_argref;
 
 typedef struct tj_launch {
@@ -80,14 +84,19 @@ int tj_hip_abi_version(void);
 const char* tj_hip_last_error(void);
 int tj_hip_device_info(int device, tj_device_info* out);
 
+/* hipRTC version (hiprtcVersion) and HIP runtime version (hipRuntimeGetVersion), for
+ * keying cached code objects by toolchain.  Needs no device. */
+int tj_hip_toolchain_version(int* hiprtc_major, int* hiprtc_minor, int* hip_runtime);
+
 /* hipRTC: source -> code object (malloc'ed; release with tj_hip_free). */
 int tj_hip_compile(const char* source, const char* name, const char* const* opts, int nopts,
                    void** code, size_t* code_size);
 void tj_hip_free(void* p);
 
 /* Load the code object on `device`, resolve `nkernels` kernels, validate argument
- * references (args holds sum(launches[k].nargs) entries, kernel by kernel) and
- * allocate the arena with one hipMalloc. */
+ * references (args holds sum(launches[k].nargs) entries, kernel by kernel; every
+ * ARENA reference must lie inside the arena: 0 < bytes and offset + bytes <=
+ * arena_bytes) and allocate the arena with one hipMalloc. */
 int tj_hip_program_create(int device, const void* code, size_t code_size, int nkernels,
                           const char* const* names, const tj_launch* launches, const tj_argref* args,
                           size_t arena_bytes, int n_inputs, int n_outputs, void** handle);

@@ -223,6 +223,14 @@ int tj_hip_device_info(int device, tj_device_info* out) {
   return 0;
 }
 
+int tj_hip_toolchain_version(int* hiprtc_major, int* hiprtc_minor, int* hip_runtime) {
+  if (!hiprtc_major || !hiprtc_minor || !hip_runtime) return fail("tj_hip_toolchain_version: null argument");
+  hiprtcResult r = hiprtcVersion(hiprtc_major, hiprtc_minor);
+  if (r != HIPRTC_SUCCESS) return fail(std::string("hiprtcVersion: ") + hiprtcGetErrorString(r));
+  TJ_HIP(hipRuntimeGetVersion(hip_runtime));
+  return 0;
+}
+
 int tj_hip_compile(const char* source, const char* name, const char* const* opts, int nopts, void** code,
                    size_t* code_size) {
   if (!source || !code || !code_size) return fail("tj_hip_compile: null argument");
@@ -277,11 +285,11 @@ int tj_hip_program_create(int device, const void* code, size_t code_size, int nk
   p->n_in = n_inputs;
   p->n_out = n_outputs;
   p->arena_bytes = arena_bytes;
-  DeviceScope scope(device);
-  TJ_HIP(hipModuleLoadData(&p->module, code));
+  // 1. validate the whole launch and argument table (no device work yet)
   size_t pos = 0;
   for (int k = 0; k < nkernels; ++k) {
     KernelRec rec;
+    if (!names[k]) return fail("tj_hip_program_create: null kernel name");
     rec.name = names[k];
     rec.launch = launches[k];
     const tj_launch& l = rec.launch;
@@ -290,8 +298,6 @@ int tj_hip_program_create(int device, const void* code, size_t code_size, int nk
       return fail("zero-sized launch for " + rec.name);
     if (static_cast<uint64_t>(l.block[0]) * l.block[1] * l.block[2] > 1024) return fail("block too large for " + rec.name);
     if (l.lds_bytes > 160u * 1024u) return fail("dynamic LDS over 160 KiB for " + rec.name);
-    hipError_t e = hipModuleGetFunction(&rec.fn, p->module, rec.name.c_str());
-    if (e != hipSuccess) return hip_fail(e, ("hipModuleGetFunction " + rec.name).c_str());
     if (l.nargs && !args) return fail("tj_hip_program_create: null argument table");
     for (uint32_t i = 0; i < l.nargs; ++i) {
       const tj_argref& a = args[pos++];
@@ -300,8 +306,11 @@ int tj_hip_program_create(int device, const void* code, size_t code_size, int nk
       } else if (a.kind == TJ_ARG_OUTPUT) {
         if (a.value < 0 || a.value >= n_outputs) return fail("output index out of range in " + rec.name);
       } else if (a.kind == TJ_ARG_ARENA) {
-        if (a.value < 0 || static_cast<size_t>(a.value) >= (arena_bytes ? arena_bytes : 1))
-          return fail("arena offset out of range in " + rec.name);
+        // the whole buffer, not just its first byte, must lie inside the arena
+        if (a.value < 0 || a.bytes <= 0 || static_cast<uint64_t>(a.value) > arena_bytes ||
+            static_cast<uint64_t>(a.bytes) > arena_bytes - static_cast<uint64_t>(a.value))
+          return fail("arena buffer [" + std::to_string(a.value) + ", +" + std::to_string(a.bytes) +
+                      ") outside the " + std::to_string(arena_bytes) + "-byte arena in " + rec.name);
       } else {
         return fail("bad argument kind in " + rec.name);
       }
@@ -313,6 +322,13 @@ int tj_hip_program_create(int device, const void* code, size_t code_size, int nk
   }
   for (KernelRec& k : p->kernels)
     for (size_t i = 0; i < k.values.size(); ++i) k.params[i] = &k.values[i];
+  // 2. load the code object, resolve the kernels, allocate the arena
+  DeviceScope scope(device);
+  TJ_HIP(hipModuleLoadData(&p->module, code));
+  for (KernelRec& k : p->kernels) {
+    hipError_t e = hipModuleGetFunction(&k.fn, p->module, k.name.c_str());
+    if (e != hipSuccess) return hip_fail(e, ("hipModuleGetFunction " + k.name).c_str());
+  }
   if (arena_bytes) {
     void* a = nullptr;
     TJ_HIP(hipMalloc(&a, arena_bytes));

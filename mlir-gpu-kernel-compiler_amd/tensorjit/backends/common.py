@@ -89,10 +89,14 @@ def inner_stride(shape: Shape, strides: tuple[int, ...]) -> int:
     return 0
 
 
-# fp32 expressions.  exp / sigmoid / silu / gelu / div use the native-unit helpers of
-# the device prelude (tj_exp, tj_rcp, A&S 7.1.26 tj_erf): each is within a few ulp
-# (erf within 1.5e-7 absolute), far inside the 1e-5 relative parity bound, and
-# keeps HBM-bound pointwise kernels off the VALU limit.
+# fp32 expressions.  exp / sigmoid / silu / gelu use the native-unit helpers of the
+# device prelude (tj_exp, tj_rcp, A&S 7.1.26 tj_erf): each is within a few ulp (erf
+# within 1.5e-7 absolute), far inside the 1e-5 relative parity bound, and keeps
+# HBM-bound pointwise kernels off the VALU limit.  ``div`` is IEEE division
+# (correctly rounded, as in the reference's expression table): int32 storage
+# truncates the fp32 quotient, and a*rcp(b) would turn exact quotients such as
+# 41/41 into 0.99999994 -> 0; the hardware reciprocal also flushes 1/b to zero
+# for |b| > 2^126.
 HIP_EXPR = {
     "neg": "(-{0})",
     "exp": "tj_exp({0})",
@@ -108,7 +112,7 @@ HIP_EXPR = {
     "add": "({0} + {1})",
     "sub": "({0} - {1})",
     "mul": "({0} * {1})",
-    "div": "({0} * tj_rcp({1}))",
+    "div": "({0} / {1})",
     "pow": "powf({0}, {1})",
     "maximum": "fmaxf({0}, {1})",
     "minimum": "fminf({0}, {1})",

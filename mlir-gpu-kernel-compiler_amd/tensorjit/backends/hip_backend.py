@@ -124,28 +124,29 @@ def generate(program: Program, configs: dict[int, MatmulConfig] | None = None) -
 WS_ALIGN = 256
 
 
-def workspace_layout(launches: list[Launch], base: int) -> tuple[dict[int, int], int]:
-    """Arena offsets of the kernels' workspaces (split-K partials), placed after the
-    planned intermediates (``base`` bytes) in the same allocation, and the total size."""
+def workspace_layout(launches: list[Launch], base: int) -> tuple[dict[int, tuple[int, int]], int]:
+    """Arena ``(offset, bytes)`` of each kernel's workspace (split-K partials), placed
+    after the planned intermediates (``base`` bytes) in the same allocation, and the
+    total arena size."""
     off = -(-base // WS_ALIGN) * WS_ALIGN
-    ws: dict[int, int] = {}
+    ws: dict[int, tuple[int, int]] = {}
     for launch in launches:
         need = launch.meta.get("workspace", 0)
         if need:
-            ws[launch.meta["kernel"]] = off
+            ws[launch.meta["kernel"]] = (off, need)
             off += -(-need // WS_ALIGN) * WS_ALIGN
     return ws, (off if ws else base)
 
 
-def launch_args(launches: list[Launch], kernel_args: list[list], ws: dict[int, int]) -> list[list]:
+def launch_args(launches: list[Launch], kernel_args: list[list], ws: dict[int, tuple[int, int]]) -> list[list]:
     """Per-launch pointer refs: the kernel's inputs and outputs, plus its workspace for
-    the launches that take one (``meta["ws_arg"]``)."""
+    the launches that take one (``meta["ws_arg"]``) as ``(ARENA, offset, bytes)``."""
     out = []
     for launch in launches:
         idx = launch.meta["kernel"]
         refs = list(kernel_args[idx])
         if launch.meta.get("ws_arg"):
-            refs.append((rt.ARENA, ws[idx]))
+            refs.append((rt.ARENA, *ws[idx]))
         out.append(refs)
     return out
 
@@ -157,19 +158,41 @@ def launch_args(launches: list[Launch], kernel_args: list[list], ws: dict[int, i
 _compile_lock = threading.Lock()
 
 
-def arch_of(device_index: int | None) -> str:
+def target_of(device_index: int | None) -> str:
+    """The device's full ``gcnArchName`` (e.g. ``gfx950:sramecc+:xnack-``), or
+    ``TENSORJIT_HIP_ARCH`` when set."""
     forced = os.environ.get("TENSORJIT_HIP_ARCH")
     if forced:
         return forced
     if device_index is None:
         return DEFAULT_ARCH
-    return rt.device_info(device_index).arch.decode().split(":")[0]
+    return rt.device_info(device_index).arch.decode()
 
 
-def compile_source(source: str, arch: str, name: str = "tensorjit.hip") -> bytes:
-    """hipRTC compile with an on-disk code-object cache (source hash, target, ABI)."""
+def arch_of(device_index: int | None) -> str:
+    """The gfx processor of the device (``gfx950``): the hipRTC ``--offload-arch``."""
+    return target_of(device_index).split(":")[0]
+
+
+_toolchain: str | None = None
+
+
+def toolchain_tag() -> str:
+    """hipRTC and HIP runtime versions plus this library's ABI: part of every cached
+    code object's key, so a ROCm upgrade recompiles instead of loading old code."""
+    global _toolchain
+    if _toolchain is None:
+        major, minor, runtime = rt.toolchain_version()
+        _toolchain = f"hiprtc{major}.{minor}-hip{runtime}-abi{rt.ABI_VERSION}"
+    return _toolchain
+
+
+def compile_source(source: str, arch: str, name: str = "tensorjit.hip", target: str | None = None) -> bytes:
+    """hipRTC compile for ``--offload-arch=arch`` with an on-disk code-object cache keyed
+    by source, options, the full target name (``target``, default ``arch``) and the
+    toolchain."""
     opts = (f"--offload-arch={arch}", *COMPILE_OPTS)
-    cache = CodeObjectCache(arch, f"hiprtc-abi{rt.ABI_VERSION}")
+    cache = CodeObjectCache(target or arch, toolchain_tag())
     code = cache.get(source, opts)
     if code is not None:
         return code
@@ -200,7 +223,8 @@ class HipProgram:
             raise rt.HipError("the hip backend needs a ROCm GPU; torch.cuda.is_available() is False")
         self.device_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
         self.backend = "hip"
-        self.arch = arch_of(self.device_index)
+        self.target = target_of(self.device_index)
+        self.arch = self.target.split(":")[0]
         self.plan: MemoryPlan = plan_memory(program)
         self.matmul_configs: dict[int, MatmulConfig] = {}
         self._tuned_ms: dict[int, float] = {}
@@ -221,7 +245,7 @@ class HipProgram:
             if k.kind == "matmul":
                 self.matmul_configs[idx] = self._pick_config(k, idx, tune)
         self.source, self.launches = generate(program, self.matmul_configs)
-        self.code = compile_source(self.source, self.arch)
+        self.code = compile_source(self.source, self.arch, target=self.target)
         self._workspace, self.arena_bytes = workspace_layout(self.launches, self.plan.arena_bytes)
         self._native = self._load(self.code, self.launches, launch_args(self.launches, self._args, self._workspace))
 
@@ -233,7 +257,7 @@ class HipProgram:
         self.stats = {"calls": 0, "graph_replays": 0}
 
     # -- construction helpers -------------------------------------------------------
-    def _ref(self, n: Node) -> tuple[int, int]:
+    def _ref(self, n: Node) -> tuple[int, ...]:
         src = self.program.resolve(n)
         if id(src) in self._input_index:
             return rt.INPUT, self._input_index[id(src)]
@@ -242,7 +266,7 @@ class HipProgram:
         off = self.plan.offset(src)
         if off is None:
             raise RuntimeError(f"{n.name} has no storage (not an input, output or planned intermediate)")
-        return rt.ARENA, off
+        return rt.ARENA, off, (math.prod(src.shape) if src.shape else 1) * src.dtype.itemsize
 
     def _load(self, code: bytes, launches: list[Launch], args) -> rt.NativeHipProgram:
         return rt.NativeHipProgram(self.device_index, code, [l.name for l in launches],
@@ -277,7 +301,7 @@ class HipProgram:
 
         def build(cfg: MatmulConfig):
             src, launches = generate(single, {0: cfg})
-            code = compile_source(src, self.arch)
+            code = compile_source(src, self.arch, target=self.target)
             ws, arena = workspace_layout(launches, 0)
             prog = rt.NativeHipProgram(self.device_index, code, [l.name for l in launches],
                                        [(l.grid, l.block, 0) for l in launches], launch_args(launches, args, ws),

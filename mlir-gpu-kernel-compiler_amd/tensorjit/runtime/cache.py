@@ -1,114 +1,165 @@
-"""On-disk caches: HIP code objects and persisted GEMM autotune choices.
+"""On-disk caches of the hip backend: compiled code objects and GEMM tile choices.
 
-Root: ``$TENSORJIT_CACHE_DIR`` or ``~/.cache/tensorjit`` (ref
-``tensorjit/runtime/cache.py:14-61``).  Code objects are keyed by the source
-hash, the gfx target and the hipRTC version; autotune entries carry the
-target in their key, so a cache directory can be shared between machines of
-different architectures.
+Both live under ``$TENSORJIT_CACHE_DIR``, else ``~/.cache/tensorjit`` -- the
+reference's cache root (``tensorjit/runtime/cache.py:14-18``).
+
+* ``CodeObjectCache``: one file per hipRTC build.  The file name is a digest of
+  everything that decides the machine code: the source, the compile options,
+  the device's full ``gcnArchName`` (feature flags included) and the toolchain
+  (hipRTC and HIP runtime versions).  Upgrading ROCm or moving the cache to a
+  different part therefore misses instead of loading stale code.
+* ``AutotuneStore``: the reference's ``autotune.json`` format
+  (``tensorjit/runtime/cache.py:28-61``): ``{key: {"config": {...}, "ms": t}}``.
+  A write merges the new entry into what is on disk under an exclusive file
+  lock, so processes tuning different shapes at the same time keep each
+  other's results; a read picks up entries other processes wrote since.
+  Keys name their gfx target (``hip|gfx950|matmul|...``), and a key missing from
+  the user's file is looked up in the package's measured table for that
+  target (``tensorjit/tuned/<target>.json``) unless ``TENSORJIT_RETUNE=1``.
 """
 from __future__ import annotations
 
+import fcntl
 import hashlib
 import json
 import os
+import tempfile
 import threading
+from contextlib import contextmanager
 from pathlib import Path
-
-
-def cache_dir() -> Path:
-    d = Path(os.environ.get("TENSORJIT_CACHE_DIR", Path.home() / ".cache" / "tensorjit"))
-    d.mkdir(parents=True, exist_ok=True)
-    return d
-
-
-def content_hash(*parts: str) -> str:
-    h = hashlib.sha256()
-    for p in parts:
-        h.update(p.encode())
-        h.update(b"\0")
-    return h.hexdigest()[:20]
-
-
-def _atomic_write(path: Path, data: bytes) -> None:
-    tmp = path.with_name(f"{path.name}.{os.getpid()}.{threading.get_ident()}.tmp")
-    tmp.write_bytes(data)
-    os.replace(tmp, path)
-
 
 TUNED_DIR = Path(__file__).resolve().parents[1] / "tuned"
 
 
-def _packaged(key: str) -> dict | None:
-    """Read-only warm-start table shipped with the package (``tuned/<target>.json``),
-    keyed like the user store; consulted when the user store has no entry."""
-    parts = key.split("|")
-    if len(parts) < 2:
-        return None
+def cache_dir() -> Path:
+    root = os.environ.get("TENSORJIT_CACHE_DIR") or str(Path.home() / ".cache" / "tensorjit")
+    path = Path(root)
+    path.mkdir(parents=True, exist_ok=True)
+    return path
+
+
+def content_hash(*parts: str) -> str:
+    """Hex digest naming a tuple of strings (each part length-prefixed, so ("ab", "c")
+    and ("a", "bc") differ)."""
+    h = hashlib.blake2b(digest_size=16)
+    for part in parts:
+        data = part.encode()
+        h.update(len(data).to_bytes(8, "little"))
+        h.update(data)
+    return h.hexdigest()
+
+
+def _replace_file(path: Path, data: bytes) -> None:
+    """Write ``data`` to a temporary file beside ``path`` and rename it into place, so a
+    reader sees either the old or the new file, never a partial one."""
+    fd, tmp = tempfile.mkstemp(prefix=f".{path.name}.", dir=path.parent)
     try:
-        table = json.loads((TUNED_DIR / f"{parts[1]}.json").read_text())
+        with os.fdopen(fd, "wb") as f:
+            f.write(data)
+        os.replace(tmp, path)
+    except BaseException:
+        try:
+            os.unlink(tmp)
+        except OSError:
+            pass
+        raise
+
+
+def packaged_entry(key: str) -> dict | None:
+    """Entry for ``key`` in the package's measured table of the key's gfx target."""
+    fields = key.split("|")
+    if len(fields) < 2 or not fields[1]:
+        return None
+    table = TUNED_DIR / f"{fields[1]}.json"
+    try:
+        return json.loads(table.read_text()).get(key)
     except (OSError, ValueError):
         return None
-    return table.get(key)
 
 
 class AutotuneStore:
-    """JSON file of ``key -> {"config": ..., "ms": ...}``; writes are atomic renames.
+    """Persisted GEMM tile choices: ``get(key)``, ``put(key, config, ms)``, ``clear()``."""
 
-    Lookups fall back to the package's warm-start table for the key's gfx target,
-    so a fresh machine starts with measured tile choices instead of re-tuning;
-    set ``TENSORJIT_RETUNE=1`` to ignore that table."""
+    _thread_lock = threading.Lock()
 
-    _lock = threading.Lock()
+    def __init__(self, path: str | Path | None = None):
+        p = Path(path) if path is not None else Path("autotune.json")
+        self.path = p if p.is_absolute() else cache_dir() / p
+        self._entries: dict[str, dict] = {}
+        self._stamp: tuple[int, int] | None = None
 
-    def __init__(self, name: str = "autotune.json"):
-        self.path = cache_dir() / name
-        self._data: dict[str, dict] | None = None
+    def _file_stamp(self) -> tuple[int, int] | None:
+        try:
+            st = self.path.stat()
+        except OSError:
+            return None
+        return st.st_mtime_ns, st.st_size
 
-    def _load(self) -> dict:
-        if self._data is None:
+    def _read_disk(self) -> dict[str, dict]:
+        try:
+            data = json.loads(self.path.read_text())
+        except (OSError, ValueError):
+            return {}
+        return data if isinstance(data, dict) else {}
+
+    def _refresh(self) -> None:
+        stamp = self._file_stamp()
+        if stamp != self._stamp:
+            self._entries = self._read_disk()
+            self._stamp = stamp
+
+    @contextmanager
+    def _exclusive(self):
+        """This process's threads and other processes, one writer at a time."""
+        self.path.parent.mkdir(parents=True, exist_ok=True)
+        with self._thread_lock, open(self.path.with_name(self.path.name + ".lock"), "a+") as lk:
+            fcntl.flock(lk, fcntl.LOCK_EX)
             try:
-                self._data = json.loads(self.path.read_text())
-            except (OSError, ValueError):
-                self._data = {}
-        return self._data
+                yield
+            finally:
+                fcntl.flock(lk, fcntl.LOCK_UN)
 
     def get(self, key: str) -> dict | None:
-        with self._lock:
-            hit = self._load().get(key)
+        with self._thread_lock:
+            self._refresh()
+            hit = self._entries.get(key)
         if hit is None and os.environ.get("TENSORJIT_RETUNE") != "1":
-            hit = _packaged(key)
+            hit = packaged_entry(key)
         return hit
 
     def put(self, key: str, cfg: dict, ms: float) -> None:
-        with self._lock:
-            d = self._load()
-            d[key] = {"config": cfg, "ms": ms}
-            _atomic_write(self.path, json.dumps(d, indent=1, sort_keys=True).encode())
+        with self._exclusive():
+            merged = self._read_disk()
+            merged[key] = {"config": dict(cfg), "ms": float(ms)}
+            _replace_file(self.path, json.dumps(merged, indent=1, sort_keys=True).encode())
+            self._entries, self._stamp = merged, self._file_stamp()
 
     def clear(self) -> None:
-        with self._lock:
-            self._data = {}
-            if self.path.exists():
+        with self._exclusive():
+            try:
                 self.path.unlink()
+            except FileNotFoundError:
+                pass
+            self._entries, self._stamp = {}, None
 
 
 class CodeObjectCache:
-    """Compiled gfx code objects, one file per (source, target, compiler) triple."""
+    """hipRTC code objects on disk, keyed by source, options, target and toolchain."""
 
-    def __init__(self, target: str, compiler_tag: str):
+    def __init__(self, target: str, toolchain: str):
         self.target = target
-        self.compiler_tag = compiler_tag
+        self.toolchain = toolchain
 
     def path(self, source: str, opts: tuple[str, ...]) -> Path:
-        key = content_hash(source, self.target, self.compiler_tag, " ".join(opts))
-        return cache_dir() / f"tj_hip_{key}_{self.target}.co"
+        digest = content_hash(source, "\n".join(opts), self.target, self.toolchain)
+        gfx = self.target.split(":")[0]
+        return cache_dir() / f"tj_hip_{gfx}_{digest}.co"
 
     def get(self, source: str, opts: tuple[str, ...]) -> bytes | None:
-        p = self.path(source, opts)
         try:
-            return p.read_bytes()
+            return self.path(source, opts).read_bytes()
         except OSError:
             return None
 
     def put(self, source: str, opts: tuple[str, ...], code: bytes) -> None:
-        _atomic_write(self.path(source, opts), code)
+        _replace_file(self.path(source, opts), code)

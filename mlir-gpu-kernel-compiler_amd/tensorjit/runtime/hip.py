@@ -14,7 +14,7 @@ from typing import Sequence
 
 LIB_NAME = "libtjhip.so"
 LIB_PATH = Path(__file__).resolve().parents[1] / LIB_NAME
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 INPUT, ARENA, OUTPUT = 0, 1, 2
 
@@ -24,7 +24,8 @@ class HipError(RuntimeError):
 
 
 class ArgRef(ctypes.Structure):
-    _fields_ = [("kind", ctypes.c_int32), ("pad_", ctypes.c_int32), ("value", ctypes.c_int64)]
+    _fields_ = [("kind", ctypes.c_int32), ("pad_", ctypes.c_int32), ("value", ctypes.c_int64),
+                ("bytes", ctypes.c_int64)]
 
 
 class LaunchDesc(ctypes.Structure):
@@ -51,6 +52,7 @@ SIGNATURES = {
     "tj_hip_abi_version": (ctypes.c_int, []),
     "tj_hip_last_error": (ctypes.c_char_p, []),
     "tj_hip_device_info": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(DeviceInfo)]),
+    "tj_hip_toolchain_version": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int)] * 3),
     "tj_hip_compile": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), ctypes.c_int,
                                       _PP, ctypes.POINTER(ctypes.c_size_t)]),
     "tj_hip_free": (None, [_VP]),
@@ -106,6 +108,14 @@ def device_info(device: int = 0) -> DeviceInfo:
     return info
 
 
+def toolchain_version() -> tuple[int, int, int]:
+    """(hipRTC major, hipRTC minor, HIP runtime version); needs no GPU."""
+    major, minor, runtime = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check(load().tj_hip_toolchain_version(ctypes.byref(major), ctypes.byref(minor), ctypes.byref(runtime)),
+          "tj_hip_toolchain_version")
+    return major.value, minor.value, runtime.value
+
+
 def compile_source(source: str, name: str, opts: Sequence[str]) -> bytes:
     lib = load()
     copts = (ctypes.c_char_p * len(opts))(*[o.encode() for o in opts])
@@ -127,14 +137,14 @@ class NativeHipProgram:
     """Owns one ``tj_hip_program`` handle."""
 
     def __init__(self, device: int, code: bytes, names: Sequence[str], launches: Sequence[tuple],
-                 args: Sequence[Sequence[tuple[int, int]]], arena_bytes: int, n_in: int, n_out: int):
+                 args: Sequence[Sequence[tuple[int, ...]]], arena_bytes: int, n_in: int, n_out: int):
         lib = load()
         self._lib = lib
         self.n_in, self.n_out = n_in, n_out
         k = len(names)
         cnames = (ctypes.c_char_p * max(k, 1))(*[n.encode() for n in names])
         descs = (LaunchDesc * max(k, 1))()
-        flat: list[tuple[int, int]] = []
+        flat: list[tuple[int, ...]] = []
         for i, ((grid, block, lds), refs) in enumerate(zip(launches, args)):
             descs[i].grid[:] = list(grid)
             descs[i].block[:] = list(block)
@@ -142,8 +152,10 @@ class NativeHipProgram:
             descs[i].nargs = len(refs)
             flat.extend(refs)
         crefs = (ArgRef * max(len(flat), 1))()
-        for i, (kind, value) in enumerate(flat):
-            crefs[i].kind, crefs[i].value = kind, value
+        for i, ref in enumerate(flat):
+            # (INPUT, i) / (OUTPUT, j) / (ARENA, offset, bytes)
+            crefs[i].kind, crefs[i].value = ref[0], ref[1]
+            crefs[i].bytes = ref[2] if len(ref) > 2 else 0
         self._code = ctypes.create_string_buffer(code, len(code))
         handle = ctypes.c_void_p()
         check(lib.tj_hip_program_create(device, self._code, len(code), k, cnames, descs, crefs, arena_bytes, n_in, n_out,

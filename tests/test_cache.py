@@ -32,8 +32,56 @@ def test_packaged_table_is_a_fallback_only(tmp_path, monkeypatch):
     mine = MatmulConfig(64, 64, 16, 4, 2, 2, 32, 1).as_dict()
     store.put(key, mine, 9.0)                      # the user's own measurement wins
     assert store.get(key)["config"] == mine
-    assert cache._packaged("no-bars-in-this-key") is None
-    assert cache._packaged("hip|gfx000|matmul|x") is None
+    assert cache.packaged_entry("no-bars-in-this-key") is None
+    assert cache.packaged_entry("hip|gfx000|matmul|x") is None
+
+
+def test_writers_merge_instead_of_overwriting(tmp_path):
+    """Two stores (as two processes would) writing different keys keep both entries, and
+    a store sees entries another one wrote after it was opened."""
+    path = tmp_path / "autotune.json"
+    a, b = cache.AutotuneStore(path), cache.AutotuneStore(path)
+    cfg = MatmulConfig(64, 64, 16, 4, 2, 2, 32, 1).as_dict()
+    assert a.get("k1") is None and b.get("k2") is None       # both have read the (empty) file
+    a.put("k1", cfg, 1.0)
+    b.put("k2", cfg, 2.0)
+    on_disk = json.loads(path.read_text())
+    assert set(on_disk) == {"k1", "k2"}
+    assert a.get("k2") == {"config": cfg, "ms": 2.0}
+    a.clear()
+    assert b.get("k1") is None and not path.exists()
+
+
+def test_relative_store_name_lives_in_the_cache_dir(tmp_path, monkeypatch):
+    monkeypatch.setenv("TENSORJIT_CACHE_DIR", str(tmp_path / "c"))
+    assert cache.AutotuneStore().path == tmp_path / "c" / "autotune.json"
+    assert cache.AutotuneStore("other.json").path == tmp_path / "c" / "other.json"
+
+
+def test_code_object_key_covers_source_options_target_and_toolchain(tmp_path, monkeypatch):
+    monkeypatch.setenv("TENSORJIT_CACHE_DIR", str(tmp_path))
+    base = cache.CodeObjectCache("gfx950:sramecc+:xnack-", "hiprtc7.2-hip70226015")
+    opts = ("--offload-arch=gfx950", "-O3")
+    base.put("src", opts, b"code")
+    assert base.get("src", opts) == b"code"
+    misses = [
+        cache.CodeObjectCache("gfx950:sramecc+:xnack-", "hiprtc7.3-hip70300000").get("src", opts),  # new compiler
+        cache.CodeObjectCache("gfx950:sramecc-:xnack-", "hiprtc7.2-hip70226015").get("src", opts),  # other features
+        base.get("src2", opts),
+        base.get("src", ("--offload-arch=gfx950", "-O2")),
+    ]
+    assert misses == [None] * 4
+    assert cache.content_hash("ab", "c") != cache.content_hash("a", "bc")
+
+
+def test_hip_backend_tags_code_objects_with_the_hiprtc_version():
+    from tensorjit.backends import hip_backend
+    from tensorjit.runtime import hip as rt
+
+    major, minor, runtime = rt.toolchain_version()
+    assert major >= 6 and runtime > 0
+    tag = hip_backend.toolchain_tag()
+    assert f"hiprtc{major}.{minor}" in tag and f"hip{runtime}" in tag
 
 
 @pytest.mark.parametrize("key", sorted(json.loads((cache.TUNED_DIR / "gfx950.json").read_text())))

@@ -139,9 +139,9 @@ def test_k_split_gemm_has_a_partial_and_a_sum_launch():
     assert launches[0].grid == (12, 8, 8) and launches[0].meta["workspace"] == 8 * 512 * 768 * 4
     assert launches[1].meta["family"] == "ksplit_sum" and launches[1].grid == (384, 1, 1)
     ws, arena = hb.workspace_layout(launches, 1000)
-    assert ws == {0: 1024} and arena == 1024 + 8 * 512 * 768 * 4
+    assert ws == {0: (1024, 8 * 512 * 768 * 4)} and arena == 1024 + 8 * 512 * 768 * 4
     refs = hb.launch_args(launches, [[("in", 0), ("in", 1), ("in", 2), ("out", 0)]], ws)
-    assert all(r[-1] == (hb.rt.ARENA, 1024) for r in refs)
+    assert all(r[-1] == (hb.rt.ARENA, 1024, 8 * 512 * 768 * 4) for r in refs)
     hb.compile_source(src, "gfx950")
     # splits must divide K into whole K steps
     assert not hb.config_ok(MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 7), DType.f32, p.kernels[0].anchor)

@@ -132,19 +132,60 @@ def test_int32_arithmetic_and_max_are_exact_below_2_24():
     assert torch.equal(m(x), x.amax(-1))
 
 
+def test_int32_division_is_exact():
+    """int32 a / b evaluates as a correctly rounded fp32 quotient truncated on store (the
+    reference's expression is a plain ``/``).  For |a| < 2^24 the rounded quotient never
+    crosses an integer, so the result equals integer division truncated toward zero --
+    including exact multiples such as 41 / 41, which a reciprocal-multiply would store as 0."""
+    q = torch.arange(-199, 200, device=DEV, dtype=torch.int32)
+    d = torch.arange(1, 3000, device=DEV, dtype=torch.int32)
+    a = (q[:, None] * d[None, :]).contiguous()
+    b = d[None, :].expand_as(a).contiguous()
+    f = tj.jit(lambda u, v: u / v)
+    out = f(a, b)
+    assert out.dtype == torch.int32
+    assert torch.equal(out, q[:, None].expand_as(a))
+    assert int(f(torch.tensor([41], device=DEV, dtype=torch.int32),
+                 torch.tensor([41], device=DEV, dtype=torch.int32))[0]) == 1
+    g = torch.Generator(device=DEV).manual_seed(1)
+    a = torch.randint(-2 ** 23, 2 ** 23, (256, 1024), device=DEV, dtype=torch.int32, generator=g)
+    b = torch.randint(1, 2 ** 12, (256, 1024), device=DEV, dtype=torch.int32, generator=g)
+    b = torch.where(torch.rand(b.shape, device=DEV, generator=g) < 0.5, -b, b)
+    assert torch.equal(f(a, b), torch.div(a, b, rounding_mode="trunc"))
+
+
+def test_fp32_division_keeps_tiny_quotients():
+    """fp32 ``/`` is IEEE division: quotients by divisors near the top of the range come out
+    as the correctly rounded (subnormal) values torch computes, not 0."""
+    x = torch.linspace(-4, 4, 1000, device=DEV)
+    y = torch.full((1000,), 3.0e38, device=DEV)
+    out = tj.jit(lambda u, v: u / v)(x, y)
+    assert torch.equal(out, x / y) and bool((out[x != 0] != 0).all())
+
+
 # ------------------------------------------------------------------ reductions / rows
 
 
 @pytest.mark.parametrize("n", [1, 17, 100, 1000, 100000])
 def test_reductions(n):
     torch.manual_seed(0)
-    x = torch.randn(6, n, device=DEV)
-    f = tj.jit(lambda t: (tj.sum(t), tj.max(t), tj.mean(t, keepdim=True)))
-    s, m, mu = f(x)
-    refs = oracle.run(lambda t: (tj.sum(t), tj.max(t), tj.mean(t, keepdim=True)), x.cpu())
-    close_f32(s, refs[0], scale=1e-5 * math.sqrt(n))
-    assert torch.equal(m.cpu(), x.amax(-1).cpu())          # max is bit-exact
-    close_f32(mu, refs[2], scale=1e-5 * math.sqrt(n))
+    red = lambda t: (tj.sum(t), tj.max(t), tj.mean(t, keepdim=True))  # noqa: E731
+    f = tj.jit(red)
+    if n <= 1000:
+        x = torch.randn(6, n, device=DEV)
+        s, m, mu = f(x)
+        refs = oracle.run(red, x.cpu())
+        close_f32(s, refs[0], scale=1e-5 * math.sqrt(n))
+        assert torch.equal(m.cpu(), x.amax(-1).cpu())          # max is bit-exact
+        close_f32(mu, refs[2], scale=1e-5 * math.sqrt(n))
+    # small integers: every partial sum is an integer below 2^24, so the sum is exact in
+    # any order and a dropped or doubled element changes it; mean = sum / n correctly rounded
+    xi = torch.randint(-3, 4, (6, n), device=DEV).float()
+    s, m, mu = f(xi)
+    exact = xi.cpu().double().sum(-1)
+    assert torch.equal(s.cpu().double(), exact)
+    assert torch.equal(m.cpu(), xi.amax(-1).cpu())
+    assert torch.equal(mu.cpu().reshape(-1), exact.float() / float(n))
 
 
 def test_reduce_non_last_axis_via_transpose():
@@ -722,6 +763,129 @@ def test_every_bf16_tile_config_is_exact_on_integer_data(tb):
             assert torch.equal(out, ref), (m, n, kk, tb, cfg)
             tried += 1
         assert tried >= (3 if m > 16 else 1)
+
+
+@pytest.mark.parametrize("tb", [True, False])
+def test_every_fp32_tile_config_is_exact_on_integer_data(tb):
+    """Every fp32 candidate tiling -- 32x32x2 and 16x16x4 MFMA tiles, K split over
+    workgroups -- on shapes with ragged M / N / K edges, exact on small-integer data (every
+    partial sum is an integer below 2^24, so any summation order gives the same bits)."""
+    from tensorjit.backends import hip_backend as hb
+    from tensorjit.runtime.autotune import HIP_F32_CANDIDATES
+
+    torch.manual_seed(0)
+    mi32 = ksplit = 0
+    for m, n, kk in [(300, 520, 136), (100, 72, 40), (130, 260, 1024)]:
+        a = torch.randint(-2, 3, (m, kk), device=DEV).float()
+        b = torch.randint(-2, 3, (n, kk) if tb else (kk, n), device=DEV).float()
+        fn = (lambda x, y: tj.linear(x, y)) if tb else (lambda x, y: tj.matmul(x, y))
+        ref = (a.double() @ (b.double().t() if tb else b.double())).float()
+        mm = C_lower(fn, a, b).kernels[0].anchor
+        tried = 0
+        for cfg in HIP_F32_CANDIDATES:
+            if not hb.config_ok(cfg, hb.compute_dtype(mm), mm):
+                continue
+            out = _run_with_config(fn, [a, b], cfg)
+            assert torch.equal(out, ref), (m, n, kk, tb, cfg)
+            tried += 1
+            mi32 += cfg.MI == 32
+            ksplit += cfg.KSPLIT > 1
+        assert tried >= 4, (m, n, kk)
+    assert mi32 >= 4 * 3 and ksplit >= 4
+
+
+def test_config4_fp32_full_size_on_its_packaged_tile_vs_oracle():
+    """Config 4's fp32 variant, gelu(x @ w.T + bias) at 4096^3, through ``tj.jit`` on the tile
+    the packaged table holds for it (128x128x32 with 32x32x2 MFMAs): the oracle on a 64-row
+    sample at the fp32 bound, and a float64 product on the whole output."""
+    from tensorjit.backends import hip_backend as hb
+    from tensorjit.runtime.autotune import MatmulConfig
+    from tensorjit.runtime.cache import packaged_entry
+
+    torch.manual_seed(0)
+    x = torch.randn(4096, 4096, device=DEV)
+    w = 0.02 * torch.randn(4096, 4096, device=DEV)
+    bias = 0.02 * torch.randn(4096, device=DEV)
+    fn = lambda x, w, b: tj.gelu(tj.linear(x, w, b))  # noqa: E731
+    f = tj.jit(fn)
+    out = f(x, w, bias)
+    cp = f.compiled(x, w, bias)
+    entry = packaged_entry(hb.matmul_key(cp.program.kernels[0], cp.arch))
+    assert entry is not None and cp.matmul_configs[0] == MatmulConfig.from_dict(entry["config"])
+    assert cp.matmul_configs[0].MI == 32
+    rows = torch.arange(0, 4096, 64, device=DEV)
+    (orc,) = oracle.run(fn, x[rows].cpu(), w.cpu(), bias.cpu())
+    close_f32(out[rows], orc)
+    ref = F.gelu(F.linear(x.double(), w.double(), bias.double()))
+    close_f32(out, ref)
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_config1_mlp_full_size_vs_oracle(use_graph, monkeypatch):
+    """Config 1, the README MLP block at [512, 768] -> 3072 fp32 on its packaged tiles (the
+    down-projection split 8 ways over K), against the oracle at the fp32 bound -- on every
+    call, in eager launches and in hipGraph replays."""
+    monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "1" if use_graph else "0")
+    torch.manual_seed(0)
+    x = torch.randn(512, 768, device=DEV)
+    g = 1 + 0.1 * torch.randn(768, device=DEV)
+    w1, b1 = 0.02 * torch.randn(3072, 768, device=DEV), 0.02 * torch.randn(3072, device=DEV)
+    w2, b2 = 0.02 * torch.randn(768, 3072, device=DEV), 0.02 * torch.randn(768, device=DEV)
+    args = [x, g, w1, b1, w2, b2]
+    f = tj.jit(MLP)
+    for step in range(3):
+        xs = x + step
+        (ref,) = oracle.run(MLP, xs.cpu(), *[a.cpu() for a in args[1:]])
+        out = f(xs, *args[1:])
+        close_f32(out, ref)
+    cp = f.compiled(*args)
+    assert cp.num_kernels == 3 and cp.stats["graph_replays"] == (3 if use_graph else 0)
+    assert cp.matmul_configs[2].KSPLIT == 8 and len(cp.launches) == 4
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_on_device_autotune_times_candidates_and_persists_the_winner(dt, monkeypatch, tmp_path):
+    """``tune=True`` for a GEMM shape absent from the packaged table: the backend compiles and
+    times the cost model's best candidates on device buffers, stores the winner in a fresh
+    autotune store, runs with it (checked against the oracle), and a later compile of the same
+    shape reads the stored choice instead of tuning again.  Reference flow:
+    tensorjit/runtime/autotune.py:83-118; its test tests/test_cuda_backend.py:68-85."""
+    import json
+
+    from tensorjit.backends import hip_backend as hb
+    from tensorjit.runtime.autotune import MatmulConfig
+    from tensorjit.runtime.cache import packaged_entry
+
+    monkeypatch.delenv("TENSORJIT_NO_AUTOTUNE", raising=False)
+    monkeypatch.delenv("TENSORJIT_RETUNE", raising=False)
+    monkeypatch.setenv("TENSORJIT_CACHE_DIR", str(tmp_path / "fresh"))
+    torch.manual_seed(0)
+    m, n, k = (320, 576, 448) if dt == torch.bfloat16 else (200, 264, 384)
+    x = torch.randn(m, k, device=DEV).to(dt)
+    w = (0.05 * torch.randn(n, k, device=DEV)).to(dt)
+    b = (0.05 * torch.randn(n, device=DEV)).to(dt)
+    fn = lambda x, w, b: tj.gelu(tj.linear(x, w, b))  # noqa: E731
+    f = tj.jit(fn, tune=True)
+    out = f(x, w, b)
+    cp = f.compiled(x, w, b)
+    key = hb.matmul_key(cp.program.kernels[0], cp.arch)
+    assert packaged_entry(key) is None
+    stored = json.loads((tmp_path / "fresh" / "autotune.json").read_text())[key]
+    assert MatmulConfig.from_dict(stored["config"]) == cp.matmul_configs[0]
+    assert 0 < stored["ms"] < 1e3
+    (orc,) = oracle.run(fn, x.float().cpu(), w.float().cpu(), b.float().cpu())
+    if dt == torch.float32:
+        close_f32(out, orc)
+    else:
+        close_lowp(out, orc)
+
+    def no_tuning(*a, **kw):
+        raise AssertionError("a stored choice must not be tuned again")
+
+    monkeypatch.setattr(hb.HipProgram, "_autotune", no_tuning)
+    again = tj.jit(fn, tune=True)
+    assert torch.equal(again(x, w, b), out)
+    assert again.compiled(x, w, b).matmul_configs[0] == cp.matmul_configs[0]
 
 
 @pytest.mark.parametrize("case", ["f32_residual", "f32_ragged_gelu", "bf16_batched", "skinny_bias_gelu"])
