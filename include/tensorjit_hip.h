@@ -105,6 +105,18 @@ int tj_hip_program_create(int device, const void* code, size_t code_size, int nk
  * Asynchronous: never synchronises. */
 int tj_hip_program_run(void* handle, const void* const* inputs, void* const* outputs, void* stream);
 
+/* Allocation-free variant of tj_hip_program_run.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under stream capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The program's intermediates and
+ * split-K partials go to a static device array of TJ_HIP_STATIC_ARENA_BYTES per GPU
+ * instead of the program's own arena; a program whose arena is larger is rejected
+ * with an error.  The call allocates nothing (the first call on a device looks the
+ * array's address up once).  Every call on one GPU shares that array, which keeps the
+ * last call's contents: calls that overlap on one GPU (two streams, two threads) race.
+ * Nothing in it needs clearing -- every call writes each intermediate before reading it. */
+#define TJ_HIP_STATIC_ARENA_BYTES ((size_t)64 << 20)
+int tj_hip_program_run_static(void* handle, const void* const* inputs, void* const* outputs, void* stream);
+
 /* Capture the launch sequence for this input/output pointer set into a hipGraph exec
  * (kept in a small per-program cache keyed by the pointer set). */
 int tj_hip_program_capture(void* handle, const void* const* inputs, void* const* outputs);

@@ -18,17 +18,25 @@
 // ctypes CUDA driver (tensorjit/backends/cuda_driver.py:79-168).
 #include "../../include/tensorjit_hip.h"
 
-#include <hip/hip_runtime_api.h>
+#include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
+#include <atomic>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <list>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
+
+// Arena of tj_hip_program_run_static: file-scope device memory, so that entry point
+// never allocates.  Every GPU the library runs on holds its own copy until the
+// process ends.  Host code never uses this name as an address: the device address
+// comes from hipGetSymbolAddress, once per device (static_arena below).
+static __device__ __align__(256) char scratch[TJ_HIP_STATIC_ARENA_BYTES];
 
 namespace {
 
@@ -107,13 +115,15 @@ struct Program {
     if (module) (void)hipModuleUnload(module);
   }
 
-  void bind(const void* const* in, void* const* out) {
+  // Fill every kernel's pointer table; `base` is the arena the ARENA offsets refer to
+  // (the program's own, or the static one of tj_hip_program_run_static).
+  void bind(const void* const* in, void* const* out, char* base) {
     for (KernelRec& k : kernels) {
       for (size_t i = 0; i < k.refs.size(); ++i) {
         const tj_argref& r = k.refs[i];
         switch (r.kind) {
           case TJ_ARG_INPUT: k.values[i] = const_cast<void*>(in[r.value]); break;
-          case TJ_ARG_ARENA: k.values[i] = arena + r.value; break;
+          case TJ_ARG_ARENA: k.values[i] = base + r.value; break;
           default: k.values[i] = out[r.value]; break;
         }
       }
@@ -160,7 +170,7 @@ struct Program {
       return 0;
     }
     if (!capture_stream) TJ_HIP(hipStreamCreateWithFlags(&capture_stream, hipStreamNonBlocking));
-    bind(in, out);
+    bind(in, out, arena);
     GraphRec rec;
     rec.key = std::move(key);
     TJ_HIP(hipStreamBeginCapture(capture_stream, hipStreamCaptureModeThreadLocal));
@@ -190,6 +200,31 @@ struct Program {
 };
 
 Program* as_program(void* h) { return static_cast<Program*>(h); }
+
+constexpr int kMaxDevices = 64;
+std::mutex g_static_mu;
+std::atomic<char*> g_static_arena[kMaxDevices];
+
+// Device address of `scratch` on `device`, which must be the current device; looked up
+// with hipGetSymbolAddress on the first call for that device and kept.
+int static_arena(int device, char** out) {
+  if (device < 0 || device >= kMaxDevices) return fail("static arena: device index out of range");
+  char* ptr = g_static_arena[device].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(g_static_mu);
+    ptr = g_static_arena[device].load(std::memory_order_relaxed);
+    if (!ptr) {
+      void* addr = nullptr;
+      hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+      if (!addr) return fail("hipGetSymbolAddress(scratch) returned a null address");
+      ptr = static_cast<char*>(addr);
+      g_static_arena[device].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return 0;
+}
 
 uint64_t now_ns() {
   return std::chrono::duration_cast<std::chrono::nanoseconds>(
@@ -344,7 +379,30 @@ int tj_hip_program_run(void* handle, const void* const* inputs, void* const* out
   if ((p->n_in && !inputs) || (p->n_out && !outputs)) return fail("tj_hip_program_run: null pointer table");
   const uint64_t t0 = now_ns();
   DeviceScope scope(p->device);
-  p->bind(inputs, outputs);
+  p->bind(inputs, outputs, p->arena);
+  int rc = p->launch_all(static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  p->stats.calls++;
+  p->stats.host_ns += now_ns() - t0;
+  return 0;
+}
+
+int tj_hip_program_run_static(void* handle, const void* const* inputs, void* const* outputs, void* stream) {
+  Program* p = as_program(handle);
+  if (!p) return fail("tj_hip_program_run_static: null program");
+  if ((p->n_in && !inputs) || (p->n_out && !outputs)) return fail("tj_hip_program_run_static: null pointer table");
+  if (p->arena_bytes > TJ_HIP_STATIC_ARENA_BYTES)
+    return fail("tj_hip_program_run_static: the program's intermediates need " + std::to_string(p->arena_bytes) +
+                " bytes, more than the " + std::to_string(static_cast<size_t>(TJ_HIP_STATIC_ARENA_BYTES)) +
+                "-byte static arena (use tj_hip_program_run)");
+  const uint64_t t0 = now_ns();
+  DeviceScope scope(p->device);
+  char* base = nullptr;
+  if (p->arena_bytes) {
+    int rc = static_arena(p->device, &base);
+    if (rc) return rc;
+  }
+  p->bind(inputs, outputs, base);
   int rc = p->launch_all(static_cast<hipStream_t>(stream));
   if (rc) return rc;
   p->stats.calls++;
@@ -401,7 +459,7 @@ int tj_hip_kernel_time(void* handle, int k, const void* const* inputs, void* con
   if ((p->n_in && !inputs) || (p->n_out && !outputs)) return fail("tj_hip_kernel_time: null pointer table");
   DeviceScope scope(p->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  p->bind(inputs, outputs);
+  p->bind(inputs, outputs, p->arena);
   KernelRec& kr = p->kernels[k];
   for (int i = 0; i < warmup; ++i)
     if (int rc = p->launch_one(kr, s)) return rc;

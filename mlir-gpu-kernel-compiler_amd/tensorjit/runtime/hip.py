@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().parents[1] / LIB_NAME
 ABI_VERSION = 2
 
 INPUT, ARENA, OUTPUT = 0, 1, 2
+STATIC_ARENA_BYTES = 64 << 20   # TJ_HIP_STATIC_ARENA_BYTES
 
 
 class HipError(RuntimeError):
@@ -60,6 +61,7 @@ SIGNATURES = {
                                              ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(LaunchDesc),
                                              ctypes.POINTER(ArgRef), ctypes.c_size_t, ctypes.c_int, ctypes.c_int, _PP]),
     "tj_hip_program_run": (ctypes.c_int, [_VP, _PP, _PP, _VP]),
+    "tj_hip_program_run_static": (ctypes.c_int, [_VP, _PP, _PP, _VP]),
     "tj_hip_program_capture": (ctypes.c_int, [_VP, _PP, _PP]),
     "tj_hip_program_replay": (ctypes.c_int, [_VP, _PP, _PP, _VP]),
     "tj_hip_program_stats": (ctypes.c_int, [_VP, ctypes.POINTER(Stats)]),
@@ -164,6 +166,12 @@ class NativeHipProgram:
 
     def run(self, ins: Sequence[int], outs: Sequence[int], stream: int) -> None:
         check(self._lib.tj_hip_program_run(self.handle, ptr_table(ins), ptr_table(outs), stream), "tj_hip_program_run")
+
+    def run_static(self, ins: Sequence[int], outs: Sequence[int], stream: int) -> None:
+        """``run`` with the intermediates in the library's static per-GPU arena (allocates
+        nothing; rejects programs whose arena exceeds ``STATIC_ARENA_BYTES``)."""
+        check(self._lib.tj_hip_program_run_static(self.handle, ptr_table(ins), ptr_table(outs), stream),
+              "tj_hip_program_run_static")
 
     def capture(self, ins: Sequence[int], outs: Sequence[int]) -> None:
         check(self._lib.tj_hip_program_capture(self.handle, ptr_table(ins), ptr_table(outs)), "tj_hip_program_capture")

@@ -1,0 +1,73 @@
+"""tj_hip_program_run_static: the allocation-free variant of tj_hip_program_run.
+
+Same kernels, same launch order, intermediates in the library's static per-GPU
+arena instead of the program's own: outputs must equal tj_hip_program_run's bit for
+bit, on two calls in a row with the second program smaller than the first (the
+static arena then still holds the first call's larger contents), and a program whose
+arena exceeds the static one is refused before any launch.
+"""
+import pytest
+import torch
+
+import tensorjit as tj
+from tensorjit.runtime import hip as rt
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _env(monkeypatch, tmp_path_factory):
+    if not (torch.cuda.is_available() and torch.version.hip):
+        pytest.skip("needs a ROCm GPU")
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    monkeypatch.setenv("TENSORJIT_CACHE_DIR", str(tmp_path_factory.getbasetemp() / "tjcache"))
+
+
+def _mlp(x, g, w1, b1, w2, b2):
+    return x + tj.linear(tj.gelu(tj.linear(tj.layer_norm(x, g), w1, b1)), w2, b2)
+
+
+def _inputs(rows, d=768, f=3072, seed=0):
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    shapes = [(rows, d), (d,), (f, d), (f,), (d, f), (d,)]
+    scale = [1.0, 0.1, 0.02, 0.02, 0.02, 0.02]
+    return [torch.randn(s, device=DEV, generator=gen) * c for s, c in zip(shapes, scale)]
+
+
+def _both(cp, args):
+    """Outputs of tj_hip_program_run and tj_hip_program_run_static for the same inputs."""
+    stream = torch.cuda.current_stream().cuda_stream
+    ins = [a.contiguous() for a in args]
+    outs = [[torch.empty(s, dtype=d, device=DEV) for s, d in cp._out_specs] for _ in range(2)]
+    ip = [t.data_ptr() for t in ins]
+    cp.native.run(ip, [t.data_ptr() for t in outs[0]], stream)
+    cp.native.run_static(ip, [t.data_ptr() for t in outs[1]], stream)
+    torch.cuda.synchronize()
+    return outs
+
+
+def test_static_arena_run_matches_the_allocating_run():
+    f = tj.jit(_mlp)
+    big = _inputs(512)             # arena: LayerNorm + gelu outputs + 8-way split-K partials
+    cp_big = f.compiled(*big)
+    assert 0 < cp_big.arena_bytes <= rt.STATIC_ARENA_BYTES and len(cp_big.launches) == 4
+    small = _inputs(64, seed=1)
+    cp_small = f.compiled(*small)
+    assert 0 < cp_small.arena_bytes < cp_big.arena_bytes
+    for cp, args in ((cp_big, big), (cp_small, small), (cp_big, _inputs(512, seed=2))):
+        ref, got = _both(cp, args)
+        for r, o in zip(ref, got):
+            assert torch.equal(r, o)
+        torch.testing.assert_close(got[0], cp(*args)[0], atol=0, rtol=0)
+
+
+def test_programs_larger_than_the_static_arena_are_refused():
+    args = _inputs(16384)          # 48 MiB LayerNorm output + 192 MiB gelu output
+    cp = tj.jit(_mlp).compiled(*args)
+    assert cp.arena_bytes > rt.STATIC_ARENA_BYTES
+    out = torch.zeros(cp._out_specs[0][0], device=DEV)
+    with pytest.raises(rt.HipError, match="static arena"):
+        cp.native.run_static([a.data_ptr() for a in args], [out.data_ptr()], torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert not bool(out.any())     # refused before any launch
