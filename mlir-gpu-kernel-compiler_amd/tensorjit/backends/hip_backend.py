@@ -206,6 +206,13 @@ def compile_source(source: str, arch: str, name: str = "tensorjit.hip", target: 
 # executor
 # ---------------------------------------------------------------------------
 
+# hipGraph replay by default from this many launches per call.  Measured on MI355X with the
+# reference's overhead chain (softmax(x @ w + 0.5) repeated): a direct hipModuleLaunchKernel
+# costs 2.3-2.8 us of host time, a graph launch 21-25 us plus ~0.6 us per kernel node, so
+# 8 launches run 30 us direct / 33 us replayed and 16 launches 48 / 41 us.
+# TENSORJIT_HIP_GRAPH=1 / 0 forces replay on / off.
+GRAPH_MIN_LAUNCHES = 12
+
 
 class HipProgram:
     """A compiled program bound to one GPU (see module docstring for the protocol)."""
@@ -250,10 +257,10 @@ class HipProgram:
         self._native = self._load(self.code, self.launches, launch_args(self.launches, self._args, self._workspace))
 
         self.pool = BufferPool()
-        # hipGraph replay is opt-in: on ROCm a graph launch costs more host time
-        # (~30 us) than launching the few kernels of a fused program directly (~4 us each)
-        env = os.environ.get("TENSORJIT_HIP_GRAPH", "0") == "1"
-        self.use_graph = env if use_graph is None else use_graph
+        env = os.environ.get("TENSORJIT_HIP_GRAPH")
+        if use_graph is None:
+            use_graph = env == "1" if env in ("0", "1") else len(self.launches) >= GRAPH_MIN_LAUNCHES
+        self.use_graph = use_graph
         self.stats = {"calls": 0, "graph_replays": 0}
 
     # -- construction helpers -------------------------------------------------------

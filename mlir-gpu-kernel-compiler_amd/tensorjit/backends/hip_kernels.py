@@ -16,13 +16,15 @@ grid-stride loop; HIP's dispatcher spreads workgroups over all XCDs
 round-robin).
 
 Family 2 (``row`` and stand-alone ``reduce``; reference template
-``tensorjit/backends/cuda_backend.py:168-289``): one workgroup per row.  A
-lane owns ``NCH`` 16-byte chunks of the row, chunk ``c`` at element
-``(c*T + tid)*VEC``, so each chunk load is coalesced across the workgroup.
-External row inputs are loaded once into VGPRs at kernel entry (the
-reference reloads them in every stage) and values needed by later stages
-stay in VGPRs.  A reduction is a per-lane partial, a wave64 xor butterfly and
-one LDS exchange between the waves (one barrier, its own LDS slots per
+``tensorjit/backends/cuda_backend.py:168-289``): ``T`` lanes per row, each
+owning ``NCH`` 16-byte chunks of it, chunk ``c`` at element ``(c*T + tid)*VEC``,
+so each chunk load is coalesced.  Rows up to 4 KiB get one wave each (several
+rows per workgroup), rows up to 16 KiB one workgroup with one chunk per lane,
+longer rows several chunks per lane (``row_shape``).  External row inputs are
+loaded once into VGPRs at kernel entry (the reference reloads them in every
+stage) and values needed by later stages stay in VGPRs.  A reduction is a
+per-lane partial, a wave64 DPP all-reduce and, with more than one wave per
+row, one LDS exchange between the waves (one barrier, its own LDS slots per
 reduction so consecutive reductions never race).  A row group without any
 reduction is emitted as a flat family-1 loop nest over ``rows x N``.
 """
@@ -288,6 +290,39 @@ def row_geometry(N: int, vec: int, streaming_ok: bool) -> tuple[int, int, bool]:
     return t, nch, False
 
 
+# Row layouts, chosen by row size in 16-byte chunks (nv), measured on MI355X against a
+# flat copy of the same bytes (165 us for bf16 [65536, 4096] on the same box):
+# * nv <= 256 (rows up to 4 KiB): one 64-lane wave per row, WAVE_ROWS_PER_BLOCK rows per
+#   workgroup; reductions never leave the wave (no LDS, no barrier).  Config 5's bf16
+#   softmax [262144, 2048]: 360 us against 395 us for one 256-lane workgroup per row.
+# * nv <= 1024 (up to 16 KiB): one workgroup per row, one chunk per lane (nv lanes rounded
+#   up to a whole wave).  Streaming copies run fastest with a single 16-byte load per lane
+#   (two or more per lane lose 6-12%): RMSNorm bf16 [65536, 4096] 167 us against 173 us
+#   with 256 lanes x 2 chunks.
+# * longer rows: row_geometry (up to 1024 lanes x 16 chunks, then a rolled loop).
+WAVE_ROW_MAX_CHUNKS = 4
+WAVE_ROWS_PER_BLOCK = 4
+ONE_CHUNK_MAX_LANES = 1024
+
+
+@dataclass(frozen=True)
+class RowShape:
+    lanes: int          # lanes per row
+    chunks: int         # 16-byte chunks per lane
+    streaming: bool     # rolled chunk loop, inputs loaded per stage
+    rows_per_block: int
+
+
+def row_shape(N: int, vec: int, streaming_ok: bool) -> RowShape:
+    nv = -(-N // vec)
+    if nv <= 64 * WAVE_ROW_MAX_CHUNKS:
+        return RowShape(64, -(-nv // 64), False, WAVE_ROWS_PER_BLOCK)
+    if nv <= ONE_CHUNK_MAX_LANES:
+        return RowShape(64 * -(-nv // 64), 1, False, 1)
+    t, nch, streaming = row_geometry(N, vec, streaming_ok)
+    return RowShape(t, nch, streaming, 1)
+
+
 def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[str, Launch]:
     k = g.k
     nrows = math.prod(rows) if rows else 1
@@ -298,7 +333,11 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
 
     dt = _kernel_dtype(k)
     vec = _vec_for(N, N, dt)
-    T, NCH, streaming = row_geometry(N, vec, streaming_ok=len(stages) == 1)
+    shape = row_shape(N, vec, streaming_ok=len(stages) == 1)
+    T, NCH, streaming, R = shape.lanes, shape.chunks, shape.streaming, shape.rows_per_block
+    if R > 1 and nrows < R * 256:
+        # too few rows to fill the chip with R-row workgroups: one row per workgroup
+        R = 1
     nwaves = T // 64
     full = N % (T * vec) == 0
     inside = {id(n) for n in k.nodes}
@@ -341,11 +380,19 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
                                      vec_shape)
             vec_ext[id(n)] = (n, strides)
 
-    L = [f'extern "C" __global__ __launch_bounds__({T}) void {g.fname}({g.params()}) {{']
-    if nred:
+    L = [f'extern "C" __global__ __launch_bounds__({T * R}) void {g.fname}({g.params()}) {{']
+    if nred and nwaves > 1:
         L.append(f"  __shared__ float tj_red[{nred}][{nwaves}];")
-    L.append(f"  const {idx_t} r = blockIdx.x;")
-    L.append("  const unsigned int tid = threadIdx.x;")
+    if R == 1:
+        L.append(f"  const {idx_t} r = blockIdx.x;")
+        L.append("  const unsigned int tid = threadIdx.x;")
+    else:
+        # one wave per row: reductions never leave the wave, so a wave past the last
+        # row simply returns
+        L.append(f"  const {idx_t} r = ({idx_t})blockIdx.x * {R}u + (threadIdx.x >> 6);")
+        L.append("  const unsigned int tid = threadIdx.x & 63u;")
+        if nrows % R:
+            L.append(f"  if (r >= {nrows}u) return;")
     if scalars:
         L.append("  float " + ", ".join(g.names[id(n)] for n in scalars) + ";")
 
@@ -494,5 +541,6 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
             # per-row scalar stage over [rows] or [rows, 1]: linear index r addresses both
             L += scalar_lines(st.nodes, st, tuple(st.iter_shape), "r")
     L.append("}")
-    meta = {"family": "row", "vec": vec, "threads": T, "chunks": NCH, "streaming": streaming, "rows": nrows, "n": N}
-    return "\n".join(L), Launch(g.fname, (nrows, 1, 1), (T, 1, 1), 0, meta)
+    meta = {"family": "row", "vec": vec, "threads": T, "chunks": NCH, "streaming": streaming, "rows": nrows, "n": N,
+            "rows_per_block": R}
+    return "\n".join(L), Launch(g.fname, (-(-nrows // R), 1, 1), (T * R, 1, 1), 0, meta)

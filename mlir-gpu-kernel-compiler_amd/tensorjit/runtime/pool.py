@@ -8,11 +8,10 @@ its memory -- no tensor, no view, no storage handle.
 Mechanism (this module's own): the pool owns each buffer as a bare
 ``UntypedStorage`` and never keeps a tensor of it.  Every call gets a *new*
 tensor built on a free storage with ``Tensor.set_``.  Any tensor or view the
-caller still holds keeps a reference on the storage's C++ object, so a
-storage is free exactly when the pool's handle is its only user: use count 1
-on the C++ side and no Python reference to the handle beyond the pool's own
-(a caller may hold ``out.untyped_storage()``, which is the very same Python
-object).
+caller still holds keeps a reference on the storage's C++ object, so a storage
+is free exactly when the pool's handle is its only user: use count 1 on the C++
+side and no Python reference to the handle beyond the pool's own (a caller may
+hold ``out.untyped_storage()``, which is the very same Python object).
 
 On the GPU the point is pointer stability: a program called in a loop whose
 results are dropped each time gets the same output addresses every call,
@@ -32,7 +31,7 @@ class _Buffer:
 
     __slots__ = ("storage", "dtype", "device", "shape", "stride")
 
-    def __init__(self, shape: tuple[int, ...], dtype: torch.dtype, device: torch.device):
+    def __init__(self, shape: tuple[int, ...], dtype: torch.dtype, device):
         t = torch.empty(shape, dtype=dtype, device=device)
         self.storage = t.untyped_storage()
         self.dtype, self.device, self.shape, self.stride = dtype, t.device, tuple(shape), t.stride()
@@ -65,7 +64,7 @@ class BufferPool:
         for buf in held:
             if buf.unused():
                 return buf.tensor()
-        buf = _Buffer(shape, dtype, torch.device(device))
+        buf = _Buffer(shape, dtype, device)
         held.append(buf)
         if len(held) > self.MAX_HELD:
             del held[0]

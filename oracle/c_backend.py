@@ -391,7 +391,7 @@ FLAGS = ["-O3", "-shared", "-fPIC", "-ffast-math", "-march=native", "-fopenmp", 
 
 
 def build(source: str) -> ctypes.CDLL:
-    tag = hashlib.sha256(("oracle-v1\0" + source).encode()).hexdigest()[:20]
+    tag = hashlib.sha256(("oracle-v2\0" + source).encode()).hexdigest()[:20]
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     so = BUILD_DIR / f"oracle_{tag}.so"
     if not so.exists():
@@ -409,41 +409,71 @@ def build(source: str) -> ctypes.CDLL:
     return ctypes.CDLL(str(so))
 
 
+def gen_runner(program, plan, in_index: dict[int, int], out_index: dict[int, int]) -> str:
+    """``tj_run(in, out, arena)``: every kernel of the program in order, each argument
+    resolved at generation time to caller input i, caller output j or arena + offset --
+    the execution model of the reference's native runtime (``csrc/runtime.cpp:46-110``:
+    pre-resolved INPUT/OUTPUT/ARENA references, one planned arena, one call per program)."""
+    lines = ["void tj_run(void* const* in, void* const* out, char* arena) {"]
+    for idx, k in enumerate(program.kernels):
+        refs = []
+        for n in list(k.inputs) + list(k.outputs):
+            src = program.resolve(n)
+            if id(src) in in_index:
+                refs.append(f"in[{in_index[id(src)]}]")
+            elif id(src) in out_index:
+                refs.append(f"out[{out_index[id(src)]}]")
+            else:
+                off = plan.offset(src)
+                if off is None:
+                    raise RuntimeError(f"{n.name}: no storage in the oracle's plan")
+                refs.append(f"(void*)(arena + {off})")
+        lines.append(f"  {{ void* a[] = {{{', '.join(refs) or '0'}}}; k{idx}(a); }}")
+    lines.append("}")
+    return "\n".join(lines)
+
+
 class OracleProgram:
-    """Runs a fused program on CPU fp32 tensors through the generated C."""
+    """Runs a fused program on CPU fp32 tensors through the generated C: one native call
+    per program call (``tj_run``), intermediates in one planned arena reused by every call."""
 
     def __init__(self, program):
+        from tensorjit.passes.memory_planner import plan_memory
+
         self.program = program
-        self.source = generate(program)
+        g = program.graph
+        self.plan = plan_memory(program)
+        in_index = {id(n): i for i, n in enumerate(g.inputs)}
+        returned = {id(program.resolve(o)) for o in g.outputs}
+        self._out_nodes = []
+        for k in program.kernels:
+            for o in k.outputs:
+                if id(o) in returned and id(o) not in in_index and all(o is not x for x in self._out_nodes):
+                    self._out_nodes.append(o)
+        out_index = {id(o): j for j, o in enumerate(self._out_nodes)}
+        self.source = generate(program) + "\n\n" + gen_runner(program, self.plan, in_index, out_index)
         self.lib = build(self.source)
-        self.fns = []
-        for idx in range(len(program.kernels)):
-            fn = getattr(self.lib, f"k{idx}")
-            fn.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
-            fn.restype = None
-            self.fns.append(fn)
+        self._run = self.lib.tj_run
+        self._run.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p]
+        self._run.restype = None
+        # torch's CPU allocations are 64-byte aligned, the planner's alignment
+        self.arena = torch.empty(max(self.plan.arena_bytes, 64), dtype=torch.uint8)
 
     def __call__(self, *inputs: torch.Tensor) -> list[torch.Tensor]:
         g = self.program.graph
         if len(inputs) != len(g.inputs):
             raise TypeError(f"expected {len(g.inputs)} inputs, got {len(inputs)}")
-        env: dict[int, torch.Tensor] = {}
+        ins = []
         for node, t in zip(g.inputs, inputs):
             if tuple(t.shape) != tuple(node.shape):
                 raise ValueError(f"{node.name}: expected {node.shape}, got {tuple(t.shape)}")
-            env[id(node)] = t.detach().to("cpu", torch.float32).contiguous()
-        keep = []
-        for k, fn in zip(self.program.kernels, self.fns):
-            ins = []
-            for i in k.inputs:
-                src = self.program.resolve(i)
-                ins.append(env[id(src)])
-            outs = [torch.empty(o.shape, dtype=torch.float32) for o in k.outputs]
-            for o, t in zip(k.outputs, outs):
-                env[id(o)] = t
-            ptrs = (ctypes.c_void_p * (len(ins) + len(outs)))(*[t.data_ptr() for t in ins + outs])
-            fn(ptrs)
-            keep.append(outs)
+            ins.append(t.detach().to("cpu", torch.float32).contiguous())
+        outs = [torch.empty(o.shape, dtype=torch.float32) for o in self._out_nodes]
+        cin = (ctypes.c_void_p * max(len(ins), 1))(*[t.data_ptr() for t in ins])
+        cout = (ctypes.c_void_p * max(len(outs), 1))(*[t.data_ptr() for t in outs])
+        self._run(cin, cout, self.arena.data_ptr())
+        env = {id(n): t for n, t in zip(g.inputs, ins)}
+        env.update({id(o): t for o, t in zip(self._out_nodes, outs)})
         result = []
         for o in g.outputs:
             src = self.program.resolve(o)

@@ -63,12 +63,43 @@ def test_launch_geometry():
 
 
 def test_row_kernel_geometry_for_benchmark_rows():
-    from tensorjit.backends.hip_kernels import row_geometry
+    from tensorjit.backends.hip_kernels import RowShape, row_geometry, row_shape
 
-    assert row_geometry(4096, 8, False) == (256, 2, False)     # bf16 N=4096: 256 lanes x 2 x 16 B
-    assert row_geometry(2048, 4, False) == (256, 2, False)     # fp32 N=2048
-    assert row_geometry(768, 4, False) == (192, 1, False)      # fp32 N=768 (MLP LayerNorm)
-    assert row_geometry(100000, 4, True)[2] is True             # long stand-alone reductions stream
+    # rows of 8-16 KiB: one workgroup per row, one 16-byte chunk per lane
+    assert row_shape(4096, 8, False) == RowShape(512, 1, False, 1)     # config 3 LN / RMS bf16
+    assert row_shape(2048, 4, False) == RowShape(512, 1, False, 1)     # config 3 softmax fp32
+    assert row_shape(4096, 4, False) == RowShape(1024, 1, False, 1)    # fp32 N=4096
+    # rows up to 4 KiB: one wave per row, 4 rows per workgroup
+    assert row_shape(2048, 8, False) == RowShape(64, 4, False, 4)      # config 5 softmax bf16
+    assert row_shape(768, 4, False) == RowShape(64, 3, False, 4)       # config 1 LayerNorm fp32
+    assert row_shape(70, 1, False) == RowShape(64, 2, False, 4)        # unvectorised odd rows
+    # longer rows: several chunks per lane, then a rolled loop
+    assert row_shape(8192, 4, False) == RowShape(256, 8, False, 1)
+    assert row_geometry(4096, 8, False) == (256, 2, False)
+    assert row_shape(100000, 4, True).streaming is True                # long stand-alone reductions stream
+
+
+def test_row_kernel_launch_shapes():
+    """Wave-per-row kernels put 4 rows in a workgroup when there are rows enough to fill the
+    chip (a ragged last workgroup returns its extra waves), else one row per workgroup; the
+    reductions are wave-only there (no LDS array), and 8 KiB rows take 512-lane workgroups."""
+    import tensorjit as tj
+    from tensorjit.compiler import lower
+
+    def launch(shape, dt, fn=lambda s: tj.softmax(s)):
+        p = lower(tj.trace(fn, [TensorType(shape, dt)]), "hip")
+        src, ls = hb.generate(p)
+        return src, ls[0]
+
+    src, l = launch((262144, 2048), DType.bf16)
+    assert l.grid == (65536, 1, 1) and l.block == (256, 1, 1) and "tj_red" not in src
+    assert "threadIdx.x >> 6" in src and "return;" not in src.split("tj0_")[1]
+    src, l = launch((1000, 2048), DType.bf16)
+    assert l.grid == (1000, 1, 1) and l.block == (64, 1, 1)        # too few rows for 4 per workgroup
+    src, l = launch((4098, 1000), DType.f32)
+    assert l.grid == (1025, 1, 1) and l.block == (256, 1, 1) and "if (r >= 4098u) return;" in src
+    src, l = launch((65536, 2048), DType.f32)
+    assert l.grid == (65536, 1, 1) and l.block == (512, 1, 1) and "tj_red" in src
 
 
 def test_every_candidate_config_generates_valid_code():

@@ -392,6 +392,39 @@ def test_mlp_matches_eager_with_and_without_graph(use_graph, monkeypatch):
     assert cp.num_kernels == 3 and "__global__" in cp.source
 
 
+def test_graph_replay_is_the_default_from_twelve_launches(monkeypatch):
+    """Without TENSORJIT_HIP_GRAPH a program replays a hipGraph when it has at least
+    GRAPH_MIN_LAUNCHES launches per call (measured crossover of launch cost vs graph cost)
+    and launches directly below that; the variable forces either way."""
+    from tensorjit.backends.hip_backend import GRAPH_MIN_LAUNCHES
+
+    monkeypatch.delenv("TENSORJIT_HIP_GRAPH", raising=False)
+    x, w = torch.randn(16, 32, device=DEV), torch.randn(32, 32, device=DEV)
+
+    def chain(n):
+        def fn(a, b):
+            for _ in range(n):
+                a = tj.softmax(tj.matmul(a, b) + 0.5)
+            return a
+        return fn
+
+    ref8 = x
+    for _ in range(8):
+        ref8 = torch.softmax(ref8 @ w + 0.5, -1)
+    long_, short = tj.jit(chain(8)), tj.jit(chain(2))
+    for _ in range(3):
+        torch.testing.assert_close(long_(x, w), ref8, atol=1e-5, rtol=1e-5)
+        short(x, w)
+    cl, cs = long_.compiled(x, w), short.compiled(x, w)
+    assert len(cl.launches) == 16 >= GRAPH_MIN_LAUNCHES > len(cs.launches) == 4
+    assert cl.use_graph and cl.stats["graph_replays"] == 3
+    assert not cs.use_graph and cs.stats["graph_replays"] == 0
+    monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "0")
+    assert not tj.jit(chain(8)).compiled(x, w).use_graph
+    monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "1")
+    assert tj.jit(chain(2)).compiled(x, w).use_graph
+
+
 def test_graph_replays_match_eager_every_time(monkeypatch):
     monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "1")
     torch.manual_seed(0)
@@ -688,11 +721,11 @@ def test_config5_block_with_fused_attention_vs_oracle():
     assert cp.num_kernels == 10 and any("attention" in l.name for l in cp.launches)
     (ref,) = oracle.run(bench._fn_block, *[a.float().cpu() for a in args])
     close_lowp(out, ref, tol=3e-2)
+    cp.use_graph = False
     eager = cp(*args)[0].clone()
     cp.use_graph = True
     for _ in range(3):
         assert torch.equal(cp(*args)[0], eager)
-    cp.use_graph = False
 
 
 def test_config5_transformer_block_small_bf16_vs_oracle():
@@ -709,11 +742,11 @@ def test_config5_transformer_block_small_bf16_vs_oracle():
     close_lowp(out, ref, tol=3e-2)
     # graph replay of the same program gives the same bits as eager launches
     cp = f.compiled(*args)
+    cp.use_graph = False
     eager = cp(*args)[0].clone()
     cp.use_graph = True
     for _ in range(3):
         assert torch.equal(cp(*args)[0], eager)
-    cp.use_graph = False
 
 
 def _run_with_config(fn, args, cfg):
