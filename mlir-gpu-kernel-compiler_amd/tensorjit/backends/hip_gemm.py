@@ -86,7 +86,9 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
         if ok and mm is not None:
             M, N, K, tb = matmul_dims(mm)
             a, b = mm.inputs
-            ok = tb and M <= cfg.TM and K % 8 == 0 and a.dtype == b.dtype == dt
+            # buffer descriptors: byte offsets and ranges in 31 bits (out-of-range marker 2^31)
+            ok = (tb and M <= cfg.TM and K % 8 == 0 and a.dtype == b.dtype == dt
+                  and (N + cfg.TN) * K * 2 < 2**31 and M * K * 2 < 2**31)
         return ok
     if cfg.INTERLEAVE and (cfg.PINGPONG or (cfg.TK // ki) % 2):
         return False
@@ -129,9 +131,11 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     A workgroup owns TN = NT * MI output columns; its ``SPLIT_K`` waves each take a
     contiguous K slice.  The MFMA operands need no LDS: with K-contiguous A and B,
     lane ``l``'s 16-byte load of row ``l % MI`` at k-chunk ``l / MI`` is exactly its
-    operand register, so each wave streams B straight from HBM into the matrix core,
-    ``U`` loads ahead, and reuses each A fragment for its NT column tiles.  Partial
-    tiles are summed through LDS (one barrier), then the epilogue runs per element."""
+    operand register, so each wave streams B straight from HBM into the matrix core
+    and reuses each A fragment for its NT column tiles.  The loads of ``D = TK / KI``
+    K-steps are in flight ahead of the MFMAs (a ring of D register sets, the whole
+    slice unrolled).  Partial tiles are summed through LDS (one barrier), then the
+    epilogue runs per element."""
     k = g.k
     mm = k.anchor
     a, b = mm.inputs
@@ -150,8 +154,7 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     Kw = K // S                                      # this workgroup's K range
     steps_total = -(-Kw // KI)
     steps_per_wave = -(-steps_total // SK)
-    iters = -(-steps_per_wave // U)
-    k_guard = steps_per_wave * SK * KI != Kw or iters * U != steps_per_wave
+    k_guard = steps_per_wave * SK * KI != Kw          # some slice runs past the workgroup's K range
     A, B = g.names[id(a)], g.names[id(b)]
     epilogue = [n for n in k.nodes if n is not mm]
     fname = g.fname
@@ -182,45 +185,62 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     else:
         L.append(f"  const {CTYPE[a.dtype]}* __restrict__ Ab = {A}_p;")
         L.append(f"  const {CTYPE[b.dtype]}* __restrict__ Bb = {B}_p;")
+    # Operands come through buffer descriptors: a lane whose row is past M or N, or
+    # whose K position is past its slice, gets an offset beyond the descriptor's range
+    # and reads zeros -- no branch around any load, so the loads of D K-steps stay in
+    # flight ahead of the MFMAs (a ring of D register sets, fully unrolled).
+    OOB = 0x80000000
     L.append(f"  const unsigned int row = lane % {MI}u, kofs = (lane / {MI}u) * {KPL}u;")
-    L.append(f"  const bool arow_ok = row < {M}u;")
-    L.append(f"  const {CTYPE[a.dtype]}* Ar = Ab + (arow_ok ? row : 0u) * {K}u;")
-    L.append(f"  bool bcol_ok[{NT}];")
-    L.append(f"  const {CTYPE[b.dtype]}* Br[{NT}];")
-    L.append("#pragma unroll")
-    L.append(f"  for (int t = 0; t < {NT}; ++t) {{")
-    L.append(f"    bcol_ok[t] = n0 + t * {MI}u + row < {N}u;")
-    L.append(f"    Br[t] = Bb + (bcol_ok[t] ? n0 + t * {MI}u + row : 0u) * {K}u;")
-    L.append("  }")
-    acc_t = "tj_f32x16" if NACC == 16 else "tj_f32x4"
-    L.append(f"  {acc_t} acc[{NT}];")
-    L.append("#pragma unroll")
-    L.append(f"  for (int t = 0; t < {NT}; ++t) acc[t] = ({acc_t})(0.0f);")
+    L.append(f"  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, {M * K * 2}, 0x00020000);")
+    L.append(f"  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, {N * K * 2}, 0x00020000);")
     # the K slice of wave w in workgroup b is (w + b) mod SK: at any moment the
     # workgroups read different parts of A (which every workgroup reads whole) instead
     # of all requesting the same lines (27.7 vs 30.5 us for 16 x 8192 x 8192, TN 32)
     L.append(f"  const unsigned int kw = {'blockIdx.y * ' + str(Kw) + 'u + ' if S > 1 else ''}"
              f"((wave + blockIdx.x) % {SK}u) * {steps_per_wave * KI}u;")
-    L.append(f"  for (int it = 0; it < {iters}; ++it) {{")
-    L.append(f"    tj_u32x4 ra[{U}], rb[{U}][{NT}];")
+    kmax = f"{Kw}u" if S == 1 else f"(blockIdx.y + 1u) * {Kw}u"
+    L.append(f"  const unsigned int kend = {kmax} < kw + {steps_per_wave * KI}u ? {kmax} : kw + {steps_per_wave * KI}u;")
+    L.append(f"  const unsigned int offA = row < {M}u ? (row * {K}u + kw + kofs) * 2u : {OOB}u;")
+    L.append(f"  unsigned int offB[{NT}];")
     L.append("#pragma unroll")
-    L.append(f"    for (int u = 0; u < {U}; ++u) {{")
-    L.append(f"      const unsigned int kk = kw + (it * {U} + u) * {KI}u + kofs;")
-    if k_guard:
-        L.append(f"      const bool kin = (it * {U} + u) < {steps_per_wave} && kk < {K}u;")
-    else:
-        L.append("      const bool kin = true;")
-    L.append("      ra[u] = (arow_ok && kin) ? *(const tj_u32x4*)(Ar + kk) : (tj_u32x4){0u, 0u, 0u, 0u};")
-    L.append("#pragma unroll")
-    L.append(f"      for (int t = 0; t < {NT}; ++t)")
-    L.append("        rb[u][t] = (bcol_ok[t] && kin) ? *(const tj_u32x4*)(Br[t] + kk) : (tj_u32x4){0u, 0u, 0u, 0u};")
-    L.append("    }")
-    L.append("#pragma unroll")
-    L.append(f"    for (int u = 0; u < {U}; ++u)")
-    L.append("#pragma unroll")
-    L.append(f"      for (int t = 0; t < {NT}; ++t)")
-    L.append(f"        acc[t] = {builtin}(__builtin_bit_cast({opvec}, ra[u]), __builtin_bit_cast({opvec}, rb[u][t]), acc[t], 0, 0, 0);")
+    L.append(f"  for (int t = 0; t < {NT}; ++t) {{")
+    L.append(f"    const unsigned int col = n0 + t * {MI}u + row;")
+    L.append(f"    offB[t] = col < {N}u ? (col * {K}u + kw + kofs) * 2u : {OOB}u;")
     L.append("  }")
+    acc_t = "tj_f32x16" if NACC == 16 else "tj_f32x4"
+    L.append(f"  {acc_t} acc[{NT}];")
+    L.append("#pragma unroll")
+    L.append(f"  for (int t = 0; t < {NT}; ++t) acc[t] = ({acc_t})(0.0f);")
+    D = max(1, min(U, steps_per_wave))
+    L.append(f"  tj_u32x4 ra[{D}], rb[{D}][{NT}];")
+
+    def load(step: int) -> list[str]:
+        slot, byte = step % D, step * KI * 2
+        # a lane whose 16-byte chunk starts at or past the end of the slice reads zeros
+        # (slices are whole multiples of the chunk, so no chunk straddles the end)
+        kin = f"kw + {step * KI}u + kofs < kend" if k_guard else None
+        out = []
+        va = f"offA + {byte}u" if not kin else f"({kin}) ? offA + {byte}u : {OOB}u"
+        out.append(f"  ra[{slot}] = __builtin_bit_cast(tj_u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsA, {va}, 0, 0));")
+        for t in range(NT):
+            vb = f"offB[{t}] + {byte}u" if not kin else f"({kin}) ? offB[{t}] + {byte}u : {OOB}u"
+            out.append(f"  rb[{slot}][{t}] = __builtin_bit_cast(tj_u32x4, "
+                       f"__builtin_amdgcn_raw_buffer_load_b128(rsB, {vb}, 0, 0));")
+        return out
+
+    # The written order is kept (sched_barrier between steps): left alone, the scheduler
+    # sinks every load next to its MFMA to save registers, leaving ~2 K-steps in flight.
+    for step in range(min(D, steps_per_wave)):
+        L += load(step)
+    L.append("  __builtin_amdgcn_sched_barrier(0);")
+    for step in range(steps_per_wave):
+        slot = step % D
+        for t in range(NT):
+            L.append(f"  acc[{t}] = {builtin}(__builtin_bit_cast({opvec}, ra[{slot}]), "
+                     f"__builtin_bit_cast({opvec}, rb[{slot}][{t}]), acc[{t}], 0, 0, 0);")
+        if step + D < steps_per_wave:
+            L += load(step + D)
+        L.append("  __builtin_amdgcn_sched_barrier(0);")
     if MI == 32:
         row_of, col_of = "(r / 4) * 8 + (lane / 32u) * 4 + (r % 4)", "lane % 32u"
     else:
