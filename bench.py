@@ -535,8 +535,8 @@ def mfma_sustained(torch) -> dict:
 def profile_set(torch, dev, steps) -> None:
     """Kernels for rocprofv3 counter runs: the headline kernel, a plain copy-like
     calibration kernel of known traffic (y = x + 0.5, fp32 [16384,4096]: 256 MiB
-    read + 256 MiB written), the row configs, the config-4 bf16 GEMM and config 5's
-    fused attention, ``steps`` launches each."""
+    read + 256 MiB written), the row configs, the config-4 bf16 GEMM and its decode
+    shape, config 5's bf16 softmax rows and fused attention, ``steps`` launches each."""
     import tensorjit as tj
 
     args = c2_inputs(torch, torch.float32, dev)
@@ -568,6 +568,18 @@ def profile_set(torch, dev, steps) -> None:
     for _ in range(steps):
         jf(xg, wg, bg)
     del xg, wg, bg
+    xs = torch.randn(16, 8192, device=dev, generator=gen).bfloat16()
+    ws = (0.02 * torch.randn(8192, 8192, device=dev, generator=gen)).bfloat16()
+    bs = (0.02 * torch.randn(8192, device=dev, generator=gen)).bfloat16()
+    jf = tj.jit(_fn_gemm)
+    for _ in range(steps):
+        jf(xs, ws, bs)
+    del xs, ws, bs
+    s5 = (torch.randn(262144, 2048, device=dev, generator=gen) * 3).bfloat16()
+    jf = tj.jit(_fn_softmax)
+    for _ in range(steps):
+        jf(s5)
+    del s5
     qkv = [torch.randn(4, 32, 2048, 128, device=dev, generator=gen).bfloat16() for _ in range(3)]
     jf = tj.jit(_fn_attn)
     for _ in range(steps):
