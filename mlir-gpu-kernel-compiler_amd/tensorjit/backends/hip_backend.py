@@ -257,6 +257,7 @@ class HipProgram:
         self._native = self._load(self.code, self.launches, launch_args(self.launches, self._args, self._workspace))
 
         self.pool = BufferPool()
+        self._init_call_path()
         env = os.environ.get("TENSORJIT_HIP_GRAPH")
         if use_graph is None:
             use_graph = env == "1" if env in ("0", "1") else len(self.launches) >= GRAPH_MIN_LAUNCHES
@@ -337,20 +338,42 @@ class HipProgram:
     def native(self) -> rt.NativeHipProgram:
         return self._native
 
-    def _prepare(self, inputs) -> list[torch.Tensor]:
+    def _init_call_path(self) -> None:
+        """Everything a call needs that does not depend on the call's tensors."""
         g = self.program.graph
-        if len(inputs) != len(g.inputs):
-            raise TypeError(f"expected {len(g.inputs)} inputs, got {len(inputs)}")
+        self._in_checks = [(n.name, torch.Size(n.shape), TORCH_DTYPE[n.dtype]) for n in g.inputs]
+        self._dev = torch.device("cuda", self.device_index)
+        out_pos = {id(o): j for j, o in enumerate(self._out_nodes)}
+        in_pos = {id(n): i for i, n in enumerate(g.inputs)}
+        # per graph output: (0, output j) / (1, input i) / (2, const node), and its shape when
+        # it is a reshape alias of that value
+        self._result_plan = []
+        for o in g.outputs:
+            src = self.program.resolve(o)
+            if id(src) in out_pos:
+                kind, what = 0, out_pos[id(src)]
+            elif id(src) in in_pos:
+                kind, what = 1, in_pos[id(src)]
+            elif src.op == "const":
+                kind, what = 2, src
+            else:
+                raise RuntimeError(f"output {o.name} is not produced by any kernel")
+            reshape = tuple(o.shape) if tuple(src.shape) != tuple(o.shape) else None
+            self._result_plan.append((kind, what, reshape))
+
+    def _prepare(self, inputs) -> list[torch.Tensor]:
+        if len(inputs) != len(self._in_checks):
+            raise TypeError(f"expected {len(self._in_checks)} inputs, got {len(inputs)}")
         ins = []
-        for node, t in zip(g.inputs, inputs):
+        for (name, shape, dtype), t in zip(self._in_checks, inputs):
             if not isinstance(t, torch.Tensor):
-                raise TypeError(f"{node.name}: expected a torch.Tensor, got {type(t)}")
-            if tuple(t.shape) != tuple(node.shape) or t.dtype != TORCH_DTYPE[node.dtype]:
-                raise ValueError(f"{node.name}: expected {tuple(node.shape)} {TORCH_DTYPE[node.dtype]}, "
-                                 f"got {tuple(t.shape)} {t.dtype}")
-            if t.device != self.device and not (t.is_cuda and t.device.index == self.device_index):
-                raise ValueError(f"{node.name}: tensor on {t.device}, program compiled for {self.device}")
-            t = t.contiguous()
+                raise TypeError(f"{name}: expected a torch.Tensor, got {type(t)}")
+            if t.shape != shape or t.dtype != dtype:
+                raise ValueError(f"{name}: expected {tuple(shape)} {dtype}, got {tuple(t.shape)} {t.dtype}")
+            if t.get_device() != self.device_index:
+                raise ValueError(f"{name}: tensor on {t.device}, program compiled for {self._dev}")
+            if not t.is_contiguous():
+                t = t.contiguous()
             if t.data_ptr() % 16:
                 t = t.clone()   # 16-byte vector loads need 16-byte aligned bases
             ins.append(t)
@@ -358,32 +381,28 @@ class HipProgram:
 
     def __call__(self, *inputs: torch.Tensor) -> list[torch.Tensor]:
         ins = self._prepare(inputs)
-        outs = [self.pool.take_output(shape, dtype, self.device) for shape, dtype in self._out_specs]
-        ip = [t.data_ptr() for t in ins]
-        op = [t.data_ptr() for t in outs]
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        take, dev = self.pool.take_output, self._dev
+        outs = [take(shape, dtype, dev) for shape, dtype in self._out_specs]
+        stream = torch._C._cuda_getCurrentRawStream(self.device_index)
         self.stats["calls"] += 1
-        if self.use_graph and self.launches:
-            self._native.replay(ip, op, stream)
-            self.stats["graph_replays"] += 1
-        elif self.launches:
-            self._native.run(ip, op, stream)
+        if self.launches:
+            if self.use_graph:
+                self._native.replay_tensors(ins, outs, stream)
+                self.stats["graph_replays"] += 1
+            else:
+                self._native.run_tensors(ins, outs, stream)
         return self._results(ins, outs)
 
     def _results(self, ins: list[torch.Tensor], outs: list[torch.Tensor]) -> list[torch.Tensor]:
-        g = self.program.graph
-        env = {id(o): t for o, t in zip(self._out_nodes, outs)}
-        env.update({id(n): t for n, t in zip(g.inputs, ins)})
         result = []
-        for o in g.outputs:
-            src = self.program.resolve(o)
-            if id(src) in env:
-                t = env[id(src)]
-            elif src.op == "const":
-                t = torch.full(src.shape, src.attrs["value"], dtype=TORCH_DTYPE[src.dtype], device=self.device)
+        for kind, what, reshape in self._result_plan:
+            if kind == 0:
+                t = outs[what]
+            elif kind == 1:
+                t = ins[what]
             else:
-                raise RuntimeError(f"output {o.name} was not produced")
-            result.append(t.reshape(o.shape) if tuple(t.shape) != tuple(o.shape) else t)
+                t = torch.full(what.shape, what.attrs["value"], dtype=TORCH_DTYPE[what.dtype], device=self._dev)
+            result.append(t if reshape is None else t.reshape(reshape))
         return result
 
     # -- measurement helpers --------------------------------------------------------

@@ -81,7 +81,7 @@ class JitFunction:
 
     def _key(self, args: Sequence[torch.Tensor]) -> tuple:
         dev = args[0].device
-        return (tuple((tuple(a.shape), a.dtype) for a in args), str(dev), pick_backend(dev.type, self.backend))
+        return (tuple((a.shape, a.dtype) for a in args), dev, pick_backend(dev.type, self.backend))
 
     def trace(self, *args: torch.Tensor) -> Graph:
         return trace(self.fn, [tensor_type_of(a) for a in args], name=getattr(self.fn, "__name__", "main"))

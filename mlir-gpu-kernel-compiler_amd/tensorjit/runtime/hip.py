@@ -159,31 +159,51 @@ class NativeHipProgram:
             crefs[i].kind, crefs[i].value = ref[0], ref[1]
             crefs[i].bytes = ref[2] if len(ref) > 2 else 0
         self._code = ctypes.create_string_buffer(code, len(code))
+        # pointer tables reused by every call (a program is not re-entrant: it has one arena)
+        self._in_arr = (ctypes.c_void_p * max(n_in, 1))()
+        self._out_arr = (ctypes.c_void_p * max(n_out, 1))()
         handle = ctypes.c_void_p()
         check(lib.tj_hip_program_create(device, self._code, len(code), k, cnames, descs, crefs, arena_bytes, n_in, n_out,
                                         ctypes.byref(handle)), "tj_hip_program_create")
         self.handle = handle
 
+    def _tables(self, ins: Sequence[int], outs: Sequence[int]):
+        if len(ins) != self.n_in or len(outs) != self.n_out:
+            raise HipError(f"expected {self.n_in} input and {self.n_out} output pointers, got {len(ins)} and {len(outs)}")
+        ia, oa = self._in_arr, self._out_arr
+        for i, p in enumerate(ins):
+            ia[i] = p
+        for j, p in enumerate(outs):
+            oa[j] = p
+        return ia, oa
+
     def run(self, ins: Sequence[int], outs: Sequence[int], stream: int) -> None:
-        check(self._lib.tj_hip_program_run(self.handle, ptr_table(ins), ptr_table(outs), stream), "tj_hip_program_run")
+        check(self._lib.tj_hip_program_run(self.handle, *self._tables(ins, outs), stream), "tj_hip_program_run")
+
+    def run_tensors(self, ins, outs, stream: int) -> None:
+        """``run`` on tensors (their data pointers), the executor's per-call path."""
+        self.run([t.data_ptr() for t in ins], [t.data_ptr() for t in outs], stream)
+
+    def replay_tensors(self, ins, outs, stream: int) -> None:
+        self.replay([t.data_ptr() for t in ins], [t.data_ptr() for t in outs], stream)
 
     def run_static(self, ins: Sequence[int], outs: Sequence[int], stream: int) -> None:
         """``run`` with the intermediates in the library's static per-GPU arena (allocates
         nothing; rejects programs whose arena exceeds ``STATIC_ARENA_BYTES``)."""
-        check(self._lib.tj_hip_program_run_static(self.handle, ptr_table(ins), ptr_table(outs), stream),
+        check(self._lib.tj_hip_program_run_static(self.handle, *self._tables(ins, outs), stream),
               "tj_hip_program_run_static")
 
     def capture(self, ins: Sequence[int], outs: Sequence[int]) -> None:
-        check(self._lib.tj_hip_program_capture(self.handle, ptr_table(ins), ptr_table(outs)), "tj_hip_program_capture")
+        check(self._lib.tj_hip_program_capture(self.handle, *self._tables(ins, outs)), "tj_hip_program_capture")
 
     def replay(self, ins: Sequence[int], outs: Sequence[int], stream: int) -> None:
-        check(self._lib.tj_hip_program_replay(self.handle, ptr_table(ins), ptr_table(outs), stream),
+        check(self._lib.tj_hip_program_replay(self.handle, *self._tables(ins, outs), stream),
               "tj_hip_program_replay")
 
     def kernel_time(self, k: int, ins: Sequence[int], outs: Sequence[int], stream: int, warmup: int = 2,
                     iters: int = 10) -> float:
         ms = ctypes.c_float()
-        check(self._lib.tj_hip_kernel_time(self.handle, k, ptr_table(ins), ptr_table(outs), stream, warmup, iters,
+        check(self._lib.tj_hip_kernel_time(self.handle, k, *self._tables(ins, outs), stream, warmup, iters,
                                            ctypes.byref(ms)), "tj_hip_kernel_time")
         return ms.value
 

@@ -58,8 +58,9 @@ class BufferPool:
         self._held: dict[tuple, list[_Buffer]] = {}
 
     def take_output(self, shape, dtype: torch.dtype, device) -> torch.Tensor:
-        shape = tuple(int(d) for d in shape)
-        key = (shape, dtype, str(device))
+        if type(shape) is not tuple:
+            shape = tuple(int(d) for d in shape)
+        key = (shape, dtype, device)
         held = self._held.setdefault(key, [])
         for buf in held:
             if buf.unused():

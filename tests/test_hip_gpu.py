@@ -206,6 +206,33 @@ def test_softmax_layernorm_rmsnorm(shape):
     torch.testing.assert_close(ln, F.layer_norm(x, (n,), g, b), atol=1e-3, rtol=1e-3)
 
 
+@pytest.mark.parametrize("rows,n,dt", [
+    (1030, 768, torch.float32),      # one wave per row, 4 rows per workgroup, ragged last workgroup
+    (1025, 2048, torch.bfloat16),    # 4 KiB rows: the largest wave-per-row case, ragged
+    (1000, 520, torch.float16),      # too few rows for 4 per workgroup; 65 chunks: a part-used lane
+    (300, 1200, torch.float32),      # one chunk per lane, 300 of 320 lanes used
+    (257, 4096, torch.bfloat16),     # 8 KiB rows: 512 lanes x 1 chunk
+    (64, 4096, torch.float32),       # 16 KiB rows: 1024 lanes x 1 chunk
+    (16, 12288, torch.float32),      # longer rows: several chunks per lane
+])
+def test_row_layouts_vs_oracle(rows, n, dt):
+    """Every row layout (wave per row with a ragged last workgroup, one chunk per lane with idle
+    lanes, several chunks per lane) for LayerNorm / RMSNorm / softmax against the oracle, and
+    the row max, which a DPP all-reduce must give bit for bit."""
+    from tensorjit.backends.hip_kernels import row_shape
+
+    torch.manual_seed(0)
+    x = (torch.randn(rows, n, device=DEV) * 2).to(dt)
+    g = (1 + 0.1 * torch.randn(n, device=DEV)).to(dt)
+    vec = 16 // x.element_size() if n % (16 // x.element_size()) == 0 else 1
+    shape = row_shape(n, vec, False)
+    f, _ = check_vs_oracle(lambda t, w: (tj.layer_norm(t, w), tj.rms_norm(t, w), tj.softmax(t)), x, g)
+    launch = f.compiled(x, g).launches[0]
+    assert launch.meta["threads"] == shape.lanes and launch.meta["chunks"] == shape.chunks
+    m = tj.jit(lambda t: tj.max(t))
+    assert torch.equal(m(x), x.amax(-1))
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_row_kernels_low_precision_storage(dt):
     torch.manual_seed(0)
@@ -390,6 +417,29 @@ def test_mlp_matches_eager_with_and_without_graph(use_graph, monkeypatch):
     cp = f.compiled(x, g, w1, b1, w2, b2)
     assert cp.stats["graph_replays"] == (2 if use_graph else 0)
     assert cp.num_kernels == 3 and "__global__" in cp.source
+
+
+def test_native_program_counts_calls_and_owns_the_planned_arena(monkeypatch):
+    """The reference's native-runtime test (tests/test_runtime_and_planner.py:61-77) for the
+    hip executor: three kernels, eager-equal output, one native call per program call, and an
+    arena of exactly the planned intermediates (plus split-K workspaces) in one allocation."""
+    from tensorjit.backends import hip_backend as hb
+
+    monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "0")
+    torch.manual_seed(0)
+    x, g = torch.randn(64, 128, device=DEV), torch.ones(128, device=DEV)
+    w1, b1 = torch.randn(256, 128, device=DEV), torch.randn(256, device=DEV)
+    w2, b2 = torch.randn(128, 256, device=DEV), torch.randn(128, device=DEV)
+    f = tj.jit(MLP)
+    out = f(x, g, w1, b1, w2, b2)
+    cp = f.compiled(x, g, w1, b1, w2, b2)
+    ref = x + F.linear(F.gelu(F.linear(F.layer_norm(x, (128,), g), w1, b1)), w2, b2)
+    torch.testing.assert_close(out, ref, atol=2e-3, rtol=2e-3)
+    st = cp.native_stats()
+    assert cp.num_kernels == 3 and st["calls"] == 1 and st["graph_replays"] == 0 and st["host_us"] > 0
+    ptr, nbytes = cp.native.arena()
+    assert ptr != 0 and nbytes == cp.arena_bytes == hb.workspace_layout(cp.launches, cp.plan.arena_bytes)[1]
+    assert cp.plan.arena_bytes == 64 * 128 * 4 + 64 * 256 * 4     # LayerNorm and gelu outputs
 
 
 def test_graph_replay_is_the_default_from_twelve_launches(monkeypatch):
