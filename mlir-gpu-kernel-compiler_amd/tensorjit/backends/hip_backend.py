@@ -206,6 +206,15 @@ def compile_source(source: str, arch: str, name: str = "tensorjit.hip", target: 
 # executor
 # ---------------------------------------------------------------------------
 
+def _stream_of(device_index: int) -> int:
+    return torch.cuda.current_stream(device_index).cuda_stream
+
+
+# torch's current HIP stream of a device as a raw handle: the private accessor skips building
+# a Stream object (~1 us per call); torch builds without it use the public API
+_current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", _stream_of)
+
+
 # hipGraph replay by default from this many launches per call.  Measured on MI355X with the
 # reference's overhead chain (softmax(x @ w + 0.5) repeated): a direct hipModuleLaunchKernel
 # costs 2.3-2.8 us of host time, a graph launch 21-25 us plus ~0.6 us per kernel node, so
@@ -383,7 +392,7 @@ class HipProgram:
         ins = self._prepare(inputs)
         take, dev = self.pool.take_output, self._dev
         outs = [take(shape, dtype, dev) for shape, dtype in self._out_specs]
-        stream = torch._C._cuda_getCurrentRawStream(self.device_index)
+        stream = _current_stream(self.device_index)
         self.stats["calls"] += 1
         if self.launches:
             if self.use_graph:

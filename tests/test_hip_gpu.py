@@ -132,6 +132,26 @@ def test_int32_arithmetic_and_max_are_exact_below_2_24():
     assert torch.equal(m(x), x.amax(-1))
 
 
+def test_int32_matmul_and_sums_are_exact_below_2_24():
+    """int32 GEMMs (plain, transposed weight, batched, with an integer epilogue) and row sums run
+    in fp32, as the reference's float evaluation does; with every partial sum below 2^24 the
+    stored results equal integer arithmetic bit for bit."""
+    g = torch.Generator(device=DEV).manual_seed(0)
+    a = torch.randint(-8, 9, (130, 200), device=DEV, dtype=torch.int32, generator=g)
+    b = torch.randint(-8, 9, (200, 70), device=DEV, dtype=torch.int32, generator=g)
+    w = torch.randint(-8, 9, (90, 200), device=DEV, dtype=torch.int32, generator=g)
+    c = torch.randint(-100, 100, (90,), device=DEV, dtype=torch.int32, generator=g)
+    ref = lambda x, y: (x.cpu().long() @ y.cpu().long()).int()  # noqa: E731
+    assert torch.equal(tj.jit(lambda x, y: tj.matmul(x, y))(a, b).cpu(), ref(a, b))
+    assert torch.equal(tj.jit(lambda x, y, z: tj.linear(x, y, z) * 3)(a, w, c).cpu(), (ref(a, w.t()) + c.cpu()) * 3)
+    ab = torch.randint(-8, 9, (3, 40, 64), device=DEV, dtype=torch.int32, generator=g)
+    bb = torch.randint(-8, 9, (3, 64, 24), device=DEV, dtype=torch.int32, generator=g)
+    got = tj.jit(lambda x, y: tj.matmul(x, y))(ab, bb).cpu()
+    assert torch.equal(got, torch.stack([ref(ab[i], bb[i]) for i in range(3)]))
+    rows = torch.randint(-1000, 1000, (64, 5000), device=DEV, dtype=torch.int32, generator=g)
+    assert torch.equal(tj.jit(lambda x: tj.sum(x))(rows).cpu(), rows.cpu().long().sum(-1).int())
+
+
 def test_int32_division_is_exact():
     """int32 a / b evaluates as a correctly rounded fp32 quotient truncated on store (the
     reference's expression is a plain ``/``).  For |a| < 2^24 the rounded quotient never
