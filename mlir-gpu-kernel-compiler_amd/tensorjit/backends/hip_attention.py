@@ -45,15 +45,20 @@ def _scalar_const(n: Node) -> float | None:
 
 
 def _score_scale(k1: Kernel) -> float | None:
-    """The scale of ``k1 = matmul(q, k, trans_b)`` followed by at most one scalar multiply."""
+    """The scale of ``k1 = matmul(q, k, trans_b)`` followed by at most one scalar multiply
+    (either operand order) or one division of the scores by a nonzero scalar
+    (``q @ kᵀ / sqrt(d)``, scale ``1 / c``; ``c / scores`` is not a scale)."""
     mm = k1.anchor
     if k1.kind != "matmul" or not mm.attrs.get("trans_b"):
         return None
     if k1.nodes == [mm]:
         return 1.0
-    if len(k1.nodes) != 2 or k1.nodes[1].op != "mul":
+    if len(k1.nodes) != 2 or k1.nodes[1].op not in ("mul", "div"):
         return None
     a, b = k1.nodes[1].inputs
+    if k1.nodes[1].op == "div":
+        c = _scalar_const(b) if a is mm else None
+        return None if not c else 1.0 / c
     other = b if a is mm else a if b is mm else None
     return None if other is None else _scalar_const(other)
 

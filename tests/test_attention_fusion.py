@@ -41,6 +41,24 @@ def test_unscaled_and_differently_sized_value_heads():
     assert [k.kind for k in f.kernels] == ["attention"] and f.kernels[0].attn["scale"] == 1.0
 
 
+@pytest.mark.parametrize("form,scale", [
+    (lambda s: s / 8.0, 0.125),                 # q @ kᵀ / sqrt(d)
+    (lambda s: s / 3.0, 1.0 / 3.0),
+    (lambda s: 0.25 * s, 0.25),                 # constant on the left of the multiply
+])
+def test_scale_written_as_division_or_left_multiply(form, scale):
+    fn = lambda q, k, v: tj.matmul(tj.softmax(form(tj.matmul(q, tj.transpose(k, -1, -2)))), v)  # noqa: E731
+    f = fuse_attention(lowered(fn, QKV))
+    assert [k.kind for k in f.kernels] == ["attention"] and f.kernels[0].attn["scale"] == scale
+
+
+@pytest.mark.parametrize("form", [lambda s: 8.0 / s, lambda s: s / 0.0], ids=["constant_over_scores", "by_zero"])
+def test_divisions_that_are_not_a_scale_stay_unfused(form):
+    fn = lambda q, k, v: tj.matmul(tj.softmax(form(tj.matmul(q, tj.transpose(k, -1, -2)))), v)  # noqa: E731
+    f = fuse_attention(lowered(fn, QKV))
+    assert all(k.kind != "attention" for k in f.kernels)
+
+
 @pytest.mark.parametrize("case", ["fp32", "probs_returned", "scores_reused", "head_dim_8", "extra_epilogue"])
 def test_chains_that_must_stay_unfused(case):
     if case == "fp32":

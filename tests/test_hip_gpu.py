@@ -399,6 +399,20 @@ def test_fused_attention_reads_and_writes_head_interleaved_layout(B, S, Dm, head
     close_lowp(out, ref, tol=2e-2)
 
 
+def test_fused_attention_scale_written_as_division():
+    """``q @ kᵀ / sqrt(d)`` with a head dim whose square root is not a power of two (the
+    kernel multiplies by the rounded reciprocal; the oracle divides), against the fp32 oracle."""
+    torch.manual_seed(2)
+    q, k, v = [torch.randn(1, 3, 200, 96, device=DEV).bfloat16() for _ in range(3)]
+    fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) / 96 ** 0.5), v)  # noqa: E731
+    print("attention / sqrt(96)", flush=True)
+    f = tj.jit(fn)
+    out = f(q, k, v)
+    assert f.compiled(q, k, v).num_kernels == 1
+    (ref,) = oracle.run(fn, *[t.float().cpu() for t in (q, k, v)])
+    close_lowp(out, ref, tol=2e-2)
+
+
 def test_fused_attention_large_logits_and_unit_scale():
     """Scores of magnitude ~100 (online max subtraction must keep exp2 in range) and
     no scale multiply in the chain."""
