@@ -212,13 +212,25 @@ def kernel_ms(f, args, k=None, iters=20):
     return sum(cp.kernel_time_ms(i, *args, warmup=3, iters=iters) for i in ks)
 
 
-def kernel_ms_settled(cp, args, k=None, rounds=3, iters=10):
-    """Best of ``rounds`` averages of ``iters`` launches after a warm-up long enough for
-    the clocks of an MFMA-bound kernel to settle (a cold first average reads 10-20% slow);
-    ``k=None`` sums all the program's launches."""
+def kernel_ms_settled(cp, args, k=None, rounds=3, iters=10, settle_s=0.5):
+    """Best of ``rounds`` averages of ``iters`` launches, once the clocks have settled:
+    averages of ``iters`` back-to-back launches are taken until two in a row agree within
+    1% (or ``settle_s`` of device time has passed).  An MFMA-bound kernel needs dozens of
+    launches after a cold start: config 4's GEMM reads 868, 757 and 726 us in its first
+    three averages of 10 and 697-703 us from then on.  ``k=None`` sums all the program's
+    launches."""
     ks = range(len(cp.launches)) if k is None else [k]
-    return sum(min(cp.kernel_time_ms(i, *args, warmup=10 if r == 0 else 2, iters=iters) for r in range(rounds))
-               for i in ks)
+    total = 0.0
+    for i in ks:
+        prev, spent = None, 0.0
+        while spent < settle_s * 1e3:
+            ms = cp.kernel_time_ms(i, *args, warmup=0, iters=iters)
+            spent += ms * iters
+            if prev is not None and abs(ms - prev) <= 0.01 * prev:
+                break
+            prev = ms
+        total += min(cp.kernel_time_ms(i, *args, warmup=1, iters=iters) for _ in range(rounds))
+    return total
 
 
 def load_traffic(workload: str):

@@ -64,11 +64,38 @@ def compute_dtype(mm: Node) -> DType:
     return DType.f32
 
 
+def batch_folds_into_m(mm: Node) -> bool:
+    """Is ``mm`` one 2-D GEMM over (batch x M) rows: A contiguous across its batch dims
+    and B shared by every batch entry (a projection of a [B, S, D] activation)?"""
+    batch_shape = tuple(mm.shape[:-2])
+    if not batch_shape:
+        return True
+    a, b = mm.inputs
+    M, _, K, _ = matmul_dims(mm)
+    want = tuple(s * M * K for s in contiguous_strides(batch_shape))
+    return (tuple(a.shape[:-2]) == batch_shape and _batch_strides(a, batch_shape) == want
+            and all(s == 0 for s in _batch_strides(b, batch_shape)))
+
+
+def _folded_strides(st: tuple[int, ...], batch_shape: tuple, M: int) -> tuple[int, int] | None:
+    """An epilogue input's (row, column) strides over the folded (batch x M, N) output,
+    given its strides over (batch..., i, j); None when it does not fold."""
+    *sb, si, sj = st
+    inner = M
+    for d in range(len(batch_shape) - 1, -1, -1):
+        if sb[d] != si * inner:
+            return None
+        inner *= batch_shape[d]
+    return si, sj
+
+
 def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
     """Is ``cfg`` a valid tiling for operand type ``dt`` (and for matmul ``mm`` if given)?"""
     if (dt, cfg.MI) not in MFMA:
         return False
     _, ki, _, _, _ = MFMA[(dt, cfg.MI)]
+    if cfg.PERSIST and (not cfg.DIRECT or cfg.KSPLIT > 1):
+        return False
     if cfg.KSPLIT > 1:
         # K split over workgroups: the plain double-buffered schedule or the skinny
         # kernel, every split an equal whole number of K steps (no K edge inside a split)
@@ -107,6 +134,18 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
             # buffer descriptors: byte offsets (rows padded to the tile) and ranges in int32
             ok = (tb and K % 64 == 0 and a.dtype == b.dtype == dt
                   and (M + cfg.TM) * K * 2 < 2**31 and (N + cfg.TN) * K * 2 < 2**31)
+        if ok and cfg.PERSIST:
+            # persistent tile loop: 16x16x32 MFMAs, 4 waves, a multiple of 8 workgroups
+            # (XCD order), an epilogue staging array of its own beside the two stages,
+            # whole tiles (no edges), an even number of at least 4 K tiles, no batch
+            cols = cfg.TN // cfg.WN
+            ok = (cfg.MI == 16 and cfg.num_warps == 4 and cfg.PERSIST % XCDS == 0 and cols >= 64
+                  and 2 * (cfg.TM + cfg.TN) * 128 + 4 * 16 * cols * 4 <= 160 * 1024)
+            if ok and mm is not None:
+                M, N, K, _ = matmul_dims(mm)
+                M *= math.prod(mm.shape[:-2])
+                ok = (batch_folds_into_m(mm) and M % cfg.TM == 0 and N % cfg.TN == 0 and K % 128 == 0
+                      and K >= 256 and M * N < 2**31 and M * K * 2 < 2**31)
         return ok
     if cfg.PINGPONG:
         ks = cfg.TK // ki
@@ -300,10 +339,13 @@ def _batch_strides(t: Node, batch_shape: tuple) -> tuple[int, ...]:
     return tuple(st)
 
 
-def _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, ve, cs) -> list[str]:
+def _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, ve, cs,
+               pre: dict | None = None, strides: dict | None = None) -> list[str]:
     """Epilogue of one run of ``ve`` consecutive outputs at (i, j) (both defined by the
     caller), the accumulators being ``cs`` with ``q`` the position in the run: extra
-    inputs loaded as vectors where contiguous, outputs stored as vectors."""
+    inputs loaded as vectors where contiguous (or taken from the caller's preloaded
+    arrays ``pre[id(input)]``), outputs stored as vectors.  ``strides[id(input)]``
+    overrides an input's strides over (batch..., i, j)."""
     L = []
     full_idx = list(bidx) + ["i", "j"]
     L.append(f"    float acc_v[{ve}];")
@@ -311,8 +353,11 @@ def _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, 
     L.append(f"    for (int q = 0; q < {ve}; ++q) acc_v[q] = {cs};")
     local = {id(mm): "acc_v[q]"}
     for n in epi_inputs:
+        if pre and id(n) in pre:
+            local[id(n)] = f"{pre[id(n)]}[q]"
+            continue
         consumer = next((c for c in epilogue if n in c.inputs), epilogue[0] if epilogue else mm)
-        st = access_strides(n, consumer, out_shape)
+        st = strides[id(n)] if strides else access_strides(n, consumer, out_shape)
         terms = [v if s_ == 1 else f"{v} * {s_}u" for v, s_ in zip(full_idx, st) if s_]
         off = " + ".join(terms) if terms else "0u"
         nm = g.names[id(n)]
@@ -444,27 +489,35 @@ def direct_staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx
 XCDS = 8   # MI355X: workgroups are dispatched round-robin over 8 XCDs, each with its own L2
 
 
-def tile_order_lines(ntm: int, ntn: int, group_m: int, BM: int, BN: int) -> list[str]:
-    """(m0, n0) of this workgroup.
+def tile_order_lines(ntm: int, ntn: int, group_m: int, BM: int, BN: int, vid: str | None = None,
+                     names: tuple[str, str] = ("m0", "n0"), sfx: str = "") -> list[str]:
+    """(m0, n0) of this workgroup's output tile.
 
     The grid is launched as (ntn, ntm).  Workgroup ``w`` (x-fastest linear id) runs on XCD
     ``w % 8``; re-numbering tiles so that XCD ``x`` owns the contiguous range
     ``[x*T/8, (x+1)*T/8)`` of a grouped order (``group_m`` tile rows walked column by
     column) makes the workgroups that share an L2 work on a compact block of tiles, so
     they share A row panels and B column panels in that L2 instead of each XCD streaming
-    every panel from HBM / MALL."""
+    every panel from HBM / MALL.  ``vid``: the linear id as an expression instead (a
+    persistent workgroup's virtual id, ``blockIdx.x + i * G`` with G a multiple of 8, so
+    it stays on its XCD); ``names`` / ``sfx`` name the results and temporaries."""
     T = ntm * ntn
+    m, n = names
     if group_m <= 0 or T < 2 * XCDS or T % XCDS:
-        return [f"  const unsigned int m0 = blockIdx.y * {BM}u, n0 = blockIdx.x * {BN}u;"]
+        if vid is None:
+            return [f"  const unsigned int {m} = blockIdx.y * {BM}u, {n} = blockIdx.x * {BN}u;"]
+        return [f"  const unsigned int {m} = ({vid}) / {ntn}u * {BM}u, {n} = ({vid}) % {ntn}u * {BN}u;"]
     gm = min(group_m, ntm)
     per_group = gm * ntn
+    w, t, g, first, gsz, r = (f"{v}{sfx}_" for v in ("w", "t", "g", "first", "gsz", "r"))
+    wid = f"blockIdx.y * {ntn}u + blockIdx.x" if vid is None else vid
     return [
-        f"  const unsigned int w_ = blockIdx.y * {ntn}u + blockIdx.x;",
-        f"  const unsigned int t_ = (w_ % {XCDS}u) * {T // XCDS}u + w_ / {XCDS}u;",
-        f"  const unsigned int g_ = t_ / {per_group}u, first_ = g_ * {gm}u;",
-        f"  const unsigned int gsz_ = ({ntm}u - first_) < {gm}u ? ({ntm}u - first_) : {gm}u;",
-        f"  const unsigned int r_ = t_ % {per_group}u;",
-        f"  const unsigned int m0 = (first_ + r_ % gsz_) * {BM}u, n0 = (r_ / gsz_) * {BN}u;",
+        f"  const unsigned int {w} = {wid};",
+        f"  const unsigned int {t} = ({w} % {XCDS}u) * {T // XCDS}u + {w} / {XCDS}u;",
+        f"  const unsigned int {g} = {t} / {per_group}u, {first} = {g} * {gm}u;",
+        f"  const unsigned int {gsz} = ({ntm}u - {first}) < {gm}u ? ({ntm}u - {first}) : {gm}u;",
+        f"  const unsigned int {r} = {t} % {per_group}u;",
+        f"  const unsigned int {m} = ({first} + {r} % {gsz}) * {BM}u, {n} = ({r} / {gsz}) * {BN}u;",
     ]
 
 
@@ -505,6 +558,18 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     epilogue = [n for n in k.nodes if n is not mm]
     idx_t = "unsigned long" if batch * M * N >= 2**31 or batch * max(M, N) * K >= 2**31 else "unsigned int"
 
+    epi_st = None
+    epi_inputs = [i for i in k.inputs if i is not a and i is not b]
+    if cfg.PERSIST:
+        # one 2-D GEMM over (batch x M) rows; an epilogue input that does not fold the same
+        # way (or outputs of mixed dtypes) keeps the one-tile-per-workgroup kernel
+        epi_st = {}
+        for n in epi_inputs:
+            consumer = next((c for c in epilogue if n in c.inputs), epilogue[0] if epilogue else mm)
+            epi_st[id(n)] = _folded_strides(access_strides(n, consumer, out_shape), batch_shape, M)
+        if any(v is None for v in epi_st.values()) or any(o.dtype != k.outputs[0].dtype for o in k.outputs):
+            epi_st = None
+
     S = cfg.KSPLIT
     ws_param = ", float* __restrict__ ws_p" if S > 1 else ""
     L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {fname}({g.params()}{ws_param}) {{']
@@ -517,9 +582,10 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     L.append("  const unsigned int tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;")
     L.append(f"  const unsigned int wm = wave / {WN}u, wn = wave % {WN}u;")
     ntm, ntn = -(-M // BM), -(-N // BN)
-    L += tile_order_lines(ntm, ntn, cfg.GROUP_M, BM, BN)
-    # batch offsets
-    if batch_shape:
+    if epi_st is None:
+        L += tile_order_lines(ntm, ntn, cfg.GROUP_M, BM, BN)
+    # batch offsets (none when the batch folds into the rows of a persistent kernel)
+    if batch_shape and epi_st is None:
         L.append(f"  const {idx_t} bi = blockIdx.z / {S}u;" if S > 1 else f"  const {idx_t} bi = blockIdx.z;")
         bst = contiguous_strides(batch_shape)
         bidx = []
@@ -546,6 +612,22 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
         L.append(f"  const {CTYPE[a.dtype]}* __restrict__ Ab = {A}_p;")
         L.append(f"  const {CTYPE[b.dtype]}* __restrict__ Bb = {B}_p;")
 
+    if epi_st is not None:
+        M *= batch
+        ntm = M // BM
+        pre, body, stores, early = persistent_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, M, N, BM,
+                                                             BN, WM, WN, TMW, TNW, epi_st)
+        T = ntm * ntn
+        G = min(cfg.PERSIST, T)
+        persist = {"G": G, "T": T, "K": K, "BM": BM, "BN": BN, "ntm": ntm, "ntn": ntn, "group_m": cfg.GROUP_M,
+                   "pre": pre, "epi": body, "stores": stores, "k1_early": early}
+        L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persist)
+        L.append("}")
+        lds = 2 * (BM + BN) * 128 + cfg.num_warps * 16 * TNW * MI * 4
+        meta = {"family": "matmul", "config": cfg.as_dict(), "dtype": dt.value, "M": M // batch, "N": N, "K": K,
+                "batch": batch, "trans_b": tb, "lds_bytes": lds, "flops": 2.0 * M * N * K,
+                "epilogue": "lds-staged", "persistent": G}
+        return "\n".join(L), Launch(fname, (G, 1, 1), (THREADS, 1, 1), 0, meta)
     if cfg.DIRECT:
         L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin)
         return _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW,
@@ -985,7 +1067,14 @@ def _vmcnt_only(n: int) -> str:
     return hex((n & 15) | ((n >> 4) << 14) | 0x0F70)
 
 
-def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> list[str]:
+def _lgkmcnt_only(n: int) -> str:
+    """s_waitcnt immediate for gfx9 that waits until at most ``n`` LDS / scalar-memory
+    operations are outstanding (lgkmcnt in bits 11:8; vmcnt and expcnt at their maxima)."""
+    assert 0 <= n < 16
+    return hex(0xC07F | (n << 8))
+
+
+def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persist: dict | None = None) -> list[str]:
     """Main loop for one wave per SIMD with tiles loaded straight into LDS (``DIRECT``).
 
     ``buffer_load_dwordx4 ... lds`` moves 16 bytes per lane from HBM/L2 into LDS
@@ -1016,7 +1105,15 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
     sub-step's last MFMA on that row, so only B is double-buffered: 96 fragment VGPRs
     instead of 128).  Each memory instruction has a fixed slot after one MFMA: DMA
     loads one per 64 MFMA cycles of a wave (about what the texture unit passes for
-    four waves at ~16 cycles per 1 KiB load), fragment reads in the slots between."""
+    four waves at ~16 cycles per 1 KiB load), fragment reads in the slots between.
+
+    ``persist`` (``cfg.PERSIST`` workgroups, one per CU, looping over the output tiles;
+    emitted by ``persistent_direct_lines``): the operand descriptors move with the
+    tile, the next tile's first K tile is loaded into stage 0 from tile KT-2's region B
+    on (stage 0 is free from that tile's barrier, as for any tile kt+2), its second
+    into stage 1 once the last tile's reads are done, and the epilogue stages through
+    an LDS array of its own, so the next tile's MFMAs start without a load wait and the
+    output stores drain under them."""
     nw = cfg.num_warps
     MI = cfg.MI
     KI = 16 if MI == 32 else 32               # K per MFMA
@@ -1034,7 +1131,10 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
     L = [f"  __shared__ __attribute__((aligned(1024))) char As0[{BM * 128}];",
          f"  __shared__ __attribute__((aligned(1024))) char As1[{BM * 128}];",
          f"  __shared__ __attribute__((aligned(1024))) char Bs0[{BN * 128}];",
-         f"  __shared__ __attribute__((aligned(1024))) char Bs1[{BN * 128}];",
+         f"  __shared__ __attribute__((aligned(1024))) char Bs1[{BN * 128}];"]
+    if persist:
+        L.append(f"  __shared__ __attribute__((aligned(16))) float Cs[{nw}][{16 * TNW * MI}];")
+    L += [
          "  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave);",
          "  const unsigned int drow = lane >> 3;",
          f"  tj_f32x{NACC} acc[{TMW}][{TNW}];",
@@ -1074,21 +1174,27 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
     # past M or N (no clamping).  The global_load_lds form would also work, but the
     # compiler treats it as a flat access that may touch LDS and then waits for every
     # outstanding LDS read (lgkmcnt 0) wherever one fragment is needed.
-    L.append(f"  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, {M * K * 2}, 0x00020000);")
-    L.append(f"  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, {N * K * 2}, 0x00020000);")
+    if not persist:
+        L.append(f"  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, {M * K * 2}, 0x00020000);")
+        L.append(f"  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, {N * K * 2}, 0x00020000);")
+    # persistent: each tile's descriptors start at its first row, so the lane offsets
+    # are the same for every tile
     for op, cnt, rows in (("A", a_cnt, "m0"), ("B", b_cnt, "n0")):
         L.append(f"  unsigned int vo{op}[{cnt}];")
+        base = "" if persist else f"{rows} + "
         for i in range(cnt):
             q = f"({i * nw}u + wv)"
-            L.append(f"  vo{op}[{i}] = (({rows} + {q} * 8u + drow) * {K}u + ((lane & 7u) ^ drow ^ ({q} & 3u)) * 8u) * 2u;")
+            L.append(f"  vo{op}[{i}] = (({base}{q} * 8u + drow) * {K}u + ((lane & 7u) ^ drow ^ ({q} & 3u)) * 8u) * 2u;")
 
-    def dma(kt: str, stage: int) -> list[str]:
-        """The DMA loads of tile ``kt`` into ``stage``, one statement per load."""
+    def dma(kt: str, stage: int, nxt: bool = False) -> list[str]:
+        """The DMA loads of tile ``kt`` into ``stage``, one statement per load (``nxt``:
+        K tile ``kt`` of the next output tile, through its descriptors)."""
         out = []
         for op, cnt in (("A", a_cnt), ("B", b_cnt)):
+            rs = f"rs{op}n" if nxt else f"rs{op}"
             for i in range(cnt):
                 q = f"({i * nw}u + wv)"
-                out.append(f"__builtin_amdgcn_raw_ptr_buffer_load_lds(rs{op}, (__attribute__((address_space(3))) void*)"
+                out.append(f"__builtin_amdgcn_raw_ptr_buffer_load_lds({rs}, (__attribute__((address_space(3))) void*)"
                            f"({op}s{stage} + {q} * 1024u), 16, vo{op}[{i}], (int)(({kt}) * 128u), 0, 0);")
         return out
 
@@ -1138,26 +1244,42 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
     n_b = min(split[0], n_batch)                  # loads issued in region B
     a_steps = max(1, min(split[1], KS - 1))      # region-A sub-steps taking the rest
 
-    def tile(kt: str, stage: int, carry: bool, do_load: bool, last: bool, ind: str) -> list[str]:
+    def tile(kt: str, stage: int, carry: bool, do_load: bool, last: bool, ind: str, next0: str = "",
+             pub: list[str] | None = None) -> list[str]:
         """Tile kt from LDS stage ``stage``.  The loads of tile kt+2 (into this stage,
         released by this tile's barrier) start in region B; ``carry``: the rest of tile
         kt+1's loads (begun in the previous tile's region B) go into region A here,
-        still ahead of the barrier that publishes tile kt+1.  ``last``: no tile follows."""
+        still ahead of the barrier that publishes tile kt+1.  ``last``: no tile follows.
+        ``next0`` (persistent): "load" puts the first loads of the next output tile's K
+        tile 0 into region B (in place of tile kt+2's), "carry" the rest into region A.
+        ``pub``: the publishing wait and barrier, if not the default."""
         out = []
-        rest = dma(f"({kt}) + 1", 1 - stage)[n_b:] if carry else []
+        if carry:
+            rest = dma(f"({kt}) + 1", 1 - stage)[n_b:]
+        elif next0 == "carry":
+            rest = dma("0", 1 - stage, nxt=True)[n_b:]
+        else:
+            rest = []
         # region A: sub-steps 0 .. KS-2 with the fragment reads of the next sub-steps
         for ks in range(KS - 1):
             mine = rest[len(rest) * ks // a_steps:len(rest) * (ks + 1) // a_steps] if ks < a_steps else []
             out += region(ks % 2, frag_reads((ks + 1) % 2, stage, ks + 1), mine)
         if not last:
-            out += publish + ["__builtin_amdgcn_sched_barrier(0);"]
+            out += (pub or publish) + ["__builtin_amdgcn_sched_barrier(0);"]
         # region B: last sub-step, with the first fragments of tile kt+1 and the first
         # loads of tile kt+2
         reads = frag_reads(0, 1 - stage, 0) if not last else []
-        loads = dma(f"({kt}) + 2", stage)[:n_b] if do_load else []
+        if do_load:
+            loads = dma(f"({kt}) + 2", stage)[:n_b]
+        elif next0 == "load":
+            loads = dma("0", stage, nxt=True)[:n_b]
+        else:
+            loads = []
         out += region((KS - 1) % 2, reads, loads)
         return [ind + x for x in out]
 
+    if persist:
+        return L + persistent_direct_lines(persist, KT, n_batch, dma, frag_reads, tile, opvec, MI, TMW, TNW)
     # prologue: tiles 0 and 1 in flight, wait for tile 0 only (the 2nd batch may
     # stay outstanding: vmcnt <= its load count)
     L += ["  " + x for x in dma("0", 0)]
@@ -1185,6 +1307,145 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin) -> lis
         L += tile(str(kt), kt % 2, kt + 1 < KT, kt + 2 < KT, kt + 1 == KT, "    ")
         L.append("  }")
     return L
+
+
+def persistent_direct_lines(p: dict, KT: int, n_batch: int, dma, frag_reads, tile, opvec: str, MI: int, TMW: int,
+                            TNW: int) -> list[str]:
+    """Tile loop of the persistent direct-to-LDS kernel (after the shared set-up of
+    ``direct_loop_lines``).
+
+    Workgroup b runs virtual tiles b, b + G, b + 2G, ... (G a multiple of 8, so every
+    one of them stays on b's XCD in the XCD-aware order).  Per tile: the descriptors of
+    this tile and of the next one (the same tile again after the last, so the
+    prefetches stay in bounds), the K loop -- whose tile KT-2 starts, and KT-1 finishes,
+    the loads of the next tile's K tile 0 into stage 0 -- a barrier (the last K tile's
+    reads are done), the next tile's K tile 1 into stage 1, and the epilogue through
+    the ``Cs`` array.  vmcnt counts a wave's vector-memory instructions and completes
+    them in issue order, so the waits name how many of the youngest may stay
+    outstanding: before the next tile's first fragment reads, its K tile 1 and at
+    least ``p["stores"]`` epilogue stores (issued after K tile 0); at its first
+    barrier, the epilogue stores only (issued after K tile 1; when the epilogue still
+    loads inputs, K tile 1 is issued after it and that barrier waits for everything).
+    ``p["pre"]`` loads the epilogue's row-invariant inputs before K tile 1 is issued,
+    so the epilogue itself waits on no load behind it."""
+    G, T, K, BM, BN = p["G"], p["T"], p["K"], p["BM"], p["BN"]
+    early = p["k1_early"]
+    x0 = min(63, n_batch + p["stores"])
+    x1 = min(63, p["stores"]) if early else 0
+    ntm, ntn, gm = p["ntm"], p["ntn"], p["group_m"]
+
+    def rsrc(name: str, base: str, row0: str, rows: int) -> str:
+        return (f"const __amdgpu_buffer_rsrc_t {name} = __builtin_amdgcn_make_buffer_rsrc("
+                f"(void*)({base} + (unsigned long)({row0}) * {K}u), (short)0, {rows * K * 2}, 0x00020000);")
+
+    L = tile_order_lines(ntm, ntn, gm, BM, BN, vid="blockIdx.x", names=("m0i", "n0i"), sfx="i")
+    L += ["  unsigned int v = blockIdx.x, m0 = m0i, n0 = n0i;",
+          "  {",
+          "    " + rsrc("rsA", "Ab", "m0", BM),
+          "    " + rsrc("rsB", "Bb", "n0", BN)]
+    L += ["    " + x for x in dma("0", 0) + dma("1", 1)]
+    L += [f"    __builtin_amdgcn_s_waitcnt({_vmcnt_only(n_batch)});", "    __syncthreads();", "  }"]
+    L.append(f"  {opvec} fa[{TMW}], fb[2][{TNW}];")
+    L.append("  for (unsigned int it = 0u;; ++it) {")
+    ind = "    "
+    L.append(f"{ind}const unsigned int vn = v + {G}u < {T}u ? v + {G}u : v;")
+    L += [ind + x.strip() for x in tile_order_lines(ntm, ntn, gm, BM, BN, vid="vn", names=("mn", "nn"), sfx="n")]
+    L += [ind + rsrc("rsA", "Ab", "m0", BM), ind + rsrc("rsB", "Bb", "n0", BN),
+          ind + rsrc("rsAn", "Ab", "mn", BM), ind + rsrc("rsBn", "Bb", "nn", BN)]
+    L += [f"{ind}#pragma unroll", f"{ind}for (int x = 0; x < {TMW}; ++x)", f"{ind}#pragma unroll",
+          f"{ind}  for (int y = 0; y < {TNW}; ++y) acc[x][y] = (tj_f32x{MI * MI // 64})(0.0f);"]
+    L += [ind + r for _, r in frag_reads(0, 0, 0)]
+    pub0 = [f"if (it == 0u) __builtin_amdgcn_s_waitcnt({_vmcnt_only(0)}); "
+            f"else __builtin_amdgcn_s_waitcnt({_vmcnt_only(x1)});", "__syncthreads();"]
+    L.append(f"{ind}{{  // K tile 0")
+    L += tile("0", 0, False, 2 < KT, False, ind + "  ", pub=pub0)
+    L.append(f"{ind}}}")
+    npair = max(0, KT - 3) // 2
+    if npair:
+        L.append(f"{ind}for (unsigned int kt = 1; kt < {1 + 2 * npair}u; kt += 2) {{")
+        L += tile("kt", 1, True, True, False, ind + "  ")
+        L += tile("kt + 1u", 0, True, True, False, ind + "  ")
+        L.append(f"{ind}}}")
+    for kt in range(1 + 2 * npair, KT):
+        nxt = "load" if kt == KT - 2 else "carry" if kt == KT - 1 else ""
+        L.append(f"{ind}{{  // K tile {kt}")
+        L += tile(str(kt), kt % 2, kt + 1 < KT, kt + 2 < KT, kt + 1 == KT, ind + "  ", next0=nxt)
+        L.append(f"{ind}}}")
+    # every wave's reads of the last K tile (stage 1) are done; a plain barrier, since the
+    # workgroup fence of __syncthreads would also wait for the next tile's K tile 0
+    L += [f"{ind}__builtin_amdgcn_sched_barrier(0);", f"{ind}__builtin_amdgcn_s_waitcnt({_lgkmcnt_only(0)});",
+          f"{ind}__builtin_amdgcn_s_barrier();", f"{ind}__builtin_amdgcn_sched_barrier(0);"]
+    k1 = [ind + x for x in dma("1", 1, nxt=True)] + [f"{ind}__builtin_amdgcn_sched_barrier(0);"]
+    L += [ind + x.strip() for x in p["pre"]]
+    if p["pre"]:
+        L.append(f"{ind}__builtin_amdgcn_sched_barrier(0);")
+    if early:
+        L += k1
+    L += p["epi"]
+    if not early:
+        L += k1
+    L += [f"{ind}if (vn == v) break;",
+          f"{ind}v = vn; m0 = mn; n0 = nn;",
+          f"{ind}__builtin_amdgcn_s_waitcnt({_vmcnt_only(x0)});",
+          f"{ind}__syncthreads();",
+          "  }",
+          # the last tile's prefetches (of itself again) land before the workgroup's LDS is released
+          f"  __builtin_amdgcn_s_waitcnt({_vmcnt_only(0)});"]
+    return L
+
+
+def persistent_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, M, N, BM, BN, WM, WN, TMW, TNW,
+                              epi_st: dict) -> tuple[list[str], list[str], int, bool]:
+    """Epilogue of the persistent direct kernel: (loads of row-invariant inputs, body,
+    minimum number of store instructions per wave, whether every input is preloaded).
+
+    Wave w stages its sub-tile through ``Cs[w]`` one 16-row MFMA block at a time (a
+    wave's LDS accesses complete in order: no barrier).  The rows of a block are
+    ``cols`` floats apart, a multiple of the 64 banks, so float ``c`` of row ``r`` sits
+    at column ``c ^ ((r >> 2) << 4)``: the four row groups a lane writes from land on
+    four different 16-bank ranges, and the 16-byte runs read back stay contiguous."""
+    MI = 16
+    out_dt = k.outputs[0].dtype
+    ve = 16 // out_dt.itemsize
+    cols, rows_w = TNW * MI, TMW * MI
+    per_row = cols // ve
+    assert 64 % per_row == 0 and cols >= 64
+    jcol = f"n0 + wn * {BN // WN}u + (lane % {per_row}u) * {ve}u"
+    # the row-invariant inputs are loaded raw here and converted in the body, after the
+    # next tile's K tile 1 is issued: a conversion waits for its load, and vmcnt would
+    # make that wait cover every older load as well
+    pre_lines, conv, pre = [], [], {}
+    for n in epi_inputs:
+        si, sj = epi_st[id(n)]
+        if si != 0:
+            continue
+        nm = g.names[id(n)]
+        conv.append(f"float {nm}_pre[{ve}];")
+        if sj == 1 and 16 // n.dtype.itemsize == ve:
+            pre_lines.append(f"const tj_u32x4 {nm}_raw = *(const tj_u32x4*)({nm}_p + ({jcol}));")
+            conv.append(f"tj_unpackv({nm}_raw, {nm}_p, {nm}_pre);")
+        else:
+            pre_lines.append(f"{CTYPE[n.dtype]} {nm}_raw[{ve}];")
+            pre_lines.append(f"for (int q = 0; q < {ve}; ++q) {nm}_raw[q] = {nm}_p[({jcol}) * {sj}u + q * {sj}u];")
+            conv.append(f"for (int q = 0; q < {ve}; ++q) {nm}_pre[q] = tj_ld({nm}_raw[q]);")
+        pre[id(n)] = f"{nm}_pre"
+    ind = "    "
+    L = [ind + x for x in conv] + [f"{ind}float* __restrict__ Cw = Cs[wave];"]
+    for x in range(TMW):
+        L += [f"{ind}#pragma unroll", f"{ind}for (int y = 0; y < {TNW}; ++y)", f"{ind}#pragma unroll",
+              f"{ind}  for (int r = 0; r < 4; ++r)",
+              f"{ind}    Cw[((lane / 16u) * 4u + r) * {cols}u + ((y * 16u + lane % 16u) ^ ((lane / 16u) << 4))] = "
+              f"acc[{x}][y][r];"]
+        L.append(f"{ind}#pragma unroll")
+        L.append(f"{ind}for (unsigned int c = lane; c < {16 * per_row}u; c += 64u) {{")
+        L.append(f"{ind}  const unsigned int lr = c / {per_row}u, cc = (c % {per_row}u) * {ve}u;")
+        L.append(f"{ind}  const unsigned int i = m0 + wm * {BM // WM}u + {x * 16}u + lr;")
+        L.append(f"{ind}  const unsigned int j = n0 + wn * {BN // WN}u + cc;")
+        L += [ind + x_ for x_ in _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, [], (), M, N, ve,
+                                            f"Cw[lr * {cols}u + ((cc ^ ((lr >> 2) << 4)) + q)]", pre, epi_st)]
+        L.append(f"{ind}}}")
+    stores = len(k.outputs) * rows_w * cols * out_dt.itemsize // 1024
+    return pre_lines, L, stores, len(pre) == len(epi_inputs)
 
 
 def _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW, TNW,

@@ -61,21 +61,27 @@ class MatmulConfig:
     INTERLEAVE: int = 0     # 1: one wave per SIMD, memory instructions threaded between its MFMAs
     DIRECT: int = 0         # 1: one wave per SIMD, tiles loaded straight into LDS (buffer_load_dwordx4 ... lds)
     KSPLIT: int = 1         # > 1: K split over that many workgroups, partials summed by a second launch
+    PERSIST: int = 0        # > 0 (DIRECT only): that many workgroups (one per CU) loop over the output tiles
 
     def as_dict(self) -> dict:
         return {"TM": self.TM, "TN": self.TN, "TK": self.TK, "num_warps": self.num_warps,
                 "WM": self.WM, "WN": self.WN, "MI": self.MI, "SPLIT_K": self.SPLIT_K, "GROUP_M": self.GROUP_M,
-                "PINGPONG": self.PINGPONG, "INTERLEAVE": self.INTERLEAVE, "DIRECT": self.DIRECT, "KSPLIT": self.KSPLIT}
+                "PINGPONG": self.PINGPONG, "INTERLEAVE": self.INTERLEAVE, "DIRECT": self.DIRECT, "KSPLIT": self.KSPLIT,
+                "PERSIST": self.PERSIST}
 
     @staticmethod
     def from_dict(d: dict) -> "MatmulConfig":
         return MatmulConfig(d["TM"], d["TN"], d.get("TK", 0), d.get("num_warps", 4), d.get("WM", 2),
                             d.get("WN", 2), d.get("MI", 32), d.get("SPLIT_K", 1), d.get("GROUP_M", 8),
-                            d.get("PINGPONG", 0), d.get("INTERLEAVE", 0), d.get("DIRECT", 0), d.get("KSPLIT", 1))
+                            d.get("PINGPONG", 0), d.get("INTERLEAVE", 0), d.get("DIRECT", 0), d.get("KSPLIT", 1),
+                            d.get("PERSIST", 0))
 
 
 # bf16 / fp16 candidates (MFMA 32x32x16 or 16x16x32)
 HIP_CANDIDATES: list[MatmulConfig] = [
+    # persistent direct-to-LDS kernels: one workgroup per CU looping over the output tiles
+    MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, CU_COUNT),
+    MatmulConfig(256, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, CU_COUNT),
     MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1),
     MatmulConfig(256, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1),
     MatmulConfig(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
@@ -156,7 +162,10 @@ def _sched_factor(cfg: MatmulConfig) -> float:
     """Relative MFMA-phase cost of a loop schedule, from bf16 8192^3 runs on MI355X
     (direct-to-LDS loads 3-7% ahead of ping-pong with K-split tiles, and another ~10%
     with 16x16x32 MFMAs, which hold a higher clock on random data than 32x32x16;
-    plain double-buffered loop ~9% behind ping-pong)."""
+    plain double-buffered loop ~9% behind ping-pong; the persistent direct kernel
+    1-2% ahead of the direct one at 8192^3, 1-8% on config 5's projections)."""
+    if cfg.PERSIST:
+        return 0.85
     if cfg.DIRECT:
         return 0.86 if cfg.MI == 16 else 0.95
     if cfg.INTERLEAVE:
@@ -203,8 +212,12 @@ def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) 
     t_l2 = tiles * (tm + tn) * kt * elem / L2_BYTES_PER_S
     t_hbm = (M * K + N * K + M * N) * batch * elem / HBM_BYTES_PER_S
     # a workgroup writes its output tile after its K loop; with one workgroup per CU
-    # nothing overlaps that store, which matters when the output dominates (small K)
+    # nothing overlaps that store, which matters when the output dominates (small K);
+    # a persistent workgroup starts its next tile while the stores drain (about half
+    # of them overlap: the second K step of the next tile waits for them)
     t_out = M * N * batch * (4 * S if S > 1 else elem) / HBM_BYTES_PER_S / occ
+    if cfg.PERSIST and tiles > CU_COUNT:
+        t_out *= 0.5
     # split K: the second launch reads the S fp32 partials, writes the output, and costs a launch
     t_sum = ((S * 4 + elem) * M * N * batch / HBM_BYTES_PER_S + 4e-6) if S > 1 else 0.0
     t = max(t_mfma, t_lds, t_l2, t_hbm) + t_out + t_sum

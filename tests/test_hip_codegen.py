@@ -157,6 +157,92 @@ def test_tile_order_is_a_bijection_when_compiled_for_the_host(tmp_path):
     assert subprocess.run([str(exe)]).returncode == 0
 
 
+def test_persistent_tile_order_visits_every_tile_once_on_its_xcd(tmp_path):
+    """Persistent workgroups b < min(G, T) walk virtual ids b, b + G, ... < T through the
+    same tile order (compiled with gcc on the CPU): every tile exactly once, and every
+    virtual id of a workgroup on the workgroup's own XCD (id mod 8)."""
+    import subprocess
+
+    from tensorjit.backends.hip_gemm import tile_order_lines
+
+    cases = [(32, 32, 8, 256), (4, 4, 8, 8), (3, 5, 8, 8), (43, 32, 8, 256), (2, 2, 8, 256)]
+    fns, checks = [], []
+    for ci, (ntm, ntn, gm, G) in enumerate(cases):
+        body = "\n".join(tile_order_lines(ntm, ntn, gm, 1, 1, vid="v", names=("m0", "n0"), sfx="p"))
+        fns.append(f"static void order{ci}(unsigned v, unsigned* mo, unsigned* no) {{\n{body}\n  *mo = m0; *no = n0; }}")
+        T = ntm * ntn
+        checks.append(f"""  {{ static unsigned char seen[{ntm}][{ntn}]; unsigned m, n, cnt = 0;
+    for (unsigned b = 0; b < {min(G, T)}u; ++b) for (unsigned v = b; v < {T}u; v += {G}u) {{
+      if (v % 8u != b % 8u) return 100 + {ci};
+      order{ci}(v, &m, &n); if (m >= {ntm}u || n >= {ntn}u || seen[m][n]++) return {ci + 1}; ++cnt; }}
+    if (cnt != {T}u) return 200 + {ci}; }}""")
+    src = "\n".join(fns) + "\nint main(void) {\n" + "\n".join(checks) + "\n  return 0;\n}\n"
+    c = tmp_path / "porder.c"
+    c.write_text(src)
+    exe = tmp_path / "porder"
+    subprocess.run(["gcc", "-O1", "-o", str(exe), str(c)], check=True)
+    assert subprocess.run([str(exe)]).returncode == 0
+
+
+PERSIST = MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, 256)
+
+
+def _gemm(kind):
+    """(function, operand shapes) of the persistent-kernel applicability cases."""
+    lin = lambda x, w: tj.linear(x, w)                      # noqa: E731
+    res = lambda x, w, r: tj.linear(x, w) + r               # noqa: E731
+    return {
+        "c4_bias_gelu": (lambda x, w, b: tj.gelu(tj.linear(x, w, b)), [(8192, 8192), (8192, 8192), (8192,)]),
+        "c5_folded_residual": (res, [(4, 2048, 4096), (4096, 4096), (4, 2048, 4096)]),
+        "c5_row_broadcast_residual": (res, [(4, 2048, 4096), (4096, 4096), (2048, 4096)]),
+        "ragged_m": (lin, [(8000, 4096), (4096, 4096)]),
+        "k_not_multiple_of_128": (lin, [(4096, 4160), (4096, 4160)]),
+        "k_below_256": (lin, [(4096, 128), (4096, 128)]),
+        "per_batch_weight": (lambda x, w: tj.matmul(x, tj.transpose(w, -1, -2)), [(4, 2048, 512), (4, 1024, 512)]),
+    }[kind]
+
+
+@pytest.mark.parametrize("kind,ok", [("c4_bias_gelu", True), ("c5_folded_residual", True),
+                                     ("c5_row_broadcast_residual", True), ("ragged_m", False),
+                                     ("k_not_multiple_of_128", False), ("k_below_256", False),
+                                     ("per_batch_weight", False)])
+def test_persistent_gemm_applies_to_whole_tiles_and_foldable_batches(kind, ok):
+    fn, shapes = _gemm(kind)
+    p = C.lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    assert hb.config_ok(PERSIST, DType.bf16, p.kernels[0].anchor) == ok
+    # the workgroup count must keep every virtual id on its XCD, and only the direct
+    # kernel has a persistent form
+    assert not hb.config_ok(MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, 100), DType.bf16,
+                            p.kernels[0].anchor)
+    assert not hb.config_ok(MatmulConfig(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1, 1, 256), DType.bf16,
+                            p.kernels[0].anchor)
+
+
+def test_persistent_gemm_launch_lds_and_waits():
+    """Config 4: 1024 tiles on 256 workgroups, two LDS stages plus the 32 KiB epilogue
+    staging array (the whole 160 KiB); the waits before the next tile's first fragment
+    reads (48: its K tile 1 and the 32 epilogue stores of each wave) and at its first
+    barrier (32: the stores) leave the stores draining; a residual broadcast over the
+    batch does not fold, and the direct kernel is generated instead."""
+    fn, shapes = _gemm("c4_bias_gelu")
+    p = C.lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    src, (l,) = hb.generate(p, {0: PERSIST})
+    assert l.grid == (256, 1, 1) and l.block == (256, 1, 1) and l.meta["persistent"] == 256
+    assert l.meta["lds_bytes"] == 160 * 1024 and l.meta["flops"] == 2.0 * 8192 ** 3
+    assert "__builtin_amdgcn_s_waitcnt(0xcf70)" in src and "__builtin_amdgcn_s_waitcnt(0x8f70)" in src
+    assert "_raw = *(const tj_u32x4*)" in src          # the bias is preloaded before the next K tile 1
+    hb.compile_source(src, "gfx950")
+    fn, shapes = _gemm("c5_folded_residual")
+    p = C.lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    _, (l,) = hb.generate(p, {0: PERSIST})
+    assert l.grid == (256, 1, 1) and l.meta["batch"] == 4 and l.meta["M"] == 2048
+    assert l.meta["flops"] == 2.0 * 4 * 2048 * 4096 * 4096
+    fn, shapes = _gemm("c5_row_broadcast_residual")
+    p = C.lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    _, (l,) = hb.generate(p, {0: PERSIST})
+    assert "persistent" not in l.meta and l.grid == (16, 8, 4)
+
+
 def test_k_split_gemm_has_a_partial_and_a_sum_launch():
     """K split over workgroups: the partial-product launch owns a workspace of
     batch x splits x M x N fp32 values (placed after the planned intermediates in the

@@ -1111,3 +1111,65 @@ def C_lower(fn, *args):
     from tensorjit.frontend.tracer import tensor_type_of
 
     return lower(tj.trace(fn, [tensor_type_of(a) for a in args]), "hip")
+
+
+@pytest.mark.parametrize("case", ["plain_two_tiles_each", "bias_gelu_uneven", "residual_short_k", "plain_long_k",
+                                  "batch_folded_residual", "batch_row_broadcast"])
+def test_persistent_direct_gemm_matches_the_direct_kernel(case):
+    """The persistent direct-to-LDS kernel (workgroups looping over output tiles, the next
+    tile's first K tiles prefetched under the epilogue) gives bit-identical results to the
+    one-tile-per-workgroup direct kernel with the same tiling (same MFMA order), on
+    small-integer data where both must equal the exact product: several tiles per
+    workgroup, workgroups with unequal tile counts, the shortest K loop (4 K tiles), an
+    epilogue with preloaded bias and one that loads a residual per element, a batched
+    projection folded into one GEMM over (batch x M) rows, and a residual broadcast over
+    the batch (which does not fold: the direct kernel is generated instead).  The
+    integer products are exact in fp32, so the base kernel's output is the reference
+    rounded once to bf16."""
+    from tensorjit.runtime.autotune import MatmulConfig
+
+    torch.manual_seed(0)
+    # (batch, M, N, K, epilogue, workgroups): 16 tiles on 8 workgroups (XCD order); 15
+    # tiles on 8 (plain order, one workgroup runs one tile); 4 K tiles; 16 K tiles; a
+    # [3, 256, .] activation (12 tiles on 8 workgroups)
+    bt, m, n, kk, epi, G = {"plain_two_tiles_each": ((), 1024, 1024, 384, "plain", 8),
+                            "bias_gelu_uneven": ((), 768, 1280, 640, "gelu", 8),
+                            "residual_short_k": ((), 512, 1024, 256, "res", 8),
+                            "plain_long_k": ((), 1024, 512, 1024, "plain", 8),
+                            "batch_folded_residual": ((3,), 256, 1024, 256, "res", 8),
+                            "batch_row_broadcast": ((3,), 256, 512, 256, "rowres", 8)}[case]
+    print(f"persistent gemm {case} {bt}x{m}x{n}x{kk} {epi} G={G}", flush=True)
+    a = torch.randint(-3, 4, (*bt, m, kk), device=DEV).bfloat16()
+    b = torch.randint(-3, 4, (n, kk), device=DEV).bfloat16()
+    if epi == "gelu":
+        bias = torch.randint(-8, 9, (n,), device=DEV).bfloat16()
+        fn, args = (lambda x, y, z: tj.gelu(tj.linear(x, y, z))), [a, b, bias]
+        ref = torch.nn.functional.gelu(a.float() @ b.float().t() + bias.float())
+    elif epi in ("res", "rowres"):
+        res = torch.randint(-8, 9, (*bt, m, n) if epi == "res" else (m, n), device=DEV).bfloat16()
+        fn, args = (lambda x, y, z: tj.linear(x, y) + z), [a, b, res]
+        ref = a.float() @ b.float().t() + res.float()
+    else:
+        fn, args = (lambda x, y: tj.linear(x, y)), [a, b]
+        ref = a.float() @ b.float().t()
+    base = MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1)
+    pers = MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, G)
+    mm = C_lower(fn, *args).kernels[0].anchor
+    assert hb_config_ok(pers, mm)
+    from tensorjit.backends import hip_backend as hb
+
+    launches = hb.generate(C_lower(fn, *args), {0: pers})[1]
+    assert (launches[0].meta.get("persistent") is None) == (epi == "rowres"), case
+    want = _run_with_config(fn, args, base)
+    for _ in range(2):          # twice: a race between the prefetches and the reads shows as a difference
+        got = _run_with_config(fn, args, pers)
+        assert torch.equal(got, want), case
+    # both round the exact fp32 sums to bf16 once: within bf16's half-ulp of the reference
+    err = float((want.float() - ref).abs().max() / ref.abs().max())
+    assert err < 2e-2, (case, err)
+
+
+def hb_config_ok(cfg, mm):
+    from tensorjit.backends import hip_backend as hb
+
+    return hb.config_ok(cfg, hb.compute_dtype(mm), mm)
