@@ -12,9 +12,10 @@ arena space for them.
 4 or 8 waves owns 32 query rows per wave of one (batch, head); key/value blocks
 of 64 rows stream through double-buffered LDS.  Each wave computes the scores
 transposed, ``Sᵀ = K·Qᵀ`` (MFMA 32x32x16, queries as columns), so every lane owns
-one query column: the online-softmax max / sum need one cross-lane exchange
-(``lane ^ 32``) per block, the rescale of the output accumulator is a per-lane
-multiply, and the probabilities go from the score accumulator straight into the
+half the keys of one query column: the online softmax exchanges nothing with the
+other half (``lane ^ 32``) unless the running maximum has to move, the rescale of
+the output accumulator is a per-lane multiply, and the probabilities go from the
+score accumulator straight into the
 B operand of ``Oᵀ += Vᵀ·Pᵀ`` without an LDS round trip.  V stays in its natural
 ``[key][d]`` layout in LDS; the ``Vᵀ`` operand is gathered with gfx950's
 transposing LDS read ``ds_read_b64_tr_b16`` (within each 16 lanes, lane ``i``
@@ -304,7 +305,20 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     # two waves per SIMD: one wave's softmax arithmetic runs under the other's MFMAs;
     # the compiler then keeps everything in 256 VGPRs
     occ = 2
-    L = [f'extern "C" __global__ void __launch_bounds__({THREADS}) __attribute__((amdgpu_waves_per_eu({occ}, {occ}))) {fname}(',
+    # lane l and lane l ^ 32 hold the two halves of a query's keys: gfx950's
+    # v_permlane32_swap exchanges the wave's halves in one VALU instruction (the
+    # maximum is taken of scaled scores, whatever the scale's sign)
+    L = ["__device__ __forceinline__ float tj_pair_max(float x) {",
+         "  const unsigned int u = __builtin_bit_cast(unsigned int, x);",
+         "  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);",
+         "  return fmaxf(__builtin_bit_cast(float, (unsigned int)sw[0]), __builtin_bit_cast(float, (unsigned int)sw[1]));",
+         "}",
+         "__device__ __forceinline__ float tj_pair_sum(float x) {",
+         "  const unsigned int u = __builtin_bit_cast(unsigned int, x);",
+         "  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);",
+         "  return __builtin_bit_cast(float, (unsigned int)sw[0]) + __builtin_bit_cast(float, (unsigned int)sw[1]);",
+         "}"]
+    L += [f'extern "C" __global__ void __launch_bounds__({THREADS}) __attribute__((amdgpu_waves_per_eu({occ}, {occ}))) {fname}(',
          f"    const {T}* __restrict__ in0_p, const {T}* __restrict__ in1_p, const {T}* __restrict__ in2_p,",
          f"    {T}* __restrict__ out0_p) {{",
          f"  __shared__ __attribute__((aligned(16))) {T} Ks[{NST}][{BKV}][{DP}];",
@@ -396,8 +410,12 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     # online softmax, one query column per lane (its 32 keys here + lane ^ 32's 32).
     # The extreme is taken on the raw scores (max(s*cs) = cs*max(s) for cs > 0, min for
     # cs < 0) so the scale folds into the exponent's FMA.  Lazy rescaling: the running
-    # reference max moves only when some lane's block max exceeds it by more than 8
-    # (exponents then stay <= 2^8); otherwise the output accumulator is left alone.
+    # reference max moves only when some lane's own block max exceeds it by more than 8
+    # (exponents then stay <= 2^8); otherwise the output accumulator is left alone, and
+    # no lane exchanges anything.  Only then are the two halves of a query's keys
+    # combined (lane ^ 32, one v_permlane32_swap), so both lanes of a query keep the
+    # same reference; each lane sums its own half of the row sum, combined once at the
+    # end.
     ext, ext_init, masked = ("fmaxf", "-__builtin_inff()", "-__builtin_inff()") if cs > 0 else \
         ("fminf", "__builtin_inff()", "__builtin_inff()")
 
@@ -414,14 +432,13 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         if mask is not None:
             out_l.append(f"      if ({mask} + t * 32 + (r / 4) * 8 + (int)g * 4 + r % 4 >= {Sk}) {sc}[q][t][r] = {masked};")
         out_l += [f"      mx = {ext}(mx, {sc}[q][t][r]);", "    }",
-                  f"  mx = {ext}(mx, __shfl_xor(mx, 32, 64));",
                   f"  mb[q] = mx * {cs!r}f;",
                   "  grow = grow || mb[q] > m_run[q] + 8.0f;",
                   "}",
                   "if (__builtin_amdgcn_ballot_w64(grow)) {",
                   "#pragma unroll",
                   f"  for (int q = 0; q < {QT}; ++q) {{",
-                  "    const float m_new = fmaxf(m_run[q], mb[q]);",
+                  "    const float m_new = fmaxf(m_run[q], tj_pair_max(mb[q]));",
                   "    const float alpha = __builtin_amdgcn_exp2f(m_run[q] - m_new);",
                   "    l_run[q] *= alpha;",
                   "#pragma unroll",
@@ -445,7 +462,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 "      }",
                 f"      pf[q][2 * t + h] = __builtin_bit_cast({opvec}, pw);",
                 "    }",
-                "  l_run[q] += rs + __shfl_xor(rs, 32, 64);",
+                "  l_run[q] += rs;",
                 "}"]
 
     def pv(stage: int) -> list[str]:
@@ -567,8 +584,9 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         # O = O^T / l: lane holds 4 consecutive dv per (u, r/4) for its query
         return ["#pragma unroll", f"  for (int q = 0; q < {QT}; ++q) {{",
                 "    const unsigned int qrow = qrow0 + q * 32u;",
+                "    const float l_tot = tj_pair_sum(l_run[q]);",
                 f"    if (qrow < {Sq}u) {{",
-                "      const float inv = 1.0f / l_run[q];",
+                "      const float inv = 1.0f / l_tot;",
                 "#pragma unroll",
                 f"      for (int u = 0; u < {Dv // 32}; ++u)",
                 "#pragma unroll",

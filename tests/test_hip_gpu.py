@@ -413,6 +413,22 @@ def test_fused_attention_scale_written_as_division():
     close_lowp(out, ref, tol=2e-2)
 
 
+@pytest.mark.parametrize("shapes", [[(1, 2, 300, 64)] * 3, [(1, 2, 600, 128), (1, 2, 1000, 128), (1, 2, 1000, 128)]],
+                         ids=["four_waves", "pingpong_ragged"])
+def test_fused_attention_negative_scale(shapes):
+    """A negative score scale: the block extreme is the raw minimum (masked keys +inf),
+    the running maximum is still taken over scaled scores."""
+    torch.manual_seed(3)
+    q, k, v = [torch.randn(sh, device=DEV).bfloat16() for sh in shapes]
+    fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * -0.2), v)  # noqa: E731
+    print(f"attention negative scale {shapes}", flush=True)
+    f = tj.jit(fn)
+    out = f(q, k, v)
+    assert f.compiled(q, k, v).num_kernels == 1
+    (ref,) = oracle.run(fn, *[t.float().cpu() for t in (q, k, v)])
+    close_lowp(out, ref, tol=2e-2)
+
+
 def test_fused_attention_large_logits_and_unit_scale():
     """Scores of magnitude ~100 (online max subtraction must keep exp2 in range) and
     no scale multiply in the chain."""
