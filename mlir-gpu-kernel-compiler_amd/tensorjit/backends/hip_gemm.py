@@ -164,6 +164,9 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
             and cfg.TN % (cfg.WN * cfg.MI) == 0 and cfg.TK % ki == 0 and cfg.TK > 0)
 
 
+SKINNY_A_CHUNK = 256   # K elements of A per LDS chunk of the decode GEMM (128-1024; 16 rows x 2*chunk bytes)
+
+
 def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     """Decode-shaped GEMM (M <= MI, NT layout): HBM-bound on streaming B.
 
@@ -174,7 +177,16 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     and reuses each A fragment for its NT column tiles.  The loads of ``D = TK / KI``
     K-steps are in flight ahead of the MFMAs (a ring of D register sets, the whole
     slice unrolled).  Partial tiles are summed through LDS (one barrier), then the
-    epilogue runs per element."""
+    epilogue runs per element.
+
+    A, which every workgroup reads whole (from L2), goes through LDS when the slices
+    allow it (16x16x32 MFMAs, whole 256-deep chunks, one workgroup along K): a fragment
+    load touches 16 rows x 64 bytes, and those scattered A loads on top of B's cost
+    16 x 8192 x 8192 3.5 us (23.5 vs 20.0 us with A's loads replaced by 1 KiB runs).
+    Each wave copies its slice of A 256 k at a time with ``buffer_load ... lds`` as
+    2 rows x 512 bytes per instruction into its own two chunk buffers, and reads the
+    fragments back with ``ds_read_b128``; 16-byte chunk q of row r is stored at slot
+    q ^ r, so the 16 rows a fragment read touches sit in 16 different bank groups."""
     k = g.k
     mm = k.anchor
     a, b = mm.inputs
@@ -252,6 +264,33 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     L.append(f"  for (int t = 0; t < {NT}; ++t) acc[t] = ({acc_t})(0.0f);")
     D = max(1, min(U, steps_per_wave))
     L.append(f"  tj_u32x4 ra[{D}], rb[{D}][{NT}];")
+    CH = SKINNY_A_CHUNK // KI                     # MFMA steps per A chunk
+    cb = MI * SKINNY_A_CHUNK * 2                  # bytes of one chunk buffer (16 rows x 512 B)
+    lds_a = (MI == 16 and S == 1 and not k_guard and steps_per_wave % CH == 0 and dt.itemsize == 2
+             and 2 * SK * cb + SK * MI * (TN + 1) * 4 <= 160 * 1024)
+    n_chunks = steps_per_wave // CH
+    row_b = SKINNY_A_CHUNK * 2                    # bytes of one row of a chunk
+    n_dma = cb // 1024                            # 1 KiB copy instructions per chunk
+    if lds_a:
+        L.append(f"  __shared__ __attribute__((aligned(1024))) char Ach0[{SK * cb}];")
+        L.append(f"  __shared__ __attribute__((aligned(1024))) char Ach1[{SK * cb}];")
+        L.append("  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave);")
+        # DMA lane offsets: instruction gq fills chunk bytes [1024 gq, 1024 gq + 1024),
+        # lane slot j of row r fetching 16-byte chunk j ^ r; rows past M read zeros
+        L.append(f"  unsigned int voA[{n_dma}];")
+        L.append("#pragma unroll")
+        L.append(f"  for (int gq = 0; gq < {n_dma}; ++gq) {{")
+        L.append(f"    const unsigned int byte = gq * 1024u + lane * 16u, r = byte / {row_b}u, j = (byte % {row_b}u) / 16u;")
+        L.append(f"    voA[gq] = r < {M}u ? (r * {K}u + kw + ((j ^ r) * 8u)) * 2u : {OOB}u;")
+        L.append("  }")
+        # fragment read: row lane % 16, logical chunk 4 s + lane / 16 at slot chunk ^ row
+        L.append("  const unsigned int fr = lane & 15u, fc = lane >> 4;")
+
+    def a_dma(chunk: int) -> list[str]:
+        buf = f"Ach{chunk % 2}"
+        return [f"  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsA, (__attribute__((address_space(3))) void*)"
+                f"({buf} + wv * {cb}u + {gq * 1024}u), 16, voA[{gq}], {chunk * row_b}, 0, 0);"
+                for gq in range(n_dma)]
 
     def load(step: int) -> list[str]:
         slot, byte = step % D, step * KI * 2
@@ -259,8 +298,18 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
         # (slices are whole multiples of the chunk, so no chunk straddles the end)
         kin = f"kw + {step * KI}u + kofs < kend" if k_guard else None
         out = []
-        va = f"offA + {byte}u" if not kin else f"({kin}) ? offA + {byte}u : {OOB}u"
-        out.append(f"  ra[{slot}] = __builtin_bit_cast(tj_u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsA, {va}, 0, 0));")
+        if lds_a:
+            chunk, sc = divmod(step, CH)
+            if sc == 0 and chunk + 1 < n_chunks:
+                # the next chunk goes into the buffer the chunk before this one used:
+                # its fragment reads are done once no LDS read is outstanding
+                out.append(f"  __builtin_amdgcn_s_waitcnt({_lgkmcnt_only(0)});")
+                out += a_dma(chunk + 1)
+            out.append(f"  ra[{slot}] = *(const tj_u32x4*)(Ach{chunk % 2} + wv * {cb}u + fr * {row_b}u"
+                       f" + (({4 * sc}u + fc) ^ fr) * 16u);")
+        else:
+            va = f"offA + {byte}u" if not kin else f"({kin}) ? offA + {byte}u : {OOB}u"
+            out.append(f"  ra[{slot}] = __builtin_bit_cast(tj_u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsA, {va}, 0, 0));")
         for t in range(NT):
             vb = f"offB[{t}] + {byte}u" if not kin else f"({kin}) ? offB[{t}] + {byte}u : {OOB}u"
             out.append(f"  rb[{slot}][{t}] = __builtin_bit_cast(tj_u32x4, "
@@ -269,6 +318,8 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
 
     # The written order is kept (sched_barrier between steps): left alone, the scheduler
     # sinks every load next to its MFMA to save registers, leaving ~2 K-steps in flight.
+    if lds_a:
+        L += a_dma(0)
     for step in range(min(D, steps_per_wave)):
         L += load(step)
     L.append("  __builtin_amdgcn_sched_barrier(0);")
@@ -325,7 +376,7 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
     L.append("}")
     grid = (-(-N // TN), 1, batch)
     meta = {"family": "matmul_skinny", "config": cfg.as_dict(), "dtype": dt.value, "M": M, "N": N, "K": K,
-            "batch": batch, "trans_b": tb, "lds_bytes": SK * MI * (TN + 1) * 4, "flops": 2.0 * M * N * K * batch}
+            "batch": batch, "trans_b": tb, "lds_bytes": SK * MI * (TN + 1) * 4 + (2 * SK * cb if lds_a else 0), "flops": 2.0 * M * N * K * batch}
     return "\n".join(L), Launch(fname, grid, (THREADS, 1, 1), 0, meta)
 
 

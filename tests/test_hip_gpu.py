@@ -306,6 +306,32 @@ def test_skinny_decode_matmul(dt, m, k, n):
     assert torch.equal(yi.cpu(), (xi.double() @ wi.double().t()).to(dt).cpu())
 
 
+@pytest.mark.parametrize("m", [16, 7, 1])
+def test_skinny_candidates_with_a_through_lds_are_exact(m):
+    """Every decode-GEMM candidate at K = 4096, where the waves' K slices are whole
+    256-deep chunks and A goes through LDS (1 to 8 chunks per wave, rows past M zero
+    from the copy's range check), exact on small-integer data against the exact sum
+    rounded once to bf16."""
+    from tensorjit.backends import hip_backend as hb
+    from tensorjit.runtime.autotune import HIP_CANDIDATES
+
+    torch.manual_seed(0)
+    a = torch.randint(-2, 3, (m, 4096), device=DEV).bfloat16()
+    b = torch.randint(-2, 3, (320, 4096), device=DEV).bfloat16()
+    fn = lambda x, y: tj.linear(x, y)  # noqa: E731
+    ref = (a.double() @ b.double().t()).bfloat16()
+    mm = C_lower(fn, a, b).kernels[0].anchor
+    tried = 0
+    for cfg in HIP_CANDIDATES:
+        if cfg.SPLIT_K == 1 or not hb.config_ok(cfg, hb.compute_dtype(mm), mm):
+            continue
+        print(f"skinny {m}x320x4096 {cfg}", flush=True)
+        out = _run_with_config(fn, [a, b], cfg)
+        assert torch.equal(out, ref), (m, cfg)
+        tried += 1
+    assert tried >= 8
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
 def test_mfma_layout_is_exact_on_integer_data(dt):
     """Small integers are exact in every dtype and in fp32 accumulation, so any
