@@ -1156,7 +1156,7 @@ def C_lower(fn, *args):
 
 
 @pytest.mark.parametrize("case", ["plain_two_tiles_each", "bias_gelu_uneven", "residual_short_k", "plain_long_k",
-                                  "batch_folded_residual", "batch_row_broadcast"])
+                                  "batch_folded_residual", "batch_row_broadcast", "f16_bias_gelu"])
 def test_persistent_direct_gemm_matches_the_direct_kernel(case):
     """The persistent direct-to-LDS kernel (workgroups looping over output tiles, the next
     tile's first K tiles prefetched under the epilogue) gives bit-identical results to the
@@ -1167,7 +1167,7 @@ def test_persistent_direct_gemm_matches_the_direct_kernel(case):
     projection folded into one GEMM over (batch x M) rows, and a residual broadcast over
     the batch (which does not fold: the direct kernel is generated instead).  The
     integer products are exact in fp32, so the base kernel's output is the reference
-    rounded once to bf16."""
+    rounded once to the 16-bit storage type."""
     from tensorjit.runtime.autotune import MatmulConfig
 
     torch.manual_seed(0)
@@ -1179,16 +1179,18 @@ def test_persistent_direct_gemm_matches_the_direct_kernel(case):
                             "residual_short_k": ((), 512, 1024, 256, "res", 8),
                             "plain_long_k": ((), 1024, 512, 1024, "plain", 8),
                             "batch_folded_residual": ((3,), 256, 1024, 256, "res", 8),
-                            "batch_row_broadcast": ((3,), 256, 512, 256, "rowres", 8)}[case]
-    print(f"persistent gemm {case} {bt}x{m}x{n}x{kk} {epi} G={G}", flush=True)
-    a = torch.randint(-3, 4, (*bt, m, kk), device=DEV).bfloat16()
-    b = torch.randint(-3, 4, (n, kk), device=DEV).bfloat16()
+                            "batch_row_broadcast": ((3,), 256, 512, 256, "rowres", 8),
+                            "f16_bias_gelu": ((), 512, 768, 512, "gelu", 8)}[case]
+    dt = torch.float16 if case.startswith("f16") else torch.bfloat16
+    print(f"persistent gemm {case} {bt}x{m}x{n}x{kk} {epi} G={G} {dt}", flush=True)
+    a = torch.randint(-3, 4, (*bt, m, kk), device=DEV).to(dt)
+    b = torch.randint(-3, 4, (n, kk), device=DEV).to(dt)
     if epi == "gelu":
-        bias = torch.randint(-8, 9, (n,), device=DEV).bfloat16()
+        bias = torch.randint(-8, 9, (n,), device=DEV).to(dt)
         fn, args = (lambda x, y, z: tj.gelu(tj.linear(x, y, z))), [a, b, bias]
         ref = torch.nn.functional.gelu(a.float() @ b.float().t() + bias.float())
     elif epi in ("res", "rowres"):
-        res = torch.randint(-8, 9, (*bt, m, n) if epi == "res" else (m, n), device=DEV).bfloat16()
+        res = torch.randint(-8, 9, (*bt, m, n) if epi == "res" else (m, n), device=DEV).to(dt)
         fn, args = (lambda x, y, z: tj.linear(x, y) + z), [a, b, res]
         ref = a.float() @ b.float().t() + res.float()
     else:
@@ -1206,7 +1208,7 @@ def test_persistent_direct_gemm_matches_the_direct_kernel(case):
     for _ in range(2):          # twice: a race between the prefetches and the reads shows as a difference
         got = _run_with_config(fn, args, pers)
         assert torch.equal(got, want), case
-    # both round the exact fp32 sums to bf16 once: within bf16's half-ulp of the reference
+    # both round the exact fp32 sums to 16 bits once: within half an ulp of the reference
     err = float((want.float() - ref).abs().max() / ref.abs().max())
     assert err < 2e-2, (case, err)
 
