@@ -215,6 +215,59 @@ def _stream_of(device_index: int) -> int:
 _current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", _stream_of)
 
 
+def fold_elementwise_into_gemm(program: Program) -> Program:
+    """Move an elementwise kernel into the epilogue of the GEMM that produces one of its
+    inputs, when that GEMM result has no other use.
+
+    The reference's greedy fusion joins an elementwise node to the kernel of its
+    *first* input only, and gives up when that would form a cycle.  A transformer
+    layer's second residual, ``h + linear(gelu(linear(rms(h))), w2)``, whose first input
+    ``h`` comes from the out-projection's kernel, therefore stays a kernel of its own
+    behind the down-projection, and the 64 MiB down-projection result makes a round
+    trip through HBM.  The merged kernel takes the elementwise kernel's place in the
+    schedule: the GEMM's inputs exist earlier, and the elementwise kernel's other inputs
+    exist there.  ``lower()`` keeps the reference plan; ``TENSORJIT_HIP_GEMM_EPILOGUE=0``
+    keeps it here too."""
+    if os.environ.get("TENSORJIT_HIP_GEMM_EPILOGUE", "1") == "0":
+        return program
+    kernels = list(program.kernels)
+    outs = {id(program.resolve(o)) for o in program.graph.outputs}
+    producer = {id(o): i for i, k in enumerate(kernels) for o in k.outputs}
+    changed = False
+    e = 0
+    while e < len(kernels):
+        ek = kernels[e]
+        merged = None
+        if ek.kind == "elementwise":
+            inside = {id(n) for n in ek.nodes}
+            for v in ek.inputs:
+                m = producer.get(id(v))
+                if m is None or m >= e or kernels[m].kind != "matmul":
+                    continue
+                mk = kernels[m]
+                shape = tuple(mk.anchor.shape)
+                if (mk.outputs != [v] or id(v) in outs or any(id(u) not in inside for u in v.users)
+                        or any(tuple(n.shape) != shape for n in ek.nodes)):
+                    continue
+                ins = list(mk.inputs)
+                for i in ek.inputs:
+                    if i is not v and all(i is not j for j in ins):
+                        ins.append(i)
+                merged = (m, Kernel("matmul", nodes=mk.nodes + ek.nodes, anchor=mk.anchor, inputs=ins,
+                                    outputs=list(ek.outputs)))
+                break
+        if merged is None:
+            e += 1
+            continue
+        m, k = merged
+        kernels[e] = k
+        del kernels[m]
+        producer = {id(o): i for i, kk in enumerate(kernels) for o in kk.outputs}
+        changed = True
+        e = kernels.index(k) + 1
+    return Program(program.graph, kernels, program.aliases) if changed else program
+
+
 # hipGraph replay by default from this many launches per call.  Measured on MI355X with the
 # reference's overhead chain (softmax(x @ w + 0.5) repeated): a direct hipModuleLaunchKernel
 # costs 2.3-2.8 us of host time, a graph launch 21-25 us plus ~0.6 us per kernel node, so
@@ -229,8 +282,9 @@ class HipProgram:
     def __init__(self, program: Program, device: str | torch.device = "cuda", use_graph: bool | None = None,
                  tune: bool = True):
         reject_zero_size(list(program.graph.inputs) + [n for k in program.kernels for n in k.nodes])
-        # backend-level rewrite of the planned program: attention chains -> one kernel
-        program = fuse_attention(program)
+        # backend-level rewrites of the planned program: attention chains -> one kernel,
+        # elementwise kernels behind a GEMM -> its epilogue
+        program = fold_elementwise_into_gemm(fuse_attention(program))
         self.program = program
         self.device = torch.device(device)
         if self.device.type != "cuda":

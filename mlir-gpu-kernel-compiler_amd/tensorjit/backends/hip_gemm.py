@@ -64,6 +64,13 @@ def compute_dtype(mm: Node) -> DType:
     return DType.f32
 
 
+def epilogue_inputs(k, epilogue: list[Node]) -> list[Node]:
+    """The kernel inputs the epilogue reads, in kernel-input order.  An operand of the
+    product can be one of them (``x + linear(x, w)``)."""
+    used = {id(i) for n in epilogue for i in n.inputs}
+    return [i for i in k.inputs if id(i) in used]
+
+
 def batch_folds_into_m(mm: Node) -> bool:
     """Is ``mm`` one 2-D GEMM over (batch x M) rows: A contiguous across its batch dims
     and B shared by every batch entry (a projection of a [B, S, D] activation)?"""
@@ -354,13 +361,13 @@ def gen_skinny_matmul(g: KernelGen, cfg: MatmulConfig) -> tuple[str, Launch]:
         meta = {"family": "matmul_skinny", "config": cfg.as_dict(), "dtype": dt.value, "M": M, "N": N, "K": K,
                 "batch": batch, "trans_b": tb, "lds_bytes": SK * MI * (TN + 1) * 4, "flops": 2.0 * M * N * K * batch,
                 "workspace": batch * S * M * N * 4, "ws_arg": True}
-        epi_inputs = [i for i in k.inputs if i is not a and i is not b]
+        epi_inputs = epilogue_inputs(k, epilogue)
         src2, sum_launch = gen_ksplit_sum(g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, S, fname)
         return "\n".join(L) + "\n\n" + src2, [Launch(fname, grid, (THREADS, 1, 1), 0, meta), sum_launch]
     L.append(f"    const float {g.names[id(mm)]} = s;")
     local = {id(mm): g.names[id(mm)]}
     full_idx = list(bidx) + ["i", "j"]
-    for n in [i for i in k.inputs if i is not a and i is not b]:
+    for n in epilogue_inputs(k, epilogue):
         consumer = next((c for c in epilogue if n in c.inputs), epilogue[0] if epilogue else mm)
         st = access_strides(n, consumer, out_shape)
         terms = [v if s_ == 1 else f"{v} * {s_}u" for v, s_ in zip(full_idx, st) if s_]
@@ -610,7 +617,7 @@ def gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str, 
     idx_t = "unsigned long" if batch * M * N >= 2**31 or batch * max(M, N) * K >= 2**31 else "unsigned int"
 
     epi_st = None
-    epi_inputs = [i for i in k.inputs if i is not a and i is not b]
+    epi_inputs = epilogue_inputs(k, epilogue)
     if cfg.PERSIST:
         # one 2-D GEMM over (batch x M) rows; an epilogue input that does not fold the same
         # way (or outputs of mixed dtypes) keeps the one-tile-per-workgroup kernel
@@ -1577,7 +1584,7 @@ def _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K,
                    THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname):
     a, b = mm.inputs
     # ---- epilogue on accumulators ------------------------------------------------------
-    epi_inputs = [i for i in k.inputs if i is not a and i is not b]
+    epi_inputs = epilogue_inputs(k, epilogue)
     if cfg.KSPLIT > 1:
         return _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, K, BM, BN, WM, WN, MI,
                               TMW, TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)

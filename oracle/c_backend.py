@@ -350,8 +350,13 @@ def _gen_matmul(kk: _K) -> str:
     local = {id(mm): kk.name[id(mm)]}
     L.append(f"      const float {kk.name[id(mm)]} = row[j];")
     oidx = bidx + ["i", "j"]
+    # the inputs the epilogue reads -- an operand of the product included
+    # (``x + linear(x, w)``).  The reference's c backend drops both operands from its
+    # epilogue inputs (tensorjit/backends/c_backend.py:215), so its generated C does not
+    # compile for that graph; this restatement reads them like any other input.
+    used = {id(i) for n in epi for i in n.inputs}
     for n in k.inputs:
-        if n is a or n is b:
+        if id(n) not in used:
             continue
         strd = _read_strides(n, kk.consumer(n, epi), out_shape)
         L.append(f"      const float {kk.name[id(n)]} = {kk.name[id(n)]}p[{_offset(oidx, strd)}];")

@@ -1,6 +1,7 @@
-"""Fused attention (hip backend rewrite of matmul -> softmax -> matmul), CPU side:
-which planned programs are rewritten, what the rewritten program looks like, and
-that the generated flash-attention kernel compiles for gfx950 with hipRTC."""
+"""The hip backend's rewrites of the planned program, CPU side: fused attention
+(matmul -> softmax -> matmul) and elementwise kernels moved into a GEMM's epilogue --
+which planned programs are rewritten, what the rewritten program looks like, and that
+the generated flash-attention kernel compiles for gfx950 with hipRTC."""
 import pytest
 
 import tensorjit as tj
@@ -103,6 +104,39 @@ def test_config5_block_fuses_its_attention():
     assert all(k.kind != "copy" for k in f.kernels)
     # the 1 GiB score and probability buffers are gone from the arena (2.25 GiB -> 428 MiB)
     assert plan_memory(f).arena_bytes < plan_memory(p).arena_bytes - 1.5 * 2**30
+
+
+def test_config5_second_residual_joins_the_down_projection():
+    """The reference plan keeps config 5's last add as an elementwise kernel behind the
+    down-projection; the backend rewrite moves it into that GEMM's epilogue (9 kernels),
+    and the 64 MiB down-projection result is no longer a planned buffer."""
+    import bench
+    from tensorjit.backends.hip_backend import fold_elementwise_into_gemm
+
+    shapes = [(4, 2048, 4096), (4096,), (4096, 4096), (4096, 4096), (4096, 4096), (4096, 4096), (4096,),
+              (11008, 4096), (4096, 11008)]
+    f = fuse_attention(lowered(bench._fn_block, shapes))
+    assert f.kernels[-1].kind == "elementwise" and f.kernels[-2].kind == "matmul"
+    down = f.kernels[-2].outputs[0]
+    q = fold_elementwise_into_gemm(f)
+    assert len(q.kernels) == 9 and q.kernels[-1].kind == "matmul"
+    assert [n.op for n in q.kernels[-1].nodes] == ["matmul", "add"]
+    assert q.kernels[-1].outputs == f.kernels[-1].outputs
+    assert plan_memory(f).offset(down) is not None and plan_memory(q).offset(down) is None
+
+
+def test_gemm_results_with_other_users_are_not_folded():
+    """A GEMM result that is also a graph output (or read by another kernel) keeps its
+    own store: the elementwise kernel stays."""
+    from tensorjit.backends.hip_backend import fold_elementwise_into_gemm
+
+    def fn(x, a, b):
+        h = x + tj.linear(x, a)
+        y = tj.linear(tj.relu(h), b)
+        return h + y, y
+
+    p = lowered(fn, [(256, 512), (512, 512), (512, 512)])
+    assert [k.kind for k in fold_elementwise_into_gemm(p).kernels] == [k.kind for k in p.kernels]
 
 
 @pytest.mark.parametrize("dtype", [DType.bf16, DType.f16])

@@ -113,6 +113,27 @@ def test_every_candidate_config_generates_valid_code():
             assert launches[0].meta["lds_bytes"] <= 160 * 1024
 
 
+@pytest.mark.parametrize("dtype,cands", [(DType.bf16, HIP_CANDIDATES), (DType.f32, HIP_F32_CANDIDATES)])
+@pytest.mark.parametrize("shape", [(256, 512), (16, 512), (512, 4096)])
+def test_epilogue_may_read_the_gemm_operand(dtype, cands, shape):
+    """``x + linear(x, w)``: the epilogue's residual is the product's A operand, so the
+    epilogue inputs are the kernel inputs its nodes read, operands included; every
+    candidate tiling generates it and reads x in the epilogue."""
+    types = [TensorType(shape, dtype), TensorType((shape[1], shape[1]), dtype)]
+    p = C.lower(tj.trace(lambda x, w: x + tj.linear(x, w), types), "hip")
+    plain = C.lower(tj.trace(lambda x, w: tj.linear(x, w), types), "hip")
+    (k,) = p.kernels
+    assert [n.op for n in k.nodes] == ["matmul", "add"]
+    tried = 0
+    for cfg in cands:
+        if hb.config_ok(cfg, dtype, k.anchor):
+            src, _ = hb.generate(p, {0: cfg})
+            # x is read once more than by the plain product: by the epilogue
+            assert src.count("in0_p") > hb.generate(plain, {0: cfg})[0].count("in0_p"), cfg
+            tried += 1
+    assert tried >= 10
+
+
 def test_config2_row_group_lowers_to_vectorised_flat_loop():
     src, launches = hb.generate(_program("eltwise_cfg2", DType.f32))
     assert launches[0].meta["family"] == "pointwise" and launches[0].meta["vec"] == 4

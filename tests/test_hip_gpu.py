@@ -813,7 +813,7 @@ def test_config5_block_full_size_batch0_vs_fp32():
     args = bench.block_inputs(torch, torch.device(DEV))
     f = tj.jit(bench._fn_block)
     out = f(*args)
-    assert f.compiled(*args).num_kernels == 10
+    assert f.compiled(*args).num_kernels == 9
     x, g1, wq, wk, wv, wo, g2, w1, w2 = [a.float() for a in args]
     x = x[:1]
     S, D, H = x.shape[1], x.shape[2], 32
@@ -835,8 +835,9 @@ def test_config5_block_full_size_batch0_vs_fp32():
 
 def test_config5_block_with_fused_attention_vs_oracle():
     """Config 5's layer at head dim 64 (so the attention chain and its head transposes
-    fuse into one flash kernel: 10 kernels), bf16 vs the fp32 oracle of the reference
-    plan, and hipGraph replays equal to eager launches."""
+    fuse into one flash kernel, and the second residual into the down-projection's
+    epilogue: 9 kernels), bf16 vs the fp32 oracle of the reference plan, and hipGraph
+    replays equal to eager launches."""
     import bench
 
     torch.manual_seed(0)
@@ -844,7 +845,7 @@ def test_config5_block_with_fused_attention_vs_oracle():
     f = tj.jit(bench._fn_block)
     out = f(*args)
     cp = f.compiled(*args)
-    assert cp.num_kernels == 10 and any("attention" in l.name for l in cp.launches)
+    assert cp.num_kernels == 9 and any("attention" in l.name for l in cp.launches)
     (ref,) = oracle.run(bench._fn_block, *[a.float().cpu() for a in args])
     close_lowp(out, ref, tol=3e-2)
     cp.use_graph = False
@@ -852,6 +853,69 @@ def test_config5_block_with_fused_attention_vs_oracle():
     cp.use_graph = True
     for _ in range(3):
         assert torch.equal(cp(*args)[0], eager)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_epilogue_reading_the_gemm_operand_is_exact(dt):
+    """``x + linear(x, w)``: the residual is the product's own A operand (one kernel
+    input read by the K loop and by the epilogue), on one tiling of each schedule --
+    persistent / direct-to-LDS / ping-pong / register-staged / decode for 16-bit, 32x32
+    and 16x16 tiles and a K split for fp32 -- exact on small-integer data (fp32 sums of
+    integers are exact, rounded once to the storage type as the reference is)."""
+    from tensorjit.backends import hip_backend as hb
+    from tensorjit.runtime.autotune import MatmulConfig as C
+
+    torch.manual_seed(0)
+    if dt == torch.bfloat16:
+        cases = [((512, 512), C(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, 8)),
+                 ((512, 512), C(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1)),
+                 ((300, 512), C(256, 256, 64, 8, 2, 4, 32, 1, 8, 3)),
+                 ((300, 520), C(128, 128, 32, 4, 2, 2, 32)),
+                 ((16, 4096), C(16, 32, 64, 4, 1, 1, 16, 4, 0)),
+                 ((7, 520), C(16, 32, 64, 4, 1, 1, 16, 4, 0))]
+    else:
+        cases = [((300, 520), C(128, 128, 32, 4, 2, 2, 32)), ((300, 520), C(64, 64, 32, 4, 2, 2, 16)),
+                 ((128, 512), C(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 4))]
+    fn = lambda x, w: x + tj.linear(x, w)  # noqa: E731
+    for (m, k), cfg in cases:
+        x = torch.randint(-2, 3, (m, k), device=DEV).to(dt)
+        w = torch.randint(-2, 3, (k, k), device=DEV).to(dt)
+        mm = C_lower(fn, x, w).kernels[0].anchor
+        assert hb.config_ok(cfg, hb.compute_dtype(mm), mm), cfg
+        print(f"x + linear(x, w) {m}x{k} {cfg}", flush=True)
+        out = _run_with_config(fn, [x, w], cfg)
+        ref = (x.double() + x.double() @ w.double().t()).to(dt)
+        assert torch.equal(out, ref), ((m, k), cfg)
+    # the default path (tj.jit, packaged table / cost model) too
+    x = torch.randint(-2, 3, (256, 512), device=DEV).to(dt)
+    w = torch.randint(-2, 3, (512, 512), device=DEV).to(dt)
+    assert torch.equal(tj.jit(fn)(x, w), (x.double() + x.double() @ w.double().t()).to(dt))
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_elementwise_kernel_behind_a_gemm_joins_its_epilogue(dt, monkeypatch):
+    """``h + linear(relu(h), w2)`` with ``h = x + linear(x, w1)``: the reference plan
+    leaves the last add as its own kernel (joining h's kernel would form a cycle); the
+    backend moves it into the second GEMM's epilogue (2 kernels instead of 3), against
+    the oracle of the reference plan, and the switch keeps the 3 kernels."""
+    torch.manual_seed(0)
+    x = torch.randn(256, 512, device=DEV).to(dt)
+    w1, w2 = [(0.05 * torch.randn(512, 512, device=DEV)).to(dt) for _ in range(2)]
+    fn = lambda x, a, b: (lambda h: h + tj.linear(tj.relu(h), b))(x + tj.linear(x, a))  # noqa: E731
+    f = tj.jit(fn)
+    out = f(x, w1, w2)
+    assert f.compiled(x, w1, w2).num_kernels == 2
+    (ref,) = oracle.run(fn, *[t.float().cpu() for t in (x, w1, w2)])
+    if dt == torch.float32:
+        close_f32(out, ref, scale=1e-5)
+    else:
+        close_lowp(out, ref, tol=2e-2)
+    monkeypatch.setenv("TENSORJIT_HIP_GEMM_EPILOGUE", "0")
+    f3 = tj.jit(fn)
+    out3 = f3(x, w1, w2)
+    assert f3.compiled(x, w1, w2).num_kernels == 3
+    if dt == torch.float32:
+        close_f32(out3, out, scale=1e-5)
 
 
 def test_config5_transformer_block_small_bf16_vs_oracle():
@@ -863,7 +927,7 @@ def test_config5_transformer_block_small_bf16_vs_oracle():
     args = bench.block_inputs(torch, torch.device(DEV), B=2, S=64, D=256, F=512)
     f = tj.jit(bench._fn_block)
     out = f(*args)
-    assert f.compiled(*args).num_kernels == 16
+    assert f.compiled(*args).num_kernels == 15          # the second residual joins the down-projection
     (ref,) = oracle.run(bench._fn_block, *[a.float().cpu() for a in args])
     close_lowp(out, ref, tol=3e-2)
     # graph replay of the same program gives the same bits as eager launches

@@ -77,6 +77,19 @@ def test_oracle_matmul_with_epilogue(m, k, n):
     _close(out, F.gelu(a.double() @ b.double() + bias.double()), tol=1e-3)
 
 
+def test_oracle_epilogue_reading_the_product_operand():
+    """``x + linear(x, w)`` (the residual is the product's A operand) and a layer whose
+    last add stays a kernel of its own in the plan, against float64."""
+    torch.manual_seed(0)
+    x, w, w2 = torch.randn(40, 96), 0.1 * torch.randn(96, 96), 0.1 * torch.randn(96, 96)
+    (out,) = oracle.run(lambda a, b: a + tj.linear(a, b), x, w)
+    _close(out, x.double() + x.double() @ w.double().t(), tol=1e-4)
+    fn = lambda a, b, c: (lambda h: h + tj.linear(tj.relu(h), c))(a + tj.linear(a, b))  # noqa: E731
+    (out,) = oracle.run(fn, x, w, w2)
+    h = x.double() + x.double() @ w.double().t()
+    _close(out, h + torch.relu(h) @ w2.double().t(), tol=1e-4)
+
+
 def test_oracle_batched_matmul_broadcast_and_linear():
     torch.manual_seed(0)
     a, b = torch.randn(2, 3, 8, 16), torch.randn(3, 16, 8)
