@@ -1,0 +1,104 @@
+"""Seeded random tensorjit programs for the hip backend's generator tests.
+
+``program(seed)`` returns ``(fn, shapes)``: a function on ``tj`` tensors built from a
+random mix of the ops the fusion passes turn into the four kernel families --
+pointwise chains with broadcasting, last-axis and non-last-axis reductions (kept and
+dropped dims), softmax / LayerNorm / RMSNorm rows, linear layers with and without
+bias, batched products, transposes and reshapes -- with one or two outputs.  Every
+op takes inputs in its domain (logs and roots of ``|v| + 1``, exponents of bounded
+values), so the programs are finite and the oracle's float32 results are
+well-conditioned.  The same seed always gives the same program.
+"""
+from __future__ import annotations
+
+import random
+
+import tensorjit as tj
+
+UNARY = ["exp_tanh", "log1p_abs", "sqrt1p_abs", "rsqrt1p_abs", "tanh", "abs", "relu", "sigmoid", "gelu", "silu",
+         "neg"]
+BINARY = ["add", "sub", "mul", "div_safe", "maximum", "minimum", "where"]
+
+
+def _unary(op: str, v):
+    if op == "exp_tanh":
+        return tj.exp(tj.tanh(v))
+    if op == "log1p_abs":
+        return tj.log(tj.abs(v) + 1.0)
+    if op == "sqrt1p_abs":
+        return tj.sqrt(tj.abs(v) + 1.0)
+    if op == "rsqrt1p_abs":
+        return tj.rsqrt(tj.abs(v) + 1.0)
+    if op == "neg":
+        return -v
+    return getattr(tj, op)(v)
+
+
+def _binary(op: str, a, b):
+    if op == "add":
+        return a + b
+    if op == "sub":
+        return a - b
+    if op == "mul":
+        return a * b
+    if op == "div_safe":
+        return a / (tj.abs(b) + 1.0)
+    if op == "where":
+        return tj.where(a, b, a * 0.5)
+    return getattr(tj, op)(a, b)
+
+
+def program(seed: int):
+    """(fn, input shapes) of random program ``seed``."""
+    rng = random.Random(seed)
+    R = rng.choice([1, 3, 16, 37, 64, 130])
+    N = rng.choice([1, 5, 16, 64, 100, 128, 260])
+    N2 = rng.choice([8, 32, 96, 128])
+    batched = rng.random() < 0.25
+    B = rng.choice([2, 3]) if batched else None
+    xs = (B, R, N) if batched else (R, N)
+    shapes = [xs, (N,) if rng.random() < 0.5 else xs, (N2, N), (N2,)]
+    steps = [rng.random() for _ in range(rng.randint(2, 7))]
+    choices = [rng.randrange(1 << 30) for _ in range(64)]
+
+    def fn(x, y, w, b):
+        c = iter(choices)
+
+        def pick(seq):
+            return seq[next(c) % len(seq)]
+
+        vals = [x, x * 0.5 + y]
+        for u in steps:
+            v = pick(vals)
+            if u < 0.30:
+                vals.append(_unary(pick(UNARY), v))
+            elif u < 0.55:
+                same = [t for t in vals if t.shape == v.shape or t.shape == v.shape[-1:]]
+                vals.append(_binary(pick(BINARY), v, pick(same)))
+            elif u < 0.65:
+                red = pick(["sum", "mean", "max"])
+                r = getattr(tj, red)(v, axis=-1, keepdim=True)
+                vals.append(v - r if red != "sum" else v * tj.rsqrt(tj.abs(r) + 1.0))
+            elif u < 0.72:
+                vals.append(pick([tj.softmax, tj.rms_norm, tj.layer_norm])(v))
+            elif u < 0.84 and v.shape[-1] == N:
+                h = tj.linear(v, w, b) if next(c) % 2 else tj.linear(v, w)
+                vals.append(pick([tj.relu, tj.gelu, tj.tanh])(h))
+            elif u < 0.90 and len(v.shape) >= 2:
+                # a transpose through the pointwise / copy family and back
+                t = tj.transpose(v, -1, -2)
+                vals.append(tj.transpose(_unary(pick(UNARY), t), -1, -2))
+            elif u < 0.95 and len(v.shape) >= 2:
+                # reduce over the leading axis (moved last by a transpose), broadcast back
+                vals.append(v + tj.mean(v, axis=0))
+            else:
+                flat = 1
+                for d in v.shape:
+                    flat *= d
+                vals.append(tj.reshape(tj.reshape(v, flat), *v.shape) * 2.0)
+        outs = [vals[-1]]
+        if next(c) % 3 == 0 and vals[-2] is not vals[-1] and vals[-2] is not x:
+            outs.append(vals[-2])
+        return tuple(outs) if len(outs) > 1 else outs[0]
+
+    return fn, shapes
