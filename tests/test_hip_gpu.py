@@ -1281,3 +1281,30 @@ def hb_config_ok(cfg, mm):
     from tensorjit.backends import hip_backend as hb
 
     return hb.config_ok(cfg, hb.compute_dtype(mm), mm)
+
+
+def test_tensors_past_two_to_the_31_elements():
+    """Iteration spaces of 2^31 elements and more take 64-bit offsets: a pointwise
+    chain and an RMSNorm over [2^21 + 3, 1024] bf16, and a GEMM whose [65536, 32768]
+    output has 2^31 elements, each checked against the oracle on its first rows and on
+    the rows whose offsets are past 2^31."""
+    torch.manual_seed(0)
+    rows = 2**21 + 3
+    x = torch.randn(rows, 1024, device=DEV).bfloat16()
+    g = (1 + 0.1 * torch.randn(1024, device=DEV)).bfloat16()
+    fn = lambda t, w: (t * 2.0 + 1.0, tj.rms_norm(t, w))  # noqa: E731
+    print("past 2^31: pointwise + rms", flush=True)
+    y, r = tj.jit(fn)(x, g)
+    for sl in (slice(0, 64), slice(rows - 64, rows)):
+        ry, rr = oracle.run(fn, x[sl].float().cpu(), g.float().cpu())
+        close_lowp(y[sl], ry, tol=1e-2)
+        close_lowp(r[sl], rr, tol=2e-2)
+    del x, y, r
+    torch.cuda.empty_cache()
+    a = torch.randn(65536, 64, device=DEV).bfloat16()
+    w = torch.randn(32768, 64, device=DEV).bfloat16()
+    print("past 2^31: gemm output", flush=True)
+    out = tj.jit(lambda p, q: tj.linear(p, q))(a, w)
+    for sl in (slice(0, 32), slice(65536 - 32, 65536)):
+        ref = a[sl].float() @ w.float().t()
+        close_lowp(out[sl], ref, tol=2e-2)
