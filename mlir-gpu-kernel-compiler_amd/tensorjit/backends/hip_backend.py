@@ -23,8 +23,9 @@ import threading
 
 import torch
 
-from ..ir import DType, Node
+from ..ir import DType, Node, OpKind
 from ..passes import Kernel, Program
+from ..passes.fusion import _finalize
 from ..passes.memory_planner import MemoryPlan, plan_memory
 from ..runtime import hip as rt
 from ..runtime.autotune import HIP_CANDIDATES, HIP_F32_CANDIDATES, MatmulConfig, autotune, cost_model
@@ -268,6 +269,59 @@ def fold_elementwise_into_gemm(program: Program) -> Program:
     return Program(program.graph, kernels, program.aliases) if changed else program
 
 
+def sink_epilogue_into_rows(program: Program) -> Program:
+    """Move a GEMM epilogue value whose only readers are one stage of a later row kernel
+    into that stage, when everything it reads the row kernel can read too.
+
+    Config 5's second RMSNorm squares the out-projection's result ``x1``: the greedy
+    fusion puts ``x1 * x1`` into the out-projection's epilogue (its input's kernel), so
+    the GEMM stores it (64 MiB) and the row kernel reads it beside ``x1`` itself.
+    Computed in the row kernel's reduction stage instead, the GEMM stores one output and
+    the row kernel streams one input (its second read of a row hits L2).  The square is
+    then taken of the stored ``x1`` (rounded to the storage type) rather than of the
+    fp32 accumulator, a rounding difference below the storage precision.
+    ``TENSORJIT_HIP_GEMM_EPILOGUE=0`` keeps the reference plan."""
+    if os.environ.get("TENSORJIT_HIP_GEMM_EPILOGUE", "1") == "0":
+        return program
+    kernels = list(program.kernels)
+    g = program.graph
+    outs = {id(program.resolve(o)) for o in g.outputs}
+    changed = False
+    for mi in range(len(kernels)):
+        mk = kernels[mi]
+        if mk.kind != "matmul":
+            continue
+        for o in list(mk.outputs):
+            if o is mk.anchor or o.kind != OpKind.ELEMENTWISE or id(o) in outs or not o.users:
+                continue
+            ri = next((i for i, k in enumerate(kernels) if any(o.users[0] is n for n in k.nodes)), None)
+            if ri is None or ri <= mi or kernels[ri].kind != "row":
+                continue
+            rk = kernels[ri]
+            stage = next(st for st in rk.stages if any(o.users[0] is n for n in st.nodes))
+            vec_shape = tuple(rk.rows) + (rk.n,)
+            readable = [x for x in mk.outputs if x is not o] + list(mk.inputs)
+            if (not all(any(u is n for n in stage.nodes) for u in o.users)
+                    or tuple(o.shape) != vec_shape or tuple(stage.iter_shape) != vec_shape
+                    or not all(i.op == "const" or any(i is x for x in readable) for i in o.inputs)):
+                continue
+            new_m = Kernel("matmul", nodes=[n for n in mk.nodes if n is not o], anchor=mk.anchor)
+            _finalize(new_m, g)
+            new_stages = []
+            for st in rk.stages:
+                if st is stage:
+                    st = Kernel(st.kind, nodes=[o] + st.nodes, anchor=st.anchor)
+                    _finalize(st, g)
+                new_stages.append(st)
+            new_r = Kernel("row", nodes=[o] + rk.nodes)
+            new_r.stages, new_r.rows, new_r.n = new_stages, rk.rows, rk.n  # type: ignore[attr-defined]
+            _finalize(new_r, g)
+            kernels[mi], kernels[ri] = new_m, new_r
+            mk = new_m
+            changed = True
+    return Program(g, kernels, program.aliases) if changed else program
+
+
 # hipGraph replay by default from this many launches per call.  Measured on MI355X with the
 # reference's overhead chain (softmax(x @ w + 0.5) repeated): a direct hipModuleLaunchKernel
 # costs 2.3-2.8 us of host time, a graph launch 21-25 us plus ~0.6 us per kernel node, so
@@ -283,8 +337,9 @@ class HipProgram:
                  tune: bool = True):
         reject_zero_size(list(program.graph.inputs) + [n for k in program.kernels for n in k.nodes])
         # backend-level rewrites of the planned program: attention chains -> one kernel,
-        # elementwise kernels behind a GEMM -> its epilogue
-        program = fold_elementwise_into_gemm(fuse_attention(program))
+        # elementwise kernels behind a GEMM -> its epilogue, epilogue values only a row
+        # kernel reads -> that row kernel
+        program = sink_epilogue_into_rows(fold_elementwise_into_gemm(fuse_attention(program)))
         self.program = program
         self.device = torch.device(device)
         if self.device.type != "cuda":

@@ -125,6 +125,42 @@ def test_config5_second_residual_joins_the_down_projection():
     assert plan_memory(f).offset(down) is not None and plan_memory(q).offset(down) is None
 
 
+def test_config5_square_of_the_residual_moves_into_the_rmsnorm_row():
+    """The plan computes the second RMSNorm's x1 * x1 in the out-projection's epilogue
+    and stores it for the row kernel; the rewrite computes it in the row kernel's
+    reduction stage, so the GEMM stores x1 only and the row kernel reads x1 and g."""
+    import bench
+    from tensorjit.backends.hip_backend import fold_elementwise_into_gemm, sink_epilogue_into_rows
+
+    shapes = [(4, 2048, 4096), (4096,), (4096, 4096), (4096, 4096), (4096, 4096), (4096, 4096), (4096,),
+              (11008, 4096), (4096, 11008)]
+    f = fold_elementwise_into_gemm(fuse_attention(lowered(bench._fn_block, shapes)))
+    q = sink_epilogue_into_rows(f)
+    out_proj = [k for k in f.kernels if k.kind == "matmul" and len(k.outputs) == 2]
+    assert len(out_proj) == 1 and [n.op for n in out_proj[0].nodes] == ["matmul", "add", "mul"]
+    i = f.kernels.index(out_proj[0])
+    assert [n.op for n in q.kernels[i].nodes] == ["matmul", "add"] and len(q.kernels[i].outputs) == 1
+    row = q.kernels[i + 1]
+    assert row.kind == "row" and [n.op for n in row.nodes][:2] == ["mul", "mean"]
+    assert [x.shape for x in row.inputs] == [(4, 2048, 4096), (4096,)]
+    assert [n.op for n in row.stages[0].nodes][:2] == ["mul", "mean"]
+    assert len(q.kernels) == len(f.kernels) == 9
+
+
+def test_epilogue_values_read_elsewhere_stay_in_the_gemm():
+    """x1 * x1 also returned (or read by a pointwise kernel) keeps its place."""
+    from tensorjit.backends.hip_backend import sink_epilogue_into_rows
+
+    def fn(x, w, g):
+        h = x + tj.linear(x, w)
+        sq = h * h
+        return tj.rms_norm(h, g), sq
+
+    p = lowered(fn, [(256, 512), (512, 512), (512,)])
+    q = sink_epilogue_into_rows(p)
+    assert [[n.op for n in k.nodes] for k in q.kernels] == [[n.op for n in k.nodes] for k in p.kernels]
+
+
 def test_gemm_results_with_other_users_are_not_folded():
     """A GEMM result that is also a graph output (or read by another kernel) keeps its
     own store: the elementwise kernel stays."""
