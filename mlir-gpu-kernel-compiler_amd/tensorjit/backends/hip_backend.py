@@ -248,7 +248,7 @@ def fold_elementwise_into_gemm(program: Program) -> Program:
                 mk = kernels[m]
                 shape = tuple(mk.anchor.shape)
                 if (mk.outputs != [v] or id(v) in outs or any(id(u) not in inside for u in v.users)
-                        or any(tuple(n.shape) != shape for n in ek.nodes)):
+                        or any(tuple(n.shape) != shape or n.kind != OpKind.ELEMENTWISE for n in ek.nodes)):
                     continue
                 ins = list(mk.inputs)
                 for i in ek.inputs:
