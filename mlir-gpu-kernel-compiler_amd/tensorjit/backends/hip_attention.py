@@ -124,9 +124,13 @@ def match_attention(program: Program, i3: int) -> dict | None:
     Sk, Dv = kk.shape[-2], v.shape[-1]
     if kk.shape[-1] != D or v.shape[-2] != Sk or tuple(p.shape[-2:]) != (Sq, Sk):
         return None
-    if D % 16 or D > MAX_HEAD_DIM or Dv % 32 or Dv > MAX_HEAD_DIM or Sq < 1 or Sk < 1:
+    # K and V blocks are copied 16 bytes per lane: 64 keys x D (and x Dv) must cover the
+    # 256 lanes of a 4-wave workgroup (8 waves need multiples of 64, as their layout does)
+    if D % 32 or D > MAX_HEAD_DIM or Dv % 32 or Dv > MAX_HEAD_DIM or Sq < 1 or Sk < 1:
         return None
     if math.prod(q.shape[:-2]) > 65535 or scale == 0.0:   # one (batch, head) per grid row
+        return None
+    if math.prod(q.shape[:-2]) * max(Sq, Sk) * max(D, Dv) >= 2**32:   # 32-bit element offsets
         return None
     return {"i1": i1, "i2": i2, "i3": i3, "q": q, "k": kk, "v": v, "out": mm3, "scale": float(scale),
             "nodes": k1.nodes + k2.nodes + k3.nodes}

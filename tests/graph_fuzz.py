@@ -102,3 +102,42 @@ def program(seed: int):
         return tuple(outs) if len(outs) > 1 else outs[0]
 
     return fn, shapes
+
+
+def attention_program(seed: int):
+    """(fn, shapes) of a random attention core ``softmax(q kᵀ · s) v``: batch and head
+    dims, query / key lengths (ragged against the 64-key blocks and the 32-query
+    tiles), head dims 16-128 for q/k and 32-128 for v, and the scale written as a
+    multiply on either side or as a division."""
+    rng = random.Random(seed)
+    lead = rng.choice([(1,), (2,), (2, 3), (1, 4)])
+    sq, sk = rng.choice([1, 31, 64, 200, 513]), rng.choice([1, 40, 64, 130, 700])
+    d, dv = rng.choice([16, 32, 64, 128]), rng.choice([32, 64, 128])
+    form = rng.choice(["mul", "lmul", "div", "none"])
+    c = rng.choice([0.05, 0.125, 0.3])
+
+    def fn(q, k, v):
+        s = tj.matmul(q, tj.transpose(k, -1, -2))
+        s = {"mul": lambda t: t * c, "lmul": lambda t: c * t, "div": lambda t: t / (1.0 / c),
+             "none": lambda t: t}[form](s)
+        return tj.matmul(tj.softmax(s), v)
+
+    return fn, [(*lead, sq, d), (*lead, sk, d), (*lead, sk, dv)]
+
+
+def layer_program(seed: int):
+    """(fn, shapes) of a random pre-norm residual layer: RMSNorm or LayerNorm, a linear
+    (with or without bias) and an activation, a residual, a second norm and a second
+    linear whose residual the plan leaves as a kernel of its own."""
+    rng = random.Random(seed)
+    B = rng.choice([(), (2,)])
+    S, D, F = rng.choice([16, 100, 256]), rng.choice([64, 128, 256]), rng.choice([64, 192, 512])
+    norm1, norm2 = rng.choice([tj.rms_norm, tj.layer_norm]), rng.choice([tj.rms_norm, tj.layer_norm])
+    act = rng.choice([tj.gelu, tj.relu, tj.silu])
+    bias = rng.random() < 0.5
+
+    def fn(x, g1, w1, b1, w2, g2, w3):
+        h = x + (tj.linear(norm1(x, g1), w1, b1) if bias else tj.linear(norm1(x, g1), w1))
+        return h + tj.linear(act(tj.linear(norm2(h, g2), w2)), w3)
+
+    return fn, [(*B, S, D), (D,), (D, D), (D,), (F, D), (D,), (D, F)]

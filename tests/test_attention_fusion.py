@@ -60,7 +60,8 @@ def test_divisions_that_are_not_a_scale_stay_unfused(form):
     assert all(k.kind != "attention" for k in f.kernels)
 
 
-@pytest.mark.parametrize("case", ["fp32", "probs_returned", "scores_reused", "head_dim_8", "extra_epilogue"])
+@pytest.mark.parametrize("case", ["fp32", "probs_returned", "scores_reused", "head_dim_8", "head_dim_16",
+                                  "extra_epilogue"])
 def test_chains_that_must_stay_unfused(case):
     if case == "fp32":
         p = lowered(attn, QKV, DType.f32)
@@ -76,6 +77,9 @@ def test_chains_that_must_stay_unfused(case):
         p = lowered(fn, QKV)
     elif case == "head_dim_8":
         p = lowered(attn, [(2, 16, 8)] * 3)
+    elif case == "head_dim_16":
+        # 64 keys x 16 dims is 128 16-byte chunks, fewer than the 256 lanes that copy a block
+        p = lowered(attn, [(2, 64, 16), (2, 700, 16), (2, 700, 64)])
     else:
         p = lowered(lambda q, k, v: tj.relu(attn(q, k, v)), QKV)
     f = fuse_attention(p)

@@ -60,3 +60,69 @@ def test_random_program_matches_the_oracle(seed, monkeypatch):
             scale = float(r.abs().max()) or 1.0
             err = float(((o - r).abs() / (r.abs() + scale)).max())
             assert err <= tol, (seed, dt, err)
+
+
+ATTN_SEEDS = range(24)
+LAYER_SEEDS = range(16)
+
+
+@pytest.mark.parametrize("seed", ATTN_SEEDS)
+def test_random_attention_generates_and_compiles(seed, tj_env):
+    fn, shapes = graph_fuzz.attention_program(seed)
+    p = lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    q = hb.fuse_attention(p)
+    # head dims that are multiples of 32 fuse; 16 keeps the reference plan's three kernels
+    fused = shapes[0][-1] % 32 == 0
+    assert [k.kind for k in q.kernels] == (["attention"] if fused else [k.kind for k in p.kernels]), (seed, shapes)
+    src, _ = hb.generate(q)
+    hb.compile_source(src, "gfx950")
+
+
+@pytest.mark.parametrize("seed", LAYER_SEEDS)
+def test_random_layer_gets_the_backend_rewrites(seed, tj_env):
+    fn, shapes = graph_fuzz.layer_program(seed)
+    p = lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    q = hb.sink_epilogue_into_rows(hb.fold_elementwise_into_gemm(hb.fuse_attention(p)))
+    # the second residual joins the last GEMM's epilogue
+    assert len(q.kernels) == len(p.kernels) - 1 and q.kernels[-1].kind == "matmul"
+    src, _ = hb.generate(q)
+    hb.compile_source(src, "gfx950")
+
+
+def _check_vs_oracle(fn, shapes, seed, dts):
+    import oracle
+
+    g = torch.Generator().manual_seed(seed)
+    ins = [torch.randn(s, generator=g) for s in shapes]
+    for dt, tol in dts:
+        outs = tj.jit(fn)(*[t.to(dt).cuda() for t in ins])
+        outs = outs if isinstance(outs, (tuple, list)) else [outs]
+        refs = oracle.run(fn, *[t.to(dt).float() for t in ins])
+        for o, r in zip(outs, refs):
+            o = o.float().cpu()
+            assert o.shape == r.shape and torch.isfinite(o).all()
+            scale = float(r.abs().max()) or 1.0
+            err = float(((o - r).abs() / (r.abs() + scale)).max())
+            assert err <= tol, (seed, dt, err)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", ATTN_SEEDS)
+def test_random_attention_matches_the_oracle(seed, monkeypatch):
+    """The fused flash kernel on random shapes, bf16 and fp16, against the fp32 oracle
+    of the reference plan (2e-2, the bound of the hand-written attention tests)."""
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    fn, shapes = graph_fuzz.attention_program(seed)
+    print(f"random attention {seed} {shapes}", flush=True)
+    _check_vs_oracle(fn, shapes, seed, [(torch.bfloat16, 2e-2), (torch.float16, 2e-2)])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", LAYER_SEEDS)
+def test_random_layer_matches_the_oracle(seed, monkeypatch):
+    """A random residual layer through every backend rewrite, fp32 (1e-5) and bf16
+    (5e-2: intermediates stored in bf16), against the oracle of the reference plan."""
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    fn, shapes = graph_fuzz.layer_program(seed)
+    print(f"random layer {seed} {shapes}", flush=True)
+    _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])
