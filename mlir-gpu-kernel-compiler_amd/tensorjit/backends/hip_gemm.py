@@ -134,7 +134,9 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
               and not cfg.INTERLEAVE and cfg.SPLIT_K == 1 and cfg.WM * cfg.WN == cfg.num_warps
               and cfg.TM % (cfg.WM * 32) == 0 and cfg.TN % (cfg.WN * 32) == 0
               and cfg.TM % (8 * cfg.num_warps) == 0 and cfg.TN % (8 * cfg.num_warps) == 0
-              and 2 * (cfg.TM + cfg.TN) * 128 <= 160 * 1024)
+              and 2 * (cfg.TM + cfg.TN) * 128 <= 160 * 1024
+              # one K tile's DMA loads per wave fit the 6-bit vmcnt of the stage waits
+              and (cfg.TM + cfg.TN) // (8 * cfg.num_warps) < 64)
         if ok and mm is not None:
             M, N, K, tb = matmul_dims(mm)
             a, b = mm.inputs
@@ -144,9 +146,12 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
         if ok and cfg.PERSIST:
             # persistent tile loop: 16x16x32 MFMAs, 4 waves, a multiple of 8 workgroups
             # (XCD order), an epilogue staging array of its own beside the two stages,
-            # whole tiles (no edges), an even number of at least 4 K tiles, no batch
+            # wave columns a power of two (a staged output row splits evenly over the 64
+            # lanes), whole tiles (no edges), an even number of at least 4 K tiles, and a
+            # batch only where it folds into M
             cols = cfg.TN // cfg.WN
             ok = (cfg.MI == 16 and cfg.num_warps == 4 and cfg.PERSIST % XCDS == 0 and cols >= 64
+                  and cols & (cols - 1) == 0
                   and 2 * (cfg.TM + cfg.TN) * 128 + 4 * 16 * cols * 4 <= 160 * 1024)
             if ok and mm is not None:
                 M, N, K, _ = matmul_dims(mm)

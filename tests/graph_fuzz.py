@@ -7,7 +7,9 @@ dropped dims), softmax / LayerNorm / RMSNorm rows, linear layers with and withou
 bias, batched products, transposes and reshapes -- with one or two outputs.  Every
 op takes inputs in its domain (logs and roots of ``|v| + 1``, exponents of bounded
 values), so the programs are finite and the oracle's float32 results are
-well-conditioned.  The same seed always gives the same program.
+well-conditioned.  ``attention_program``, ``layer_program`` and ``broadcast_program``
+draw attention cores, pre-norm residual layers and 3-D / 4-D broadcast-and-permute
+programs the same way.  The same seed always gives the same program.
 """
 from __future__ import annotations
 
@@ -141,3 +143,62 @@ def layer_program(seed: int):
         return h + tj.linear(act(tj.linear(norm2(h, g2), w2)), w3)
 
     return fn, [(*B, S, D), (D,), (D, D), (D,), (F, D), (D,), (D, F)]
+
+
+def broadcast_program(seed: int):
+    """(fn, shapes) of a random 3-D / 4-D pointwise and reduction program over inputs with
+    size-1 (broadcast) dims, with permutes of inner and outer dims, last- and
+    middle-axis reductions and a row op over the last axis."""
+    rng = random.Random(seed)
+    dims = [rng.choice([1, 2, 3, 7]), rng.choice([1, 4, 33]), rng.choice([1, 16, 65]), rng.choice([8, 64, 96, 257])]
+    if rng.random() < 0.4:
+        dims = dims[1:]
+    full = tuple(dims)
+    # the second input: the same shape with some dims set to 1, possibly fewer leading dims
+    bshape = tuple(1 if rng.random() < 0.4 else d for d in full)[rng.randint(0, 1):]
+    steps = [rng.random() for _ in range(rng.randint(2, 6))]
+    choices = [rng.randrange(1 << 30) for _ in range(64)]
+
+    def fn(x, y):
+        c = iter(choices)
+
+        def pick(seq):
+            return seq[next(c) % len(seq)]
+
+        v = x * 0.5 + y
+        for u in steps:
+            if u < 0.3:
+                # the broadcast input only in arithmetic: a clamp or select against a
+                # per-row constant can leave rows of nearly equal values, which a later
+                # norm's centring turns into rounding noise (ill-conditioned in bf16)
+                op = pick(BINARY)
+                v = _binary(op, v, pick([x, y, v] if op in ("add", "sub", "mul", "div_safe") else [x, v]))
+            elif u < 0.5:
+                v = _unary(pick(UNARY), v)
+            elif u < 0.65:
+                # permute two dims and back: a copy kernel each way around a pointwise op
+                a, b = sorted(rng_pair(next(c), v.ndim))
+                v = tj.transpose(_unary(pick(UNARY), tj.transpose(v, a, b)), a, b)
+            elif u < 0.8:
+                axis = next(c) % v.ndim
+                if axis == v.ndim - 1:
+                    v = v - tj.max(v, axis=-1, keepdim=True)
+                else:
+                    # a non-last axis reduction moves that axis last and keeps it there:
+                    # broadcast it back over v with the axis moved last, then restore the order
+                    order = [d for d in range(v.ndim) if d != axis] + [axis]
+                    back = [order.index(d) for d in range(v.ndim)]
+                    t = tj.permute(v, *order) + tj.sum(v, axis=axis, keepdim=True) * 0.1
+                    v = tj.permute(t, *back)
+            else:
+                v = pick([tj.softmax, tj.rms_norm, tj.layer_norm])(v)
+        return v
+
+    return fn, [full, bshape]
+
+
+def rng_pair(r: int, n: int) -> tuple[int, int]:
+    """Two distinct axes of an n-dim value, from one random integer."""
+    a = r % n
+    b = (a + 1 + (r // n) % (n - 1)) % n
+    return a, b

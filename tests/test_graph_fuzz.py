@@ -126,3 +126,26 @@ def test_random_layer_matches_the_oracle(seed, monkeypatch):
     fn, shapes = graph_fuzz.layer_program(seed)
     print(f"random layer {seed} {shapes}", flush=True)
     _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])
+
+
+BCAST_SEEDS = range(24)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_broadcast_program_generates_and_compiles(seed, tj_env):
+    fn, shapes = graph_fuzz.broadcast_program(seed)
+    for dt in (DType.f32, DType.bf16):
+        p = lower(tj.trace(fn, [TensorType(s, dt) for s in shapes]), "hip")
+        src, _ = hb.generate(hb.sink_epilogue_into_rows(hb.fold_elementwise_into_gemm(hb.fuse_attention(p))))
+        hb.compile_source(src, "gfx950")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", BCAST_SEEDS)
+def test_random_broadcast_program_matches_the_oracle(seed, monkeypatch):
+    """3-D / 4-D programs over size-1 (broadcast) dims with permutes and middle-axis
+    reductions, fp32 (1e-5) and bf16 (5e-2), against the oracle."""
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    fn, shapes = graph_fuzz.broadcast_program(seed)
+    print(f"random broadcast program {seed} {shapes}", flush=True)
+    _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])

@@ -239,6 +239,26 @@ def test_persistent_gemm_applies_to_whole_tiles_and_foldable_batches(kind, ok):
                             p.kernels[0].anchor)
 
 
+def test_configs_the_generators_cannot_schedule_are_rejected():
+    """A direct tile whose per-wave DMA count overflows the 6-bit vmcnt (one wave over a
+    256x256 tile: 64 loads), and a persistent tile whose wave columns (96) do not split a
+    staged row evenly over the lanes, are invalid configs: gen_matmul raises ValueError."""
+    # 3072 rows and columns: whole 192-wide tiles, so only the column split rejects cols96
+    fn, shapes = (lambda x, w, b: tj.gelu(tj.linear(x, w, b))), [(3072, 4096), (3072, 4096), (3072,)]
+    p = C.lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    anchor = p.kernels[0].anchor
+    one_wave = MatmulConfig(256, 256, 64, 1, 1, 1, 16, 1, 8, 0, 0, 1)
+    cols96 = MatmulConfig(192, 192, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, 256)
+    # their neighbours are valid: one wave over 128x128 (32 loads), 4 waves with 128 columns
+    assert hb.config_ok(MatmulConfig(128, 128, 64, 1, 1, 1, 16, 1, 8, 0, 0, 1), DType.bf16, anchor)
+    assert hb.config_ok(MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, 256), DType.bf16, anchor)
+    assert hb.config_ok(MatmulConfig(192, 192, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1), DType.bf16, anchor)
+    for cfg in (one_wave, cols96):
+        assert not hb.config_ok(cfg, DType.bf16, anchor)
+        with pytest.raises(ValueError, match="not valid"):
+            hb.generate(p, {0: cfg})
+
+
 def test_persistent_gemm_launch_lds_and_waits():
     """Config 4: 1024 tiles on 256 workgroups, two LDS stages plus the 32 KiB epilogue
     staging array (the whole 160 KiB); the waits before the next tile's first fragment
