@@ -309,20 +309,9 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     # two waves per SIMD: one wave's softmax arithmetic runs under the other's MFMAs;
     # the compiler then keeps everything in 256 VGPRs
     occ = 2
-    # lane l and lane l ^ 32 hold the two halves of a query's keys: gfx950's
-    # v_permlane32_swap exchanges the wave's halves in one VALU instruction (the
-    # maximum is taken of scaled scores, whatever the scale's sign)
-    L = ["__device__ __forceinline__ float tj_pair_max(float x) {",
-         "  const unsigned int u = __builtin_bit_cast(unsigned int, x);",
-         "  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);",
-         "  return fmaxf(__builtin_bit_cast(float, (unsigned int)sw[0]), __builtin_bit_cast(float, (unsigned int)sw[1]));",
-         "}",
-         "__device__ __forceinline__ float tj_pair_sum(float x) {",
-         "  const unsigned int u = __builtin_bit_cast(unsigned int, x);",
-         "  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);",
-         "  return __builtin_bit_cast(float, (unsigned int)sw[0]) + __builtin_bit_cast(float, (unsigned int)sw[1]);",
-         "}"]
-    L += [f'extern "C" __global__ void __launch_bounds__({THREADS}) __attribute__((amdgpu_waves_per_eu({occ}, {occ}))) {fname}(',
+    # the two halves of a query's keys (lanes l and l ^ 32) combine through the prelude's
+    # tj_pair_max / tj_pair_sum (v_permlane32_swap), shared by every attention kernel of a program
+    L = [f'extern "C" __global__ void __launch_bounds__({THREADS}) __attribute__((amdgpu_waves_per_eu({occ}, {occ}))) {fname}(',
          f"    const {T}* __restrict__ in0_p, const {T}* __restrict__ in1_p, const {T}* __restrict__ in2_p,",
          f"    {T}* __restrict__ out0_p) {{",
          f"  __shared__ __attribute__((aligned(16))) {T} Ks[{NST}][{BKV}][{DP}];",

@@ -37,6 +37,17 @@ def test_plain_attention_chain_becomes_one_kernel():
     assert plan_memory(f).arena_bytes == 0
 
 
+def test_two_attention_cores_in_one_program_compile(tj_env):
+    """Two fused attention kernels share one module: their lane-pair helpers live in the
+    prelude, so the source holds each device function once and hipRTC compiles it."""
+    fn = lambda q, k, v: attn(attn(q, k, v), k, v)  # noqa: E731
+    f = fuse_attention(lowered(fn, QKV))
+    assert [k.kind for k in f.kernels] == ["attention", "attention"]
+    src, launches = hb.generate(f)
+    assert len(launches) == 2 and src.count("float tj_pair_max(") == 1
+    hb.compile_source(src, "gfx950")
+
+
 def test_unscaled_and_differently_sized_value_heads():
     f = fuse_attention(lowered(lambda q, k, v: attn(q, k, v, 1.0), [(3, 50, 32), (3, 70, 32), (3, 70, 96)]))
     assert [k.kind for k in f.kernels] == ["attention"] and f.kernels[0].attn["scale"] == 1.0

@@ -455,6 +455,24 @@ def test_fused_attention_negative_scale(shapes):
     close_lowp(out, ref, tol=2e-2)
 
 
+def test_two_fused_attention_layers_in_one_program():
+    """Two attention cores in one program (the second reads the first's output as its
+    queries): two flash kernels in one module, against the fp32 oracle."""
+    torch.manual_seed(4)
+    q, k, v = [torch.randn(2, 3, 300, 64, device=DEV).bfloat16() for _ in range(3)]
+
+    def att(q, k, v):
+        return tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * 0.125), v)
+
+    fn = lambda q, k, v: att(att(q, k, v), k, v)  # noqa: E731
+    print("two attention layers", flush=True)
+    f = tj.jit(fn)
+    out = f(q, k, v)
+    assert [l.meta["family"] for l in f.compiled(q, k, v).launches] == ["attention", "attention"]
+    (ref,) = oracle.run(fn, *[t.float().cpu() for t in (q, k, v)])
+    close_lowp(out, ref, tol=2e-2)
+
+
 def test_fused_attention_large_logits_and_unit_scale():
     """Scores of magnitude ~100 (online max subtraction must keep exp2 in range) and
     no scale multiply in the chain."""
