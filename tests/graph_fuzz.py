@@ -202,3 +202,42 @@ def rng_pair(r: int, n: int) -> tuple[int, int]:
     a = r % n
     b = (a + 1 + (r // n) % (n - 1)) % n
     return a, b
+
+
+def block_program(seed: int):
+    """(fn, shapes, scales) of a random stack of one or two pre-norm transformer blocks
+    sharing one set of weights: multi-head attention (head split and merge by reshape
+    and transpose, scale 1/sqrt(d) as a multiply or a division) with a residual, then a
+    norm, an MLP (with or without biases, gelu / silu / relu) and a residual.  ``scales``
+    multiplies each standard-normal input: weights by 1/sqrt(fan-in), biases by 0.1, so
+    the activations keep unit size and the scores stay well-conditioned."""
+    rng = random.Random(seed)
+    B, S = rng.choice([1, 2]), rng.choice([64, 100, 256])
+    heads, d = rng.choice([(2, 32), (4, 32), (2, 64), (1, 128)])
+    Dm = heads * d
+    F = rng.choice([128, 192, 384])
+    layers = rng.choice([1, 2])
+    norm1, norm2 = rng.choice([tj.rms_norm, tj.layer_norm]), rng.choice([tj.rms_norm, tj.layer_norm])
+    act = rng.choice([tj.gelu, tj.silu, tj.relu])
+    bias = rng.random() < 0.5
+    div = rng.random() < 0.5
+
+    def fn(x, g1, wq, wk, wv, wo, g2, w1, b1, w2, b2):
+        def split(t):
+            return tj.transpose(tj.reshape(t, B, S, heads, d), 1, 2)
+
+        for _ in range(layers):
+            h = norm1(x, g1)
+            q, k, v = split(tj.linear(h, wq)), split(tj.linear(h, wk)), split(tj.linear(h, wv))
+            s = tj.matmul(q, tj.transpose(k, -1, -2))
+            s = s / (d ** 0.5) if div else s * (1.0 / d ** 0.5)
+            o = tj.reshape(tj.transpose(tj.matmul(tj.softmax(s), v), 1, 2), B, S, Dm)
+            x = x + tj.linear(o, wo)
+            h = norm2(x, g2)
+            u = act(tj.linear(h, w1, b1) if bias else tj.linear(h, w1))
+            x = x + (tj.linear(u, w2, b2) if bias else tj.linear(u, w2))
+        return x
+
+    shapes = [(B, S, Dm), (Dm,), (Dm, Dm), (Dm, Dm), (Dm, Dm), (Dm, Dm), (Dm,), (F, Dm), (F,), (Dm, F), (Dm,)]
+    w, wf = Dm ** -0.5, F ** -0.5
+    return fn, shapes, [1.0, 1.0, w, w, w, w, 1.0, w, 0.1, wf, 0.1]

@@ -89,11 +89,11 @@ def test_random_layer_gets_the_backend_rewrites(seed, tj_env):
     hb.compile_source(src, "gfx950")
 
 
-def _check_vs_oracle(fn, shapes, seed, dts):
+def _check_vs_oracle(fn, shapes, seed, dts, scales=None):
     import oracle
 
     g = torch.Generator().manual_seed(seed)
-    ins = [torch.randn(s, generator=g) for s in shapes]
+    ins = [torch.randn(s, generator=g) * (scales[i] if scales else 1.0) for i, s in enumerate(shapes)]
     for dt, tol in dts:
         outs = tj.jit(fn)(*[t.to(dt).cuda() for t in ins])
         outs = outs if isinstance(outs, (tuple, list)) else [outs]
@@ -149,3 +149,33 @@ def test_random_broadcast_program_matches_the_oracle(seed, monkeypatch):
     fn, shapes = graph_fuzz.broadcast_program(seed)
     print(f"random broadcast program {seed} {shapes}", flush=True)
     _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])
+
+
+BLOCK_SEEDS = range(12)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_transformer_stack_generates_and_compiles(seed, tj_env):
+    """One or two transformer blocks in one module: in bf16 every block's attention is
+    one flash kernel and its MLP residual joins the down-projection's epilogue."""
+    fn, shapes, _ = graph_fuzz.block_program(seed)
+    p = lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    q = hb.sink_epilogue_into_rows(hb.fold_elementwise_into_gemm(hb.fuse_attention(p)))
+    kinds = [k.kind for k in q.kernels]
+    layers = kinds.count("attention")
+    assert layers >= 1 and len(kinds) == 9 * layers and "copy" not in kinds, (seed, kinds)
+    src, _ = hb.generate(q)
+    hb.compile_source(src, "gfx950")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", BLOCK_SEEDS)
+def test_random_transformer_stack_matches_the_oracle(seed, monkeypatch):
+    """Random one- and two-block transformer stacks (weights scaled by 1/sqrt(fan-in)):
+    fp32 within 1e-5 (attention unfused: the reference plan's kernels), bf16 within 3e-2
+    (fused attention, bf16 intermediates; torch's own bf16 evaluation of these programs
+    is up to 1e-2 from float64), against the oracle of the reference plan."""
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    fn, shapes, scales = graph_fuzz.block_program(seed)
+    print(f"random transformer stack {seed} {shapes[0]}", flush=True)
+    _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 3e-2)], scales)
