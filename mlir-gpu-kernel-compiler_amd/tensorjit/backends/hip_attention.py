@@ -29,6 +29,7 @@ import os
 
 from ..ir import DType, Node
 from ..passes import Kernel, Program
+from ..runtime.autotune import CU_COUNT
 from .hip_prelude import CTYPE
 
 BQ_PER_WAVE = 32
@@ -233,14 +234,27 @@ def _tile_lines(nq: int, batch: int, idx_t: str) -> list[str]:
     return [f"  const {idx_t} bh = blockIdx.x / {nq}u;", f"  const unsigned int qt = blockIdx.x % {nq}u;"]
 
 
-def attention_layout(Sq: int, D: int, Dv: int) -> tuple[int, int]:
-    """(waves per workgroup, 32-row query tiles per wave).  Long sequences: 8 waves in
-    two ping-pong groups sharing every K/V block between 256 queries (half the L2->CU
-    traffic of 4 waves), while on each SIMD one group's softmax arithmetic runs under
-    the other group's MFMAs.  Two query tiles per wave would halve the LDS fragment
-    reads per FLOP, but its accumulators do not fit beside the softmax operands in the
-    256 VGPRs the rescale arithmetic needs (the compiler spills)."""
-    if D % 64 == 0 and Dv % 64 == 0 and Sq >= 512:
+def attention_layout(batch: int, Sq: int, D: int, Dv: int) -> tuple[int, int]:
+    """(waves per workgroup, 32-row query tiles per wave).
+
+    8 waves in two ping-pong groups share every K/V block between 256 queries (half the
+    L2->CU traffic of 4 waves) while on each SIMD one group's softmax arithmetic runs
+    under the other group's MFMAs; 4 independent waves per workgroup (128 queries, two
+    workgroups per CU) otherwise.  Measured on MI355X (bf16): ping-pong is faster at head
+    dims 128 once its grid fills the 256 CUs ([4,32,2048,128] 270 vs 299 us, [1,32,4096,128]
+    255 vs 288, [8,32,1024,128] 154 vs 176, [2,8,4096,128] with exactly 256 workgroups
+    128 vs 146); 4 waves are faster with fewer ping-pong workgroups ([1,16,2048,128] 51 vs
+    55 us, [4,8,512,128] 16 vs 20) and at head dim 64 ([4,32,2048,64] 162 vs 169,
+    [16,16,512,64] 27 vs 31; equal at [2,16,2048,64]).  TENSORJIT_HIP_ATTENTION_WAVES=4
+    or 8 forces a schedule (8 needs head dims that are multiples of 64).  Two query
+    tiles per wave would halve the LDS fragment reads per FLOP, but its accumulators do
+    not fit beside the softmax operands in the 256 VGPRs the rescale arithmetic needs
+    (the compiler spills)."""
+    pingpong_ok = D % 64 == 0 and Dv % 64 == 0
+    forced = os.environ.get("TENSORJIT_HIP_ATTENTION_WAVES")
+    if forced in ("4", "8"):
+        return (8 if forced == "8" and pingpong_ok else 4), 1
+    if pingpong_ok and min(D, Dv) >= 128 and Sq >= 512 and batch * -(-Sq // 256) >= CU_COUNT:
         return 8, 1
     return 4, 1
 
@@ -277,7 +291,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
 
     (qoff, qst), (koff, kst) = base_stride(layouts[0], Sq, D, q), base_stride(layouts[1], Sk, D, kk)
     (voff, vst), (ooff, ost) = base_stride(layouts[2], Sk, Dv, v), base_stride(out_layout, Sq, Dv, out)
-    NW, QT = attention_layout(Sq, D, Dv)
+    NW, QT = attention_layout(batch, Sq, D, Dv)
     assert QT == 1, "one query tile per wave"
     THREADS = NW * 64
     # 8 waves: two groups of 4 a phase apart (ping-pong) over 3 LDS stages

@@ -37,6 +37,19 @@ def test_plain_attention_chain_becomes_one_kernel():
     assert plan_memory(f).arena_bytes == 0
 
 
+def test_attention_layout_rule():
+    """Ping-pong (8 waves) only where it measured faster: head dims of at least 128 and a
+    grid of at least one ping-pong workgroup per CU; 4 waves otherwise."""
+    from tensorjit.backends.hip_attention import attention_layout
+
+    assert attention_layout(128, 2048, 128, 128) == (8, 1)       # config 5: 1024 workgroups
+    assert attention_layout(16, 4096, 128, 128) == (8, 1)        # exactly 256
+    assert attention_layout(16, 2048, 128, 128) == (4, 1)        # 128 workgroups
+    assert attention_layout(128, 2048, 64, 64) == (4, 1)         # head dim 64
+    assert attention_layout(512, 256, 128, 128) == (4, 1)        # short query sequences
+    assert attention_layout(128, 2048, 96, 96) == (4, 1)
+
+
 def test_two_attention_cores_in_one_program_compile(tj_env):
     """Two fused attention kernels share one module: their lane-pair helpers live in the
     prelude, so the source holds each device function once and hipRTC compiles it."""
@@ -196,13 +209,18 @@ def test_gemm_results_with_other_users_are_not_folded():
                                     [(1, 2, 512, 64), (1, 2, 900, 64), (1, 2, 900, 64)],
                                     [(1, 2, 512, 64), (1, 2, 128, 64), (1, 2, 128, 64)],
                                     [(1, 2, 512, 64), (1, 2, 40, 64), (1, 2, 40, 64)]])
-def test_flash_kernel_compiles_for_gfx950(shapes, dtype, tj_env):
+@pytest.mark.parametrize("forced", [None, "8"], ids=["rule", "pingpong"])
+def test_flash_kernel_compiles_for_gfx950(shapes, dtype, forced, tj_env, monkeypatch):
+    if forced:
+        monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_WAVES", forced)
     f = fuse_attention(lowered(attn, shapes, dtype))
     src, launches = hb.generate(f)
     (l,) = launches
     from tensorjit.backends.hip_attention import attention_layout
 
-    waves, tiles = attention_layout(shapes[0][-2], shapes[0][-1], shapes[2][-1])
+    waves, tiles = attention_layout(l.meta["batch"], shapes[0][-2], shapes[0][-1], shapes[2][-1])
+    # the forced ping-pong schedule needs head dims that are multiples of 64
+    assert waves == (8 if forced and shapes[0][-1] % 64 == 0 and shapes[2][-1] % 64 == 0 else 4)
     assert "attention" in l.name and l.block == (64 * waves, 1, 1)
     assert l.grid == (-(-shapes[0][-2] // (32 * waves * tiles)) * l.meta["batch"], 1, 1)
     if waves == 8:

@@ -67,7 +67,7 @@ LAYER_SEEDS = range(16)
 
 
 @pytest.mark.parametrize("seed", ATTN_SEEDS)
-def test_random_attention_generates_and_compiles(seed, tj_env):
+def test_random_attention_generates_and_compiles(seed, tj_env, monkeypatch):
     fn, shapes = graph_fuzz.attention_program(seed)
     p = lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
     q = hb.fuse_attention(p)
@@ -76,6 +76,12 @@ def test_random_attention_generates_and_compiles(seed, tj_env):
     assert [k.kind for k in q.kernels] == (["attention"] if fused else [k.kind for k in p.kernels]), (seed, shapes)
     src, _ = hb.generate(q)
     hb.compile_source(src, "gfx950")
+    if fused and shapes[0][-1] % 64 == 0 and shapes[2][-1] % 64 == 0:
+        # the ping-pong schedule, which the layout rule keeps for large grids
+        monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_WAVES", "8")
+        src, (l,) = hb.generate(q)
+        assert l.block == (512, 1, 1)
+        hb.compile_source(src, "gfx950")
 
 
 @pytest.mark.parametrize("seed", LAYER_SEEDS)
@@ -115,6 +121,12 @@ def test_random_attention_matches_the_oracle(seed, monkeypatch):
     fn, shapes = graph_fuzz.attention_program(seed)
     print(f"random attention {seed} {shapes}", flush=True)
     _check_vs_oracle(fn, shapes, seed, [(torch.bfloat16, 2e-2), (torch.float16, 2e-2)])
+    if shapes[0][-1] % 64 == 0 and shapes[2][-1] % 64 == 0:
+        # the same cores on the ping-pong schedule (the layout rule keeps it for grids of
+        # at least 256 workgroups, which these shapes do not reach)
+        monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_WAVES", "8")
+        print(f"random attention {seed} {shapes} ping-pong", flush=True)
+        _check_vs_oracle(fn, shapes, seed, [(torch.bfloat16, 2e-2)])
 
 
 @pytest.mark.gpu
