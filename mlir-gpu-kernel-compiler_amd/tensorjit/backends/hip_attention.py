@@ -21,6 +21,11 @@ B operand of ``Oᵀ += Vᵀ·Pᵀ`` without an LDS round trip.  V stays in its n
 transposing LDS read ``ds_read_b64_tr_b16`` (within each 16 lanes, lane ``i``
 receives element ``i % 4`` of the 8-byte rows loaded by lanes ``4e + i / 4``,
 e = 0..3), two per fragment, in the key order of the score accumulator.
+
+Grids short of one workgroup per CU (few heads, long keys) split the key range: each
+workgroup runs the same loop over an equal share of the key blocks and stores its
+unnormalised output rows with their running reference and sum in a workspace, and a
+second launch combines the splits (weights ``2^(m_s - max m)``) and writes the output.
 """
 from __future__ import annotations
 
@@ -259,6 +264,35 @@ def attention_layout(batch: int, Sq: int, D: int, Dv: int) -> tuple[int, int]:
     return 4, 1
 
 
+def attention_splits(tiles: int, KB: int, pingpong: bool) -> int:
+    """Key-range splits per (batch*head, query tile) for grids that leave CUs idle: with
+    ``tiles`` workgroups short of one per CU, each workgroup takes an equal share of the
+    key blocks (``KB`` divisible by the split count, at least 2 blocks each) and writes
+    unnormalised partial outputs with their running maxima and sums; a second launch
+    combines them.  The smallest split count that reaches 256 workgroups, else the largest
+    one that divides ``KB``; 1 for the ping-pong schedule and for full grids.
+    TENSORJIT_HIP_ATTENTION_SPLITS=n forces n where it divides ``KB`` into >= 2-block parts."""
+    forced = os.environ.get("TENSORJIT_HIP_ATTENTION_SPLITS")
+    ok = [n for n in range(2, 33) if KB % n == 0 and KB // n >= 2]
+    if pingpong:
+        return 1
+    if forced is not None:
+        return int(forced) if int(forced) in ok else 1
+    if tiles >= CU_COUNT or not ok:
+        return 1
+    return next((n for n in ok if tiles * n >= CU_COUNT), ok[-1])
+
+
+def _split_tile_lines(nq: int, batch: int, NS: int, KBL: int, idx_t: str) -> list[str]:
+    """Workgroup -> (``bh``, ``qt``) and, with key splits, the split's first key block
+    ``kb0``: the (batch*head, split) pairs are the XCD-grouped "heads" of ``_tile_lines``,
+    so the query tiles that share a key range share an XCD's L2."""
+    if NS == 1:
+        return _tile_lines(nq, batch, idx_t)
+    lines = [x.replace(" bh = ", " vh = ") for x in _tile_lines(nq, batch * NS, idx_t)]
+    return lines + [f"  const {idx_t} bh = vh / {NS}u;", f"  const unsigned int kb0 = (unsigned int)(vh % {NS}u) * {KBL}u;"]
+
+
 def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     from .hip_kernels import Launch
 
@@ -299,6 +333,10 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     NST = 3 if pingpong else 2
     BQ = BQ_PER_WAVE * QT * NW
     KB = -(-Sk // BKV)
+    nq = -(-Sq // BQ)
+    NS = attention_splits(batch * nq, KB, pingpong)
+    KBL = KB // NS                              # key blocks per workgroup
+    kb0 = "" if NS == 1 else "kb0 + "           # the workgroup's first key block
     DP = D + 8                                  # 16-byte row padding: conflict-free fragment reads
     # V rows: a transposing read touches 8 rows x 64 bytes; a pitch of 32 or 96 (mod 128)
     # elements puts rows r and r+1..r+3 on disjoint bank ranges
@@ -327,12 +365,12 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     # tj_pair_max / tj_pair_sum (v_permlane32_swap), shared by every attention kernel of a program
     L = [f'extern "C" __global__ void __launch_bounds__({THREADS}) __attribute__((amdgpu_waves_per_eu({occ}, {occ}))) {fname}(',
          f"    const {T}* __restrict__ in0_p, const {T}* __restrict__ in1_p, const {T}* __restrict__ in2_p,",
-         f"    {T}* __restrict__ out0_p) {{",
+         f"    {T}* __restrict__ out0_p{', float* __restrict__ ws_p' if NS > 1 else ''}) {{",
          f"  __shared__ __attribute__((aligned(16))) {T} Ks[{NST}][{BKV}][{DP}];",
          f"  __shared__ __attribute__((aligned(16))) {T} Vs[{NST}][{BKV}][{VP}];",
          "  const unsigned int tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;",
          "  const unsigned int g = lane / 32u, col = lane % 32u;",
-         *_tile_lines(-(-Sq // BQ), batch, idx_t),
+         *_split_tile_lines(nq, batch, NS, KBL, idx_t),
          f"  const {T}* __restrict__ Qb = in0_p + ({qoff});",
          f"  const {T}* __restrict__ Kb = in1_p + ({koff});",
          f"  const {T}* __restrict__ Vb = in2_p + ({voff});",
@@ -360,7 +398,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     def k_load(blk: str) -> list[str]:
         out_l = ["#pragma unroll", f"for (int i = 0; i < {KC}; ++i) {{",
                  f"  const unsigned int c = i * {THREADS}u + tid, row = c / {D // 8}u, d8 = (c % {D // 8}u) * 8u;",
-                 f"  unsigned int key = ({blk}) * {BKV}u + row;"]
+                 f"  unsigned int key = ({kb0}{blk}) * {BKV}u + row;"]
         if ragged:
             out_l.append(f"  key = key < {Sk}u ? key : {Sk - 1}u;")
         return out_l + [f"  rk[i] = *(const tj_u32x4*)&Kb[key * {kst}u + d8];", "}"]
@@ -368,7 +406,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     def v_load(blk: str) -> list[str]:
         out_l = ["#pragma unroll", f"for (int i = 0; i < {VC}; ++i) {{",
                  f"  const unsigned int c = i * {THREADS}u + tid, row = c / {Dv // 8}u, d8 = (c % {Dv // 8}u) * 8u;",
-                 f"  unsigned int key = ({blk}) * {BKV}u + row;"]
+                 f"  unsigned int key = ({kb0}{blk}) * {BKV}u + row;"]
         if ragged:
             out_l.append(f"  key = key < {Sk}u ? key : {Sk - 1}u;")
         return out_l + [f"  rv[i] = *(const tj_u32x4*)&Vb[key * {vst}u + d8];", "}"]
@@ -428,8 +466,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
 
     def block_max(sc: str, j: int | None) -> list[str]:
         mask = None
-        if ragged and j == KB - 1:
-            mask = f"{j * BKV}"
+        if ragged and j == KBL - 1:
+            mask = f"{j * BKV}" if NS == 1 else f"(int)kb0 * {BKV} + {j * BKV}"
         elif ragged and j is None and pingpong:
             mask = "(int)jj"
             mask = f"{mask} * {BKV}"
@@ -514,27 +552,27 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         out = []
         # prologue: K(0), K(1), V(0) into LDS, S(0), then K(2) and V(1) into registers
         out += ["  " + x for x in k_load("0u") + k_store(0)]
-        if KB > 1:
+        if KBL > 1:
             out += ["  " + x for x in k_load("1u") + k_store(1)]
         out += ["  " + x for x in v_load("0u") + v_store(0)]
         out.append("  __syncthreads();")
         out += ["  " + x for x in scores("sA", 0)]
         out.append("  __syncthreads();   // every wave has read Ks[0] before K(2) replaces it")
-        if KB > 2:
+        if KBL > 2:
             out += ["  " + x for x in k_load("2u")]
-        if KB > 1:
+        if KBL > 1:
             out += ["  " + x for x in v_load("1u")]
-        # blocks 0 .. KB-4 have every step; run them in even/odd pairs, then peel the rest
-        npair = max(0, KB - 3) // 2
+        # blocks 0 .. KBL-4 have every step; run them in even/odd pairs, then peel the rest
+        npair = max(0, KBL - 3) // 2
         if npair:
             out.append(f"  for (unsigned int j = 0; j < {2 * npair}u; j += 2u) {{")
             out += ["    {"] + ["      " + x for x in iteration("j", None, 0, True, True, True, True, True)] + ["    }"]
             out += ["    {"] + ["      " + x for x in iteration("j + 1u", None, 1, True, True, True, True, True)] + ["    }"]
             out.append("  }")
-        for j in range(2 * npair, KB):
+        for j in range(2 * npair, KBL):
             out.append(f"  {{  // block {j}")
-            out += ["    " + x for x in iteration(f"{j}u", j, j % 2, j + 1 < KB, j + 2 < KB, j + 1 < KB, j + 3 < KB,
-                                                  j + 2 < KB)]
+            out += ["    " + x for x in iteration(f"{j}u", j, j % 2, j + 1 < KBL, j + 2 < KBL, j + 1 < KBL, j + 3 < KBL,
+                                                  j + 2 < KBL)]
             out.append("  }")
         return out
 
@@ -607,12 +645,84 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 "  }",
                 "}"]
 
+    # key splits: partial rows [split][bh][Sq][Dv] (fp32, unnormalised), then the rows'
+    # (running reference, sum) pairs [split][bh][Sq][2]
+    ml_base = NS * batch * Sq * Dv
+
+    def partial_epilogue_lines() -> list[str]:
+        return ["#pragma unroll", f"  for (int q = 0; q < {QT}; ++q) {{",
+                "    const unsigned int qrow = qrow0 + q * 32u;",
+                "    const float l_tot = tj_pair_sum(l_run[q]);",
+                f"    if (qrow < {Sq}u) {{",
+                f"      const unsigned int prow = ((kb0 / {KBL}u) * {batch}u + (unsigned int)bh) * {Sq}u + qrow;",
+                "#pragma unroll",
+                f"      for (int u = 0; u < {Dv // 32}; ++u)",
+                "#pragma unroll",
+                "        for (int r4 = 0; r4 < 4; ++r4) {",
+                "          tj_f32x4 w;",
+                "          w[0] = o[q][u][r4 * 4]; w[1] = o[q][u][r4 * 4 + 1]; w[2] = o[q][u][r4 * 4 + 2]; w[3] = o[q][u][r4 * 4 + 3];",
+                f"          *(tj_f32x4*)&ws_p[prow * {Dv}u + u * 32 + r4 * 8 + g * 4u] = w;",
+                "        }",
+                "      if (g == 0u) {",
+                f"        ws_p[{ml_base}u + prow * 2u] = m_run[q];",
+                f"        ws_p[{ml_base}u + prow * 2u + 1u] = l_tot;",
+                "      }",
+                "    }",
+                "  }",
+                "}"]
+
     L += [f"  tj_f32x16 sA[{QT}][{BKV // 32}], sB[{QT}][{BKV // 32}];", f"  {opvec} pf[{QT}][{BKV // 16}];"]
     L += pingpong_body() if pingpong else double_buffer_body()
-    L += epilogue_lines()
+    L += epilogue_lines() if NS == 1 else partial_epilogue_lines()
     lds = NST * BKV * (DP + VP) * dt.itemsize
     flops = 2.0 * batch * Sq * Sk * (D + Dv)
     meta = {"family": "attention", "dtype": dt.value, "batch": batch, "Sq": Sq, "Sk": Sk, "D": D, "Dv": Dv,
-            "scale": scale, "lds_bytes": lds, "flops": flops,
+            "scale": scale, "lds_bytes": lds, "flops": flops, "splits": NS,
             "schedule": "pingpong" if pingpong else "double-buffer"}
-    return "\n".join(L), Launch(fname, (-(-Sq // BQ) * batch, 1, 1), (THREADS, 1, 1), 0, meta)
+    main = Launch(fname, (nq * batch * NS, 1, 1), (THREADS, 1, 1), 0, meta)
+    if NS == 1:
+        return "\n".join(L), main
+    meta["workspace"] = (ml_base + NS * batch * Sq * 2) * 4
+    meta["ws_arg"] = True
+    # combine: one lane per 8 consecutive outputs of a row; weights 2^(m_s - max m) over
+    # the splits, out = sum_s w_s * O_s / sum_s w_s * l_s
+    runs = batch * Sq * (Dv // 8)
+    cname = fname + "_combine"
+    pack8 = ("tj_f2bf2({0}, {1})" if dt == DType.bf16 else "tj_f2h({0}) | (tj_f2h({1}) << 16)")
+    C = [f'extern "C" __global__ void __launch_bounds__(256) {cname}(',
+         f"    const {T}* __restrict__ in0_p, const {T}* __restrict__ in1_p, const {T}* __restrict__ in2_p,",
+         f"    {T}* __restrict__ out0_p, const float* __restrict__ ws_p) {{",
+         "  const unsigned int t = blockIdx.x * 256u + threadIdx.x;",
+         f"  if (t >= {runs}u) return;",
+         f"  const unsigned int d8 = (t % {Dv // 8}u) * 8u, row = t / {Dv // 8}u;",
+         f"  const {idx_t} bh = row / {Sq}u;",
+         f"  const unsigned int qrow = row % {Sq}u;",
+         f"  {T}* __restrict__ Ob = out0_p + ({ooff});",
+         f"  float mx = -__builtin_inff();",
+         "#pragma unroll",
+         f"  for (int sp = 0; sp < {NS}; ++sp) mx = fmaxf(mx, ws_p[{ml_base}u + (sp * {batch * Sq}u + row) * 2u]);",
+         "  float lt = 0.0f, acc[8];",
+         "#pragma unroll",
+         "  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;",
+         "#pragma unroll",
+         f"  for (int sp = 0; sp < {NS}; ++sp) {{",
+         f"    const unsigned int prow = sp * {batch * Sq}u + row;",
+         f"    const float w = __builtin_amdgcn_exp2f(ws_p[{ml_base}u + prow * 2u] - mx);",
+         f"    lt += w * ws_p[{ml_base}u + prow * 2u + 1u];",
+         f"    const tj_f32x4 a0 = *(const tj_f32x4*)&ws_p[prow * {Dv}u + d8];",
+         f"    const tj_f32x4 a1 = *(const tj_f32x4*)&ws_p[prow * {Dv}u + d8 + 4u];",
+         "#pragma unroll",
+         "    for (int e = 0; e < 4; ++e) { acc[e] += w * a0[e]; acc[4 + e] += w * a1[e]; }",
+         "  }",
+         "  const float inv = 1.0f / lt;",
+         "  tj_u32x4 pk;",
+         "#pragma unroll",
+         "  for (int e = 0; e < 4; ++e) {",
+         "    const float lo = acc[2 * e] * inv, hi = acc[2 * e + 1] * inv;",
+         "    pk[e] = " + pack8.format("lo", "hi") + ";",
+         "  }",
+         f"  *(tj_u32x4*)&Ob[qrow * {ost}u + d8] = pk;",
+         "}"]
+    cmeta = {"family": "attention_combine", "splits": NS, "ws_arg": True, "batch": batch, "Sq": Sq, "Dv": Dv}
+    comb = Launch(cname, (-(-runs // 256), 1, 1), (256, 1, 1), 0, cmeta)
+    return "\n".join(L) + "\n\n" + "\n".join(C), [main, comb]

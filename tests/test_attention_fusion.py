@@ -50,6 +50,35 @@ def test_attention_layout_rule():
     assert attention_layout(128, 2048, 96, 96) == (4, 1)
 
 
+def test_key_splits_for_grids_short_of_the_cus():
+    """Key-range splits only for 4-wave grids short of one workgroup per CU, with an
+    equal share of at least 2 key blocks each: the smallest count that fills the CUs."""
+    from tensorjit.backends.hip_attention import attention_splits
+
+    assert attention_splits(32, 16, False) == 8          # 2 blocks each, 256 workgroups
+    assert attention_splits(32, 64, False) == 8
+    assert attention_splits(1, 64, False) == 32          # the largest count that divides
+    assert attention_splits(9, 5, False) == 1            # 5 blocks: no equal >= 2-block split
+    assert attention_splits(256, 64, False) == 1         # the grid already fills the CUs
+    assert attention_splits(8, 64, True) == 1            # not for the ping-pong schedule
+
+
+@pytest.mark.parametrize("shapes", [[(2, 2, 1000, 128)] * 3, [(1, 1, 4096, 128)] * 3,
+                                    [(1, 3, 200, 64), (1, 3, 2000, 64), (1, 3, 2000, 128)]])
+def test_split_attention_compiles_with_its_combine_launch(shapes, tj_env):
+    f = fuse_attention(lowered(attn, shapes))
+    src, launches = hb.generate(f)
+    main, comb = launches
+    ns = main.meta["splits"]
+    assert ns > 1 and comb.meta["splits"] == ns and main.meta["ws_arg"] and comb.meta["ws_arg"]
+    B = main.meta["batch"]
+    Sq, Dv = shapes[0][-2], shapes[2][-1]
+    # partial rows plus a (reference, sum) pair per row and split
+    assert main.meta["workspace"] == ns * B * Sq * (Dv + 2) * 4
+    assert comb.grid[0] * 256 >= B * Sq * Dv // 8
+    hb.compile_source(src, "gfx950")
+
+
 def test_two_attention_cores_in_one_program_compile(tj_env):
     """Two fused attention kernels share one module: their lane-pair helpers live in the
     prelude, so the source holds each device function once and hipRTC compiles it."""
@@ -215,14 +244,16 @@ def test_flash_kernel_compiles_for_gfx950(shapes, dtype, forced, tj_env, monkeyp
         monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_WAVES", forced)
     f = fuse_attention(lowered(attn, shapes, dtype))
     src, launches = hb.generate(f)
-    (l,) = launches
+    l = launches[0]
+    # a combine launch exactly when the keys are split
+    assert len(launches) == (2 if l.meta["splits"] > 1 else 1)
     from tensorjit.backends.hip_attention import attention_layout
 
     waves, tiles = attention_layout(l.meta["batch"], shapes[0][-2], shapes[0][-1], shapes[2][-1])
     # the forced ping-pong schedule needs head dims that are multiples of 64
     assert waves == (8 if forced and shapes[0][-1] % 64 == 0 and shapes[2][-1] % 64 == 0 else 4)
     assert "attention" in l.name and l.block == (64 * waves, 1, 1)
-    assert l.grid == (-(-shapes[0][-2] // (32 * waves * tiles)) * l.meta["batch"], 1, 1)
+    assert l.grid == (-(-shapes[0][-2] // (32 * waves * tiles)) * l.meta["batch"] * l.meta["splits"], 1, 1)
     if waves == 8:
         # the last key block computes no scores for a block after it
         kb = -(-shapes[1][-2] // 64)

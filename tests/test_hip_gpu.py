@@ -461,6 +461,52 @@ def test_fused_attention_negative_scale(shapes, monkeypatch):
     close_lowp(out, ref, tol=2e-2)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shapes,scale,splits", [
+    ([(2, 2, 1000, 128)] * 3, 0.088, None),                                   # ragged last block, 8 splits
+    ([(1, 1, 4096, 128)] * 3, 0.088, None),                                   # one head, 32 splits
+    ([(1, 3, 200, 64), (1, 3, 2000, 64), (1, 3, 2000, 128)], 0.125, None),    # Dv != D, ragged
+    ([(1, 2, 300, 64), (1, 2, 1280, 64), (1, 2, 1280, 64)], -0.2, "4"),        # negative scale, forced
+    ([(2, 2, 1, 128), (2, 2, 2048, 128), (2, 2, 2048, 128)], 0.088, "2"),      # one query row
+], ids=["ragged_8", "one_head_32", "dv128_ragged", "negative_scale_4", "single_query_2"])
+def test_key_split_attention_vs_oracle(shapes, scale, splits, dt, monkeypatch):
+    """Key-range splits for grids short of the CUs: partial rows with their running
+    references and sums in the workspace, a second launch combining them, against the
+    fp32 oracle of the reference plan."""
+    if splits:
+        monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_SPLITS", splits)
+    torch.manual_seed(5)
+    q, k, v = [torch.randn(sh, device=DEV).to(dt) for sh in shapes]
+    fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * scale), v)  # noqa: E731
+    print(f"split attention {shapes} {scale} {splits} {dt}", flush=True)
+    f = tj.jit(fn)
+    out = f(q, k, v)
+    cp = f.compiled(q, k, v)
+    fam = [l.meta["family"] for l in cp.launches]
+    assert fam == ["attention", "attention_combine"] and cp.launches[0].meta["splits"] > 1, fam
+    if splits:
+        assert cp.launches[0].meta["splits"] == int(splits)
+    (ref,) = oracle.run(fn, *[t.float().cpu() for t in (q, k, v)])
+    close_lowp(out, ref, tol=2e-2)
+
+
+def test_key_split_attention_with_head_interleaved_layout():
+    """Splits with the head transposes folded into the kernel ([B,S,H,D] reads, the
+    combine writes [B,S,H,Dv] rows), against the fp32 oracle."""
+    torch.manual_seed(6)
+    B, S, Dm, heads = 1, 1024, 256, 2
+    x = torch.randn(B, S, Dm, device=DEV).bfloat16()
+    ws = [(torch.randn(Dm, Dm, device=DEV) / Dm ** 0.5).bfloat16() for _ in range(3)]
+    fn = lambda x, a, b, c: _mha(x, a, b, c, heads)  # noqa: E731
+    f = tj.jit(fn)
+    out = f(x, *ws)
+    cp = f.compiled(x, *ws)
+    fam = [l.meta["family"] for l in cp.launches]
+    assert "attention_combine" in fam and "copy" not in fam, fam
+    (ref,) = oracle.run(fn, *[t.float().cpu() for t in (x, *ws)])
+    close_lowp(out, ref, tol=2e-2)
+
+
 def test_two_fused_attention_layers_in_one_program():
     """Two attention cores in one program (the second reads the first's output as its
     queries): two flash kernels in one module, against the fp32 oracle."""
