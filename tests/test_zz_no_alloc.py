@@ -62,6 +62,27 @@ def test_static_arena_run_matches_the_allocating_run():
         torch.testing.assert_close(got[0], cp(*args)[0], atol=0, rtol=0)
 
 
+def test_static_arena_run_of_key_split_attention():
+    """The fused attention with key splits keeps its partial rows in the workspace: in
+    the static arena they match the allocating run bit for bit, a larger split program
+    first and a smaller one after it."""
+    fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * 0.088), v)  # noqa: E731
+    f = tj.jit(fn)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    cases = [[torch.randn(s, device=DEV, generator=gen).bfloat16() for s in [(2, 2, 1000, 128)] * 3],
+             [torch.randn(s, device=DEV, generator=gen).bfloat16() for s in [(1, 2, 300, 64), (1, 2, 1280, 64),
+                                                                             (1, 2, 1280, 64)]]]
+    sizes = []
+    for args in cases:
+        cp = f.compiled(*args)
+        assert [l.meta["family"] for l in cp.launches] == ["attention", "attention_combine"]
+        assert 0 < cp.arena_bytes <= rt.STATIC_ARENA_BYTES
+        sizes.append(cp.arena_bytes)
+        ref, got = _both(cp, args)
+        assert torch.equal(ref[0], got[0])
+    assert sizes[1] < sizes[0]
+
+
 def test_programs_larger_than_the_static_arena_are_refused():
     args = _inputs(16384)          # 48 MiB LayerNorm output + 192 MiB gelu output
     cp = tj.jit(_mlp).compiled(*args)
