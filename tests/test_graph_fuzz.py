@@ -2,8 +2,10 @@
 
 CPU: every program lowers, gets the backend rewrites and generates HIP that hipRTC
 compiles for gfx950.  GPU: the programs run against the CPU oracle -- float32 within
-1e-5 of the output's magnitude; bfloat16 within 5e-2, since every kernel boundary
-rounds the intermediates to bfloat16 where the oracle keeps float32."""
+1e-5 of the output's magnitude; bfloat16 within 5e-2 and float16 within 1e-2, since
+every kernel boundary rounds the intermediates to the storage type where the oracle
+keeps float32 (torch's own float16 evaluation of these programs is up to 1.6e-3 from
+float64)."""
 
 import pytest
 import torch
@@ -47,7 +49,7 @@ def test_random_program_matches_the_oracle(seed, monkeypatch):
     fn, shapes = graph_fuzz.program(seed)
     g = torch.Generator().manual_seed(seed)
     ins = [torch.randn(s, generator=g) for s in shapes]
-    for dt, tol in ((torch.float32, 1e-5), (torch.bfloat16, 5e-2)):
+    for dt, tol in ((torch.float32, 1e-5), (torch.bfloat16, 5e-2), (torch.float16, 1e-2)):
         print(f"random program {seed} {dt} {shapes}", flush=True)
         outs = tj.jit(fn)(*[t.to(dt).cuda() for t in ins])
         outs = outs if isinstance(outs, (tuple, list)) else [outs]
@@ -156,11 +158,11 @@ def test_random_broadcast_program_generates_and_compiles(seed, tj_env):
 @pytest.mark.parametrize("seed", BCAST_SEEDS)
 def test_random_broadcast_program_matches_the_oracle(seed, monkeypatch):
     """3-D / 4-D programs over size-1 (broadcast) dims with permutes and middle-axis
-    reductions, fp32 (1e-5) and bf16 (5e-2), against the oracle."""
+    reductions, fp32 (1e-5), bf16 (5e-2) and fp16 (1e-2), against the oracle."""
     monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
     fn, shapes = graph_fuzz.broadcast_program(seed)
     print(f"random broadcast program {seed} {shapes}", flush=True)
-    _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])
+    _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2), (torch.float16, 1e-2)])
 
 
 BLOCK_SEEDS = range(12)
