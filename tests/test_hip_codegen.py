@@ -321,3 +321,28 @@ def test_zero_size_tensors_are_refused_before_codegen(case):
     p = C.lower(tj.trace(fn, [TensorType(s, DType.f32) for s in shapes]), "hip")
     with pytest.raises(NotImplementedError, match="zero-size"):
         hb.generate(p)
+
+
+def _loads(fn, shapes, dt):
+    src, _ = hb.generate(C.lower(tj.trace(fn, [TensorType(s, dt) for s in shapes]), "hip"))
+    body = src.split('extern "C"', 1)[1]
+    return [ln.strip().split(" + ")[0] for ln in body.splitlines() if "tj_ldv" in ln]
+
+
+def test_nontemporal_loads_for_streamed_inputs_past_the_mall(monkeypatch):
+    """Inputs read once (no broadcast dim) get the nontemporal hint when the kernel streams
+    at least the 256 MB MALL; broadcast operands never do, and smaller kernels keep
+    plain loads (their inputs may stay cached between calls)."""
+    monkeypatch.delenv("TENSORJIT_HIP_NT_LOADS", raising=False)
+    c2 = lambda x, a, b, c: tj.gelu(x * a + b) * tj.sigmoid(c) + x  # noqa: E731
+    big = [(16384, 4096), (4096,), (4096,), (16384, 4096)]
+    assert _loads(c2, big, DType.f32) == ["tj_ldv_nt(in0_p", "tj_ldv_nt(in1_p", "tj_ldv(in2_p", "tj_ldv(in3_p"]
+    small = [(4096, 4096), (4096,), (4096,), (4096, 4096)]          # 201 MB streamed
+    assert all(x.startswith("tj_ldv(") for x in _loads(c2, small, DType.f32))
+    rms = lambda x, g: tj.rms_norm(x, g)  # noqa: E731
+    assert _loads(rms, [(65536, 4096), (4096,)], DType.bf16) == ["tj_ldv_nt(in0_p", "tj_ldv(in1_p"]
+    assert all(x.startswith("tj_ldv(") for x in _loads(rms, [(8192, 4096), (4096,)], DType.bf16))
+    monkeypatch.setenv("TENSORJIT_HIP_NT_LOADS", "1")
+    assert _loads(rms, [(8192, 4096), (4096,)], DType.bf16) == ["tj_ldv_nt(in0_p", "tj_ldv(in1_p"]
+    monkeypatch.setenv("TENSORJIT_HIP_NT_LOADS", "0")
+    assert all(x.startswith("tj_ldv(") for x in _loads(c2, big, DType.f32))
