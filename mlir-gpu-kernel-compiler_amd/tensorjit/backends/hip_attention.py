@@ -272,11 +272,11 @@ def attention_splits(tiles: int, KB: int, pingpong: bool) -> int:
     combines them.  The smallest split count that reaches 256 workgroups, else the largest
     one that divides ``KB``; 1 for the ping-pong schedule and for full grids.
     TENSORJIT_HIP_ATTENTION_SPLITS=n forces n where it divides ``KB`` into >= 2-block parts."""
-    forced = os.environ.get("TENSORJIT_HIP_ATTENTION_SPLITS")
+    forced = os.environ.get("TENSORJIT_HIP_ATTENTION_SPLITS", "")
     ok = [n for n in range(2, 33) if KB % n == 0 and KB // n >= 2]
     if pingpong:
         return 1
-    if forced is not None:
+    if forced.isdigit():
         return int(forced) if int(forced) in ok else 1
     if tiles >= CU_COUNT or not ok:
         return 1
