@@ -38,7 +38,7 @@ from dataclasses import dataclass, field
 
 from ..ir import DType, Node
 from ..passes import Kernel
-from .common import access_strides, emit_expr, inner_stride, offset_expr
+from .common import access_strides, emit_expr, inner_stride, merged_dims, offset_expr
 from .hip_prelude import CTYPE, vec_width
 
 THREADS = 256
@@ -251,6 +251,79 @@ def gen_elementwise(g: KernelGen) -> tuple[str, Launch]:
     return gen_pointwise(g, g.k.nodes, tuple(g.k.iter_shape))
 
 
+TT = 64          # tiled transpose: tile edge in elements
+
+
+def _tiled_transpose_plan(shape, st, itemsize):
+    """For a transpose whose output's innermost dim is strided in the source: the merged
+    dim groups as (E0, s0) -- the output's innermost (source stride s0) --, (Er, Ir) --
+    the group that is contiguous in the source (output stride Ir) -- and the rest as
+    batch groups [(extent, output stride, source stride)], or None when the plain copy
+    applies (vectorisable, broadcast, or 16-byte alignment not given)."""
+    groups = merged_dims(shape, st)
+    if len(groups) < 2 or groups[0][2] in (0, 1):
+        return None
+    vec = 16 // itemsize
+    rg = [i for i, g in enumerate(groups) if g[2] == 1]
+    if len(rg) != 1:
+        return None
+    E0, _, s0 = groups[0]
+    Er, Ir, _ = groups[rg[0]]
+    batch = [g for i, g in enumerate(groups) if i not in (0, rg[0])]
+    # 16-byte vectors along the source's contiguous group (reads) and the output's
+    # innermost group (writes): every row start of either must be 16-byte aligned
+    if E0 % vec or Er % vec or s0 % vec or any(g[2] % vec or g[1] % vec for g in batch) or Ir % vec:
+        return None
+    return E0, s0, Er, Ir, batch
+
+
+def gen_copy_tiled(g: KernelGen, plan) -> tuple[str, Launch]:
+    """Transpose whose output's innermost dim is strided in the source, through LDS:
+    a workgroup moves a TT x TT tile -- 16-byte loads along the source's contiguous
+    dim into LDS rows, then 16-byte stores along the output's innermost dim gathered
+    from LDS columns -- so both HBM streams are coalesced (the plain copy gathers
+    single elements at the source stride)."""
+    k = g.k
+    node = k.anchor
+    (src,) = k.inputs if k.inputs else (node.inputs[0],)
+    E0, s0, Er, Ir, batch = plan
+    ct = CTYPE[node.dtype]
+    isz = node.dtype.itemsize
+    vec = 16 // isz
+    numel = math.prod(node.shape)
+    idx_t = _index_type(numel)
+    tc, tr = -(-E0 // TT), -(-Er // TT)
+    nb = math.prod(e for e, _, _ in batch) if batch else 1
+    vpr = TT // vec                        # 16-byte vectors per tile row
+    per = TT * vpr // THREADS              # vectors per lane per phase
+    pitch = TT + vec                       # LDS row pitch: 16 bytes of padding keep rows 16-byte aligned
+    sname = g.names[id(src)]
+    L = [f'extern "C" __global__ __launch_bounds__({THREADS}) void {g.fname}({g.params()}) {{',
+         f"  __shared__ __attribute__((aligned(16))) {ct} T_[{TT}][{pitch}];",
+         f"  const unsigned int tid = threadIdx.x, c0 = (blockIdx.x % {tc}u) * {TT}u,"
+         f" r0 = ((blockIdx.x / {tc}u) % {tr}u) * {TT}u;",
+         f"  {idx_t} bi = blockIdx.x / {tc * tr}u, so = 0, oo = 0;"]
+    for j, (e, ostride, sstride) in enumerate(batch):
+        L.append(f"  {{ const {idx_t} x_ = bi % {e}u; bi /= {e}u; so += x_ * {sstride}u; oo += x_ * {ostride}u; }}")
+    # load: tile row = output-inner index c (source stride s0), 16 bytes along r
+    L += ["#pragma unroll", f"  for (int u = 0; u < {per}; ++u) {{",
+          f"    const unsigned int v = u * {THREADS}u + tid, c = v / {vpr}u, r = (v % {vpr}u) * {vec}u;",
+          f"    if (c0 + c < {E0}u && r0 + r < {Er}u)",
+          f"      *(tj_u32x4*)&T_[c][r] = *(const tj_u32x4*)&{sname}_p[so + ({idx_t})(c0 + c) * {s0}u + r0 + r];",
+          "  }", "  __syncthreads();",
+          # store: output row = r, 16 bytes along c, gathered from the LDS column
+          "#pragma unroll", f"  for (int u = 0; u < {per}; ++u) {{",
+          f"    const unsigned int v = u * {THREADS}u + tid, r = v / {vpr}u, c = (v % {vpr}u) * {vec}u;",
+          f"    if (c0 + c < {E0}u && r0 + r < {Er}u) {{",
+          f"      {ct} t_[{vec}];",
+          "#pragma unroll",
+          f"      for (int j = 0; j < {vec}; ++j) t_[j] = T_[c + j][r];",
+          f"      tj_st16(out0_p + oo + ({idx_t})(r0 + r) * {Ir}u + c0 + c, *(const tj_u32x4*)t_);",
+          "    }", "  }", "}"]
+    meta = {"family": "copy", "vec": vec, "tiled": TT, "numel": numel}
+    return "\n".join(L), Launch(g.fname, (tc * tr * nb, 1, 1), (THREADS, 1, 1), 0, meta)
+
+
 def gen_copy(g: KernelGen) -> tuple[str, Launch]:
     """Materialised transpose / broadcast_to: a bit-exact move of storage elements."""
     k = g.k
@@ -261,6 +334,10 @@ def gen_copy(g: KernelGen) -> tuple[str, Launch]:
     ct = CTYPE[node.dtype]
     st = access_strides(src, node, shape)
     inner = inner_stride(shape, st)
+    if node.op == "transpose" and len(k.outputs) == 1 and k.outputs[0] is node and node.dtype == src.dtype:
+        plan = _tiled_transpose_plan(shape, st, node.dtype.itemsize)
+        if plan is not None:
+            return gen_copy_tiled(g, plan)
     row_len = shape[-1] if shape else 1
     vec = _vec_for(row_len, numel, node.dtype)
     nvec = numel // vec

@@ -117,6 +117,21 @@ def test_transpose_reshape_and_copies_are_bit_exact():
         assert torch.equal(h(y), y.permute(3, 0, 2, 1).contiguous())
 
 
+@pytest.mark.parametrize("shape,perm", [((128, 64), (1, 0)), ((104, 48), (1, 0)), ((3, 40, 72), (2, 0, 1)),
+                                        ((5, 8, 16, 24), (3, 1, 0, 2)), ((2, 3, 96, 80), (0, 1, 3, 2)),
+                                        ((6, 5, 16, 8), (1, 3, 0, 2)), ((1000, 520), (1, 0))])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16, torch.int32])
+def test_tiled_transposes_are_bit_exact(shape, perm, dt):
+    """Transposes whose output's innermost dim is strided in the source go through the
+    LDS-tiled copy (ragged edge tiles included), bit for bit against torch."""
+    g = torch.Generator(device=DEV).manual_seed(7)
+    y = (torch.randn(shape, device=DEV, generator=g) * 1000).to(dt)
+    f = tj.jit(lambda t: tj.permute(t, *perm))
+    out = f(y)
+    assert f.compiled(y).launches[0].meta.get("tiled") == 64
+    assert torch.equal(out, y.permute(*perm).contiguous())
+
+
 def test_int32_arithmetic_and_max_are_exact_below_2_24():
     """int32 storage: pointwise ops evaluate in fp32, as the reference's expressions do, and
     convert on store, so integer results below 2^24 in magnitude are exact -- a pointwise chain
