@@ -346,3 +346,49 @@ def test_nontemporal_loads_for_streamed_inputs_past_the_mall(monkeypatch):
     assert _loads(rms, [(8192, 4096), (4096,)], DType.bf16) == ["tj_ldv_nt(in0_p", "tj_ldv(in1_p"]
     monkeypatch.setenv("TENSORJIT_HIP_NT_LOADS", "0")
     assert all(x.startswith("tj_ldv(") for x in _loads(c2, big, DType.f32))
+
+
+def test_tiled_transpose_plan_and_index_math():
+    """The tiled transpose applies where the output's innermost dim is strided in the
+    source and both 16-byte row starts are aligned; its tile index math (the loops of
+    gen_copy_tiled, replayed on the CPU over every workgroup and lane) reproduces
+    numpy's permute exactly, ragged edge tiles included."""
+    import numpy as np
+    from tensorjit.backends import hip_kernels as hk
+
+    def plan(shape_in, perm, isz):
+        cs = [int(np.prod(shape_in[i + 1:])) for i in range(len(shape_in))]
+        return hk._tiled_transpose_plan(tuple(shape_in[p] for p in perm), tuple(cs[p] for p in perm), isz)
+
+    assert plan((4, 64, 8, 32), (0, 2, 1, 3), 2) is None        # innermost dim stays contiguous: vector copy
+    assert plan((100, 40), (1, 0), 2) is None                    # 100 bf16 rows: not 16-byte aligned
+    assert plan((7, 64, 8), (2, 1, 0), 4) is None
+
+    def replay(shape_in, perm, isz):
+        x = np.arange(int(np.prod(shape_in)), dtype=np.int64).reshape(shape_in)
+        ref = np.ascontiguousarray(np.transpose(x, perm)).reshape(-1)
+        E0, s0, Er, Ir, batch = plan(shape_in, perm, isz)
+        TT, vec, T = hk.TT, 16 // isz, hk.THREADS
+        tc, tr = -(-E0 // TT), -(-Er // TT)
+        vpr = TT // vec
+        src, out = x.reshape(-1), np.full(ref.shape, -1, dtype=np.int64)
+        for blk in range(tc * tr * int(np.prod([e for e, _, _ in batch]) if batch else 1)):
+            c0, r0, bi, so, oo = (blk % tc) * TT, ((blk // tc) % tr) * TT, blk // (tc * tr), 0, 0
+            for e, ost, sst in batch:
+                so, oo, bi = so + (bi % e) * sst, oo + (bi % e) * ost, bi // e
+            tile = np.zeros((TT, TT + vec), dtype=np.int64)
+            for v in range(TT * vpr):
+                c, r = v // vpr, (v % vpr) * vec
+                if c0 + c < E0 and r0 + r < Er:
+                    tile[c, r:r + vec] = src[so + (c0 + c) * s0 + r0 + r:][:vec]
+            for v in range(TT * vpr):
+                r, c = v // vpr, (v % vpr) * vec
+                if c0 + c < E0 and r0 + r < Er:
+                    o = oo + (r0 + r) * Ir + c0 + c
+                    out[o:o + vec] = tile[c:c + vec, r]
+        assert np.array_equal(out, ref), (shape_in, perm, isz)
+
+    for shape_in, perm, isz in [((128, 64), (1, 0), 2), ((104, 48), (1, 0), 4), ((3, 40, 72), (2, 0, 1), 2),
+                                ((5, 8, 16, 24), (3, 1, 0, 2), 4), ((2, 3, 96, 80), (0, 1, 3, 2), 2),
+                                ((6, 5, 16, 8), (1, 3, 0, 2), 4)]:
+        replay(shape_in, perm, isz)
