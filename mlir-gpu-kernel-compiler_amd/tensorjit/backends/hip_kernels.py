@@ -26,7 +26,9 @@ stage) and values needed by later stages stay in VGPRs.  A reduction is a
 per-lane partial, a wave64 DPP all-reduce and, with more than one wave per
 row, one LDS exchange between the waves (one barrier, its own LDS slots per
 reduction so consecutive reductions never race).  A row group without any
-reduction is emitted as a flat family-1 loop nest over ``rows x N``.
+reduction is emitted as a flat family-1 loop nest over ``rows x N``.  A
+stand-alone reduction over few long rows splits each row over workgroups
+(``row_split``): partials into the workspace, then a combine launch per row.
 """
 from __future__ import annotations
 
@@ -38,6 +40,7 @@ from dataclasses import dataclass, field
 
 from ..ir import DType, Node
 from ..passes import Kernel
+from ..runtime.autotune import CU_COUNT
 from .common import access_strides, emit_expr, inner_stride, merged_dims, offset_expr
 from .hip_prelude import CTYPE, vec_width
 
@@ -432,6 +435,46 @@ def row_shape(N: int, vec: int, streaming_ok: bool) -> RowShape:
     return RowShape(t, nch, streaming, 1)
 
 
+# A reduction over few long rows splits each row over workgroups.  With one workgroup
+# per row, a [1, 2^26] fp32 sum ran on one CU at 62 GB/s (4.3 ms).  Here a row is cut
+# into segments of SPLIT_CHUNKS chunks of SPLIT_THREADS x 16 bytes.  Each of ``S``
+# workgroups per row loops over every S-th segment.  It preloads the segment's chunks,
+# folds them into its partial, and writes the partial to the workspace.  A second
+# launch, one workgroup per row, combines the partials.  It then divides a mean by N
+# and runs the reduction's epilogue.  Measured on MI355X, fp32 sum (max alike), one
+# workgroup per row -> split: [1, 2^26] 4330 -> 39.5 us (6.8 TB/s; torch 47.5),
+# [8, 2^23] 524 -> 39.7, [64, 2^20] 78.9 -> 42.5, [1, 2^20] 29.4 -> 4.2, [8, 2^18]
+# 8.7 -> 4.5; the combine launch costs 2.0 us, so 256 KiB rows lose ([1, 2^16]
+# 3.2 -> 4.4) and [200, 2^16] gains nothing (10.9 -> 10.6).  TENSORJIT_HIP_ROW_SPLIT=0 / 1
+# forces the split off / on.
+SPLIT_THREADS = 256
+SPLIT_CHUNKS = 8
+SPLIT_MIN_ROW_BYTES = 512 << 10
+
+
+@dataclass(frozen=True)
+class RowSplit:
+    chunks: int         # chunks per lane per segment
+    segments: int       # segments per row
+    splits: int         # workgroups per row
+
+
+def row_split(nrows: int, N: int, vec: int, itemsize: int) -> RowSplit | None:
+    """Split of a single-stage reduction over ``nrows`` rows of ``N`` elements, or None
+    when one workgroup per row already fills the chip or a row is short.  About
+    4 x CU_COUNT workgroups in all; segments shrink, down to one chunk per lane, until
+    the row count times the segments per row reaches that."""
+    forced = os.environ.get("TENSORJIT_HIP_ROW_SPLIT")
+    if forced == "0" or (forced != "1" and (nrows >= CU_COUNT or N * itemsize < SPLIT_MIN_ROW_BYTES)):
+        return None
+    target = 4 * CU_COUNT
+    per_row = -(-N // (SPLIT_THREADS * vec))
+    nch = max(1, min(SPLIT_CHUNKS, per_row * nrows // target))
+    segs = -(-per_row // nch)
+    splits = min(segs, -(-target // nrows))
+    return RowSplit(nch, segs, splits) if splits > 1 else None
+
+
 def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[str, Launch]:
     k = g.k
     nrows = math.prod(rows) if rows else 1
@@ -442,13 +485,18 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
 
     dt = _kernel_dtype(k)
     vec = _vec_for(N, N, dt)
-    shape = row_shape(N, vec, streaming_ok=len(stages) == 1)
-    T, NCH, streaming, R = shape.lanes, shape.chunks, shape.streaming, shape.rows_per_block
+    split = row_split(nrows, N, vec, dt.itemsize) if len(stages) == 1 and stages[0].kind == "reduce" else None
+    if split:
+        T, NCH, streaming, R = SPLIT_THREADS, split.chunks, False, 1
+    else:
+        shape = row_shape(N, vec, streaming_ok=len(stages) == 1)
+        T, NCH, streaming, R = shape.lanes, shape.chunks, shape.streaming, shape.rows_per_block
     if R > 1 and nrows < R * 256:
         # too few rows to fill the chip with R-row workgroups: one row per workgroup
         R = 1
     nwaves = T // 64
-    full = N % (T * vec) == 0
+    # every chunk in bounds: whole rows of chunks, and with a split whole segments
+    full = N % (T * vec * (NCH if split else 1)) == 0
     inside = {id(n) for n in k.nodes}
     escaping = {id(o): j for j, o in enumerate(k.outputs)}
     stage_of = {id(n): si for si, st in enumerate(stages) for n in st.nodes}
@@ -492,10 +540,16 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
     nt = _nt_loads(sum(math.prod(n.shape) * n.dtype.itemsize for i, (n, _) in vec_ext.items() if i in ext_streamed)
                    + sum(math.prod(o.shape or (1,)) * o.dtype.itemsize for o in k.outputs))
 
-    L = [f'extern "C" __global__ __launch_bounds__({T * R}) void {g.fname}({g.params()}) {{']
+    ws_param = ", float* __restrict__ ws_p" if split else ""
+    L = [f'extern "C" __global__ __launch_bounds__({T * R}) void {g.fname}({g.params()}{ws_param}) {{']
     if nred and nwaves > 1:
         L.append(f"  __shared__ float tj_red[{nred}][{nwaves}];")
-    if R == 1:
+    if split:
+        # workgroup (r, sb): segments sb, sb + S, ... of row r
+        L.append(f"  const {idx_t} r = blockIdx.x / {split.splits}u;")
+        L.append(f"  const unsigned int sb = blockIdx.x % {split.splits}u;")
+        L.append("  const unsigned int tid = threadIdx.x;")
+    elif R == 1:
         L.append(f"  const {idx_t} r = blockIdx.x;")
         L.append("  const unsigned int tid = threadIdx.x;")
     else:
@@ -509,6 +563,7 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
         L.append("  float " + ", ".join(g.names[id(n)] for n in scalars) + ";")
 
     def chunk_open(c: str, body_indent: str = "    ") -> list[str]:
+        c = f"(seg * {NCH}u + {c})" if split else c
         out = [f"  {{ const unsigned int n0 = ({c} * {T}u + tid) * {vec}u;"]
         if not full:
             out.append(f"  if (n0 < {N}u) {{")
@@ -530,14 +585,17 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
             L.append(f"  float {nm}_r[{NCH}][{vec}];")
         for n in kept:
             L.append(f"  float {g.names[id(n)]}_r[{NCH}][{vec}];")
-        if vec_ext:
-            L.append("#pragma unroll")
-            L.append(f"  for (int c = 0; c < {NCH}; ++c) {{")
-            L += ["  " + s for s in chunk_open("c")]
-            for n, strides in vec_ext.values():
-                L += ["      " + s for s in ext_load(n, strides, f"{g.names[id(n)]}_r[c]")]
-            L += ["  " + s for s in chunk_close()]
-            L.append("  }")
+    preload_lines = []
+    if preload and vec_ext:
+        preload_lines.append("#pragma unroll")
+        preload_lines.append(f"  for (int c = 0; c < {NCH}; ++c) {{")
+        preload_lines += ["  " + s for s in chunk_open("c")]
+        for n, strides in vec_ext.values():
+            preload_lines += ["      " + s for s in ext_load(n, strides, f"{g.names[id(n)]}_r[c]")]
+        preload_lines += ["  " + s for s in chunk_close()]
+        preload_lines.append("  }")
+    if not split:
+        L += preload_lines
 
     def elem_value(n: Node) -> str:
         """fp32 value of input/earlier-stage node ``n`` at (chunk c, lane element j)."""
@@ -630,17 +688,19 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
             upd = f"acc{st_i} = fmaxf(acc{st_i}, {xv});" if is_max else f"acc{st_i} += {xv};"
             L.append(f"  float acc{st_i} = {init};")
             used = [n for n in st.inputs if any(n in m.inputs for m in prologue + [red])]
-            L += chunk_loop(elem_block(prologue, used, [upd]))
-            wave = "tj_wave_max" if is_max else "tj_wave_sum"
-            L.append(f"  acc{st_i} = {wave}(acc{st_i});")
-            if nwaves > 1:
-                L.append(f"  if ((tid & 63u) == 0u) tj_red[{red_slot}][tid >> 6] = acc{st_i};")
-                L.append("  __syncthreads();")
-                L.append(f"  acc{st_i} = tj_red[{red_slot}][0];")
-                for w in range(1, nwaves):
-                    comb = f"fmaxf(acc{st_i}, tj_red[{red_slot}][{w}])" if is_max else f"acc{st_i} + tj_red[{red_slot}][{w}]"
-                    L.append(f"  acc{st_i} = {comb};")
+            if split:
+                # this workgroup's segments of the row: preload one, fold it in, next
+                L.append(f"  for (unsigned int seg = sb; seg < {split.segments}u; seg += {split.splits}u) {{")
+                L += ["  " + s for s in preload_lines + chunk_loop(elem_block(prologue, used, [upd]))]
+                L.append("  }")
+            else:
+                L += chunk_loop(elem_block(prologue, used, [upd]))
+            L += _block_reduce_lines(f"acc{st_i}", is_max, nwaves, red_slot)
             red_slot += 1
+            if split:
+                # the partial of segments sb, sb + S, ...; the combine launch finishes the row
+                L.append(f"  if (tid == 0u) ws_p[blockIdx.x] = acc{st_i};")
+                break
             if red.op == "mean":
                 L.append(f"  {g.names[id(red)]} = acc{st_i} / {float(N)!r}f;")
             else:
@@ -656,4 +716,49 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
     L.append("}")
     meta = {"family": "row", "vec": vec, "threads": T, "chunks": NCH, "streaming": streaming, "rows": nrows, "n": N,
             "rows_per_block": R}
-    return "\n".join(L), Launch(g.fname, (-(-nrows // R), 1, 1), (T * R, 1, 1), 0, meta)
+    if not split:
+        return "\n".join(L), Launch(g.fname, (-(-nrows // R), 1, 1), (T * R, 1, 1), 0, meta)
+
+    # combine launch: one workgroup per row folds the row's S partials, then the
+    # reduction's finish (mean: / N) and its epilogue, as the one-workgroup row does
+    st = stages[0]
+    red = st.anchor
+    S = split.splits
+    is_max = red.op == "max"
+    C = [f'extern "C" __global__ __launch_bounds__({COMBINE_THREADS}) void {g.fname}_combine({g.params()}, '
+         "const float* __restrict__ ws_p) {",
+         f"  __shared__ float tj_red[1][{COMBINE_THREADS // 64}];",
+         f"  const {idx_t} r = blockIdx.x;",
+         "  const unsigned int tid = threadIdx.x;"]
+    if scalars:
+        C.append("  float " + ", ".join(g.names[id(n)] for n in scalars) + ";")
+    C.append(f"  float acc = {'(-__builtin_inff())' if is_max else '0.0f'};")
+    upd = "acc = fmaxf(acc, ws_p[r * {S}u + s]);" if is_max else "acc += ws_p[r * {S}u + s];"
+    C.append(f"  for (unsigned int s = tid; s < {S}u; s += {COMBINE_THREADS}u) " + upd.format(S=S))
+    C += _block_reduce_lines("acc", is_max, COMBINE_THREADS // 64, 0)
+    C.append(f"  {g.names[id(red)]} = acc{' / ' + repr(float(N)) + 'f' if red.op == 'mean' else ''};")
+    C += scalar_store(red)
+    C += scalar_lines(st.nodes[st.nodes.index(red) + 1:], st, tuple(red.shape), "r", anchor=red)
+    C.append("}")
+    meta.update({"splits": S, "segments": split.segments, "workspace": nrows * S * 4, "ws_arg": True})
+    cmeta = {"family": "row_combine", "splits": S, "rows": nrows, "ws_arg": True}
+    return "\n".join(L) + "\n\n" + "\n".join(C), [
+        Launch(g.fname, (nrows * S, 1, 1), (T, 1, 1), 0, meta),
+        Launch(g.fname + "_combine", (nrows, 1, 1), (COMBINE_THREADS, 1, 1), 0, cmeta)]
+
+
+COMBINE_THREADS = 256
+
+
+def _block_reduce_lines(acc: str, is_max: bool, nwaves: int, slot: int) -> list[str]:
+    """All-reduce of ``acc`` over the workgroup: wave64 DPP, then (several waves) one
+    exchange through LDS slots ``tj_red[slot]`` behind one barrier."""
+    out = [f"  {acc} = {'tj_wave_max' if is_max else 'tj_wave_sum'}({acc});"]
+    if nwaves > 1:
+        out.append(f"  if ((tid & 63u) == 0u) tj_red[{slot}][tid >> 6] = {acc};")
+        out.append("  __syncthreads();")
+        out.append(f"  {acc} = tj_red[{slot}][0];")
+        for w in range(1, nwaves):
+            comb = f"fmaxf({acc}, tj_red[{slot}][{w}])" if is_max else f"{acc} + tj_red[{slot}][{w}]"
+            out.append(f"  {acc} = {comb};")
+    return out

@@ -392,3 +392,62 @@ def test_tiled_transpose_plan_and_index_math():
                                 ((5, 8, 16, 24), (3, 1, 0, 2), 4), ((2, 3, 96, 80), (0, 1, 3, 2), 2),
                                 ((6, 5, 16, 8), (1, 3, 0, 2), 4)]:
         replay(shape_in, perm, isz)
+
+
+def test_row_split_rule_and_index_math(monkeypatch):
+    """Reductions over fewer rows than CUs, each row at least 512 KiB, split each row over
+    workgroups.  The segment and chunk index math of the split kernel (replayed on the
+    CPU over every workgroup, segment, chunk and lane) reads every element of every row
+    exactly once, and every workgroup writes its own workspace slot."""
+    import numpy as np
+    from tensorjit.backends import hip_kernels as hk
+    from tensorjit.runtime.autotune import CU_COUNT
+
+    assert hk.row_split(CU_COUNT, 1 << 20, 4, 4) is None          # one workgroup per row fills the chip
+    assert hk.row_split(8, 32768, 4, 4) is None                  # 128 KiB rows: one workgroup each
+    assert hk.row_split(1, 1 << 26, 4, 4) == hk.RowSplit(8, 8192, 1024)
+    assert hk.row_split(1, 65536, 4, 4) is None                  # 256 KiB: the combine launch costs more
+    assert hk.row_split(1, 131072, 4, 4) == hk.RowSplit(1, 128, 128)   # short enough for one chunk a segment
+    monkeypatch.setenv("TENSORJIT_HIP_ROW_SPLIT", "0")
+    assert hk.row_split(1, 1 << 26, 4, 4) is None
+    monkeypatch.setenv("TENSORJIT_HIP_ROW_SPLIT", "1")
+    assert hk.row_split(37, 5000, 4, 4) == hk.RowSplit(1, 5, 5)
+
+    def replay(nrows, N, vec, sp):
+        T, NCH, S, SEGS = hk.SPLIT_THREADS, sp.chunks, sp.splits, sp.segments
+        seen = np.zeros(nrows * N, dtype=np.int64)
+        slots = np.zeros(nrows * S, dtype=np.int64)
+        for blk in range(nrows * S):
+            r, sb = blk // S, blk % S
+            for seg in range(sb, SEGS, S):
+                for c in range(NCH):
+                    n0 = (np.arange(T) + (seg * NCH + c) * T) * vec
+                    for n in n0[n0 < N]:
+                        seen[r * N + n:r * N + n + vec] += 1
+            slots[blk] += 1
+        assert (seen == 1).all() and (slots == 1).all(), (nrows, N, vec, sp)
+
+    for nrows, N, vec in [(1, 300000, 4), (3, 5000, 4), (2, 300001, 1), (5, 40000, 8), (1, 1 << 20, 4)]:
+        replay(nrows, N, vec, hk.row_split(nrows, N, vec, 4))
+
+
+@pytest.mark.parametrize("case", ["sum", "mse", "rms_bf16", "max_keepdim", "odd"])
+def test_split_reductions_generate_and_compile(case, tj_env):
+    cases = {
+        "sum": (lambda x: tj.sum(x), [(1 << 23,)], DType.f32, "sum"),
+        "mse": (lambda x, y: tj.mean((x - y) * (x - y), axis=-1), [(3, 300000)] * 2, DType.f32, "mean"),
+        "rms_bf16": (lambda x: tj.sqrt(tj.mean(x * x, axis=-1) + 1e-5), [(8, 262144)], DType.bf16, "mean"),
+        "max_keepdim": (lambda x: tj.max(x, axis=-1, keepdim=True) * 2.0, [(4, 262144)], DType.f32, "max"),
+        "odd": (lambda x: tj.sum(tj.abs(x), axis=-1), [(2, 300001)], DType.f32, "sum"),
+    }
+    fn, shapes, dt, red = cases[case]
+    p = C.lower(tj.trace(fn, [TensorType(s, dt) for s in shapes]), "hip")
+    src, launches = hb.generate(p)
+    part, comb = launches
+    nrows = part.meta["rows"]
+    assert comb.meta["family"] == "row_combine" and comb.grid == (nrows, 1, 1)
+    assert part.grid == (nrows * part.meta["splits"], 1, 1) and part.meta["workspace"] == nrows * part.meta["splits"] * 4
+    assert part.meta["ws_arg"] and comb.meta["ws_arg"]
+    if red == "mean":
+        assert f"acc / {float(shapes[0][-1])!r}f" in src
+    hb.compile_source(src, "gfx950")

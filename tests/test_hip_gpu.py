@@ -223,6 +223,74 @@ def test_reductions(n):
     assert torch.equal(mu.cpu().reshape(-1), exact.float() / float(n))
 
 
+SPLIT_CASES = {
+    # full reduction of one long row: 1024 workgroups, one 8-chunk segment each
+    "sum_1row": (lambda x: tj.sum(x), [(1 << 23,)], torch.float32),
+    # two workgroups' worth of segments per workgroup (the segment loop runs twice)
+    "sum_loop": (lambda x: tj.sum(x, axis=-1), [(1, 1 << 24)], torch.float32),
+    # mean of a two-input prologue, a ragged last chunk (300000 = 292.97 chunks)
+    "mse": (lambda x, y: tj.mean((x - y) * (x - y), axis=-1), [(3, 300000), (3, 300000)], torch.float32),
+    # bf16 rows, epilogue after the mean
+    "rms": (lambda x: tj.sqrt(tj.mean(x * x, axis=-1) + 1e-5), [(8, 262144)], torch.bfloat16),
+    # max with a keepdim output and an epilogue
+    "max": (lambda x: tj.max(x, axis=-1, keepdim=True) * 2.0, [(4, 262144)], torch.float32),
+    # an odd row length: scalar lanes (one element per lane)
+    "odd": (lambda x: tj.sum(tj.abs(x), axis=-1), [(2, 300001)], torch.float32),
+    # a prologue value stored as a second output beside the row sum
+    "vec_out": (lambda x: (tj.exp(tj.tanh(x)), tj.sum(tj.exp(tj.tanh(x)), axis=-1)), [(2, 262144)], torch.float32),
+}
+
+
+@pytest.mark.parametrize("case", sorted(SPLIT_CASES))
+def test_split_row_reductions_vs_oracle(case):
+    """Reductions over few long rows, split over workgroups with a combine launch: against
+    the oracle, and on small integers (every partial sum exact) bit for bit against the
+    exact sum, so a dropped or doubled chunk or segment shows."""
+    fn, shapes, dt = SPLIT_CASES[case]
+    torch.manual_seed(0)
+    print(f"split reduction {case} {shapes} {dt}", flush=True)
+    args = [torch.randn(s, device=DEV).to(dt) for s in shapes]
+    f = tj.jit(fn)
+    launches = f.compiled(*args).launches
+    assert [l.meta["family"] for l in launches[-2:]] == ["row", "row_combine"], case
+    n = shapes[0][-1]
+    outs = f(*args)
+    outs = outs if isinstance(outs, tuple) else (outs,)
+    refs = oracle.run(fn, *[a.float().cpu() for a in args])
+    for o, r in zip(outs, refs):
+        assert o.shape == r.shape
+        if o.dtype == torch.float32:
+            close_f32(o, r, scale=1e-5 * math.sqrt(n / 1024))
+        else:
+            close_lowp(o, r)
+    if case == "max":
+        assert torch.equal(outs[0], args[0].amax(-1, keepdim=True) * 2.0)
+    if case in ("sum_1row", "sum_loop", "odd"):
+        xi = torch.randint(-3, 4, shapes[0], device=DEV).float()
+        exact = xi.abs().double().sum(-1) if case == "odd" else xi.double().sum(-1)
+        assert torch.equal(f(xi).double(), exact)
+
+
+def test_forced_split_of_short_ragged_rows(monkeypatch):
+    """The split forced onto short rows (37 rows of 5000: five one-chunk segments per row,
+    the last part-used) agrees with one workgroup per row: sums on small integers bit for
+    bit, the max bit for bit, the mean to rounding."""
+    torch.manual_seed(0)
+    x = torch.randint(-3, 4, (37, 5000), device=DEV).float()
+    fn = lambda t: (tj.sum(t, axis=-1), tj.max(t * 0.5 + 1.0, axis=-1), tj.mean(t * t, axis=-1))  # noqa: E731
+    monkeypatch.setenv("TENSORJIT_HIP_ROW_SPLIT", "1")
+    fs = tj.jit(fn)
+    assert sum(l.meta["family"] == "row_combine" for l in fs.compiled(x).launches) == 3
+    split = fs(x)
+    monkeypatch.setenv("TENSORJIT_HIP_ROW_SPLIT", "0")
+    fo = tj.jit(lambda t: (tj.sum(t, axis=-1), tj.max(t * 0.5 + 1.0, axis=-1), tj.mean(t * t, axis=-1)))
+    assert not any(l.meta["family"] == "row_combine" for l in fo.compiled(x).launches)
+    one = fo(x)
+    assert torch.equal(split[0], one[0]) and torch.equal(split[1], one[1])
+    torch.testing.assert_close(split[2], one[2], rtol=1e-6, atol=0)
+    assert torch.equal(split[0].double(), x.double().sum(-1))
+
+
 def test_reduce_non_last_axis_via_transpose():
     torch.manual_seed(0)
     x = torch.randn(4, 5, 6, device=DEV)
