@@ -271,6 +271,20 @@ def test_split_row_reductions_vs_oracle(case):
         assert torch.equal(f(xi).double(), exact)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_norms_over_rows_past_the_row_fusion_limit(dt):
+    """LayerNorm / RMSNorm / softmax over 3 rows of 300000: the plan gives their reductions
+    and pointwise steps kernels of their own (rows past 8192 are not row-fused), and
+    each reduction splits its rows over workgroups."""
+    torch.manual_seed(0)
+    x = (torch.randn(3, 300000, device=DEV) * 2).to(dt)
+    g = (1 + 0.1 * torch.randn(300000, device=DEV)).to(dt)
+    print(f"long-row norms {dt}", flush=True)
+    f, _ = check_vs_oracle(lambda t, w: (tj.layer_norm(t, w), tj.rms_norm(t, w), tj.softmax(t)), x, g, scale=2e-5)
+    fams = [l.meta["family"] for l in f.compiled(x, g).launches]
+    assert fams.count("row_combine") >= 4, fams
+
+
 def test_forced_split_of_short_ragged_rows(monkeypatch):
     """The split forced onto short rows (37 rows of 5000: five one-chunk segments per row,
     the last part-used) agrees with one workgroup per row: sums on small integers bit for
