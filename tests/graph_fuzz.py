@@ -7,9 +7,11 @@ dropped dims), softmax / LayerNorm / RMSNorm rows, linear layers with and withou
 bias, batched products, transposes and reshapes -- with one or two outputs.  Every
 op takes inputs in its domain (logs and roots of ``|v| + 1``, exponents of bounded
 values), so the programs are finite and the oracle's float32 results are
-well-conditioned.  ``attention_program``, ``layer_program`` and ``broadcast_program``
-draw attention cores, pre-norm residual layers and 3-D / 4-D broadcast-and-permute
-programs the same way.  The same seed always gives the same program.
+well-conditioned.  ``attention_program``, ``layer_program``, ``broadcast_program``,
+``block_program`` and ``reduction_program`` draw attention cores, pre-norm residual
+layers, 3-D / 4-D broadcast-and-permute programs, transformer stacks and reductions over
+few long rows the same way; ``transpose_case`` draws permutes for the tiled copy.  The
+same seed always gives the same program.
 """
 from __future__ import annotations
 
@@ -241,3 +243,53 @@ def block_program(seed: int):
     shapes = [(B, S, Dm), (Dm,), (Dm, Dm), (Dm, Dm), (Dm, Dm), (Dm, Dm), (Dm,), (F, Dm), (F,), (Dm, F), (Dm,)]
     w, wf = Dm ** -0.5, F ** -0.5
     return fn, shapes, [1.0, 1.0, w, w, w, w, 1.0, w, 0.1, wf, 0.1]
+
+
+def reduction_program(seed: int):
+    """(fn, shapes) of a random reduction over few long rows (1-16 rows of 262144-524288
+    elements, some lengths odd): a pointwise prologue on one or two inputs (the second
+    the same shape or broadcast over the rows), sum / mean / max over the last axis with
+    or without keepdim, and a per-row epilogue of zero to two ops."""
+    rng = random.Random(seed)
+    R = rng.choice([1, 2, 3, 7, 16])
+    N = rng.choice([262144, 300000, 400003, 524288])
+    xs = (R, N) if R > 1 or rng.random() < 0.5 else (N,)
+    ys = xs if rng.random() < 0.5 else (N,)
+    steps = [rng.random() for _ in range(rng.randint(0, 3))]
+    red = rng.choice(["sum", "mean", "max"])
+    keep = rng.random() < 0.5
+    epi = rng.randint(0, 2)
+    choices = [rng.randrange(1 << 30) for _ in range(32)]
+
+    def fn(x, y):
+        c = iter(choices)
+
+        def pick(seq):
+            return seq[next(c) % len(seq)]
+
+        v = x
+        for u in steps:
+            v = _unary(pick(UNARY), v) if u < 0.5 else _binary(pick(["add", "sub", "mul", "div_safe", "maximum"]), v, y)
+        r = getattr(tj, red)(v, axis=-1, keepdim=keep)
+        for _ in range(epi):
+            r = pick([lambda t: t * 0.5 + 1.0, lambda t: tj.sqrt(tj.abs(t) + 1.0), tj.tanh, lambda t: -t])(r)
+        return r
+
+    return fn, [xs, ys]
+
+
+def transpose_case(seed: int):
+    """(shape, perm) of a random 2-4 dim permute whose output's innermost dim is strided in
+    the source, with both innermost dims multiples of 8 (16-byte rows for every dtype up
+    to 4 bytes) and ragged against the 64-element tiles."""
+    rng = random.Random(seed)
+    while True:
+        nd = rng.choice([2, 3, 4])
+        shape = [rng.choice([1, 2, 3, 5]) for _ in range(nd)]
+        perm = list(range(nd))
+        rng.shuffle(perm)
+        if perm[-1] == nd - 1:
+            continue
+        for d in (perm[-1], nd - 1):
+            shape[d] = 8 * rng.choice([1, 3, 8, 9, 16, 33])
+        return tuple(shape), tuple(perm)

@@ -193,3 +193,58 @@ def test_random_transformer_stack_matches_the_oracle(seed, monkeypatch):
     fn, shapes, scales = graph_fuzz.block_program(seed)
     print(f"random transformer stack {seed} {shapes[0]}", flush=True)
     _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 3e-2)], scales)
+
+
+RED_SEEDS = range(24)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_long_reduction_splits_and_compiles(seed, tj_env):
+    """Random reductions over few long rows: in fp32 and bf16 the reduction splits its
+    rows over workgroups (a combine launch follows it) and the module compiles."""
+    fn, shapes = graph_fuzz.reduction_program(seed)
+    for dt in (DType.f32, DType.bf16):
+        p = lower(tj.trace(fn, [TensorType(s, dt) for s in shapes]), "hip")
+        src, launches = hb.generate(p)
+        assert [l.meta["family"] for l in launches][-2:] == ["row", "row_combine"], (seed, dt)
+        hb.compile_source(src, "gfx950")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", RED_SEEDS)
+def test_random_long_reduction_matches_the_oracle(seed, monkeypatch):
+    """Split reductions with random prologues, epilogues, row counts and ragged row
+    lengths, fp32 (1e-5) and bf16 (5e-2), against the oracle."""
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    fn, shapes = graph_fuzz.reduction_program(seed)
+    print(f"random long reduction {seed} {shapes}", flush=True)
+    _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])
+
+
+TRANSPOSE_SEEDS = range(32)
+
+
+def test_random_transposes_take_the_tiled_copy(tj_env):
+    """Every random permute (output innermost dim strided in the source, 16-byte rows)
+    plans as one copy kernel on the LDS-tiled path, for 2- and 4-byte elements."""
+    for seed in TRANSPOSE_SEEDS:
+        shape, perm = graph_fuzz.transpose_case(seed)
+        for dt in (DType.f32, DType.bf16):
+            p = lower(tj.trace(lambda t: tj.permute(t, *perm), [TensorType(shape, dt)]), "hip")
+            src, launches = hb.generate(p)
+            assert [l.meta.get("tiled") for l in launches] == [64], (seed, shape, perm, dt)
+            if seed < 4:
+                hb.compile_source(src, "gfx950")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", TRANSPOSE_SEEDS)
+def test_random_transposes_are_bit_exact(seed):
+    shape, perm = graph_fuzz.transpose_case(seed)
+    print(f"random transpose {seed} {shape} {perm}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(shape, generator=g) * 1000
+    for dt in (torch.float32, torch.bfloat16, torch.float16, torch.int32):
+        y = x.to(dt).cuda()
+        out = tj.jit(lambda t: tj.permute(t, *perm))(y)
+        assert torch.equal(out, y.permute(*perm).contiguous()), (seed, dt)
