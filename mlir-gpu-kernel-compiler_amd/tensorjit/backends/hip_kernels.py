@@ -383,23 +383,28 @@ def gen_copy(g: KernelGen) -> tuple[str, Launch]:
 # ---------------------------------------------------------------------------
 
 
+# Rows past 256 lanes x 16 chunks: a single-stage reduction streams through a rolled
+# loop; a row with several stages keeps every stage's values in VGPRs, so it takes up to
+# 1024 lanes (16 waves: 128 VGPRs each) holding at most ROW_MAX_FLOATS floats per lane
+# per row array.  That covers every row of up to 32768 elements at any vector width.
+ROW_MAX_FLOATS = 32
+
+
 def row_geometry(N: int, vec: int, streaming_ok: bool) -> tuple[int, int, bool]:
-    """(threads T, chunks per lane NCH, streaming).  Aims at <= 256 lanes x a few
-    16-byte chunks; rows longer than 1024 lanes x 16 chunks stream through a
-    rolled loop (single-stage reductions only)."""
+    """(threads T, chunks per lane NCH, streaming).  Up to 256 lanes x 16 chunks of
+    ``vec`` elements; then a rolled loop over 1024 lanes (single-stage reductions) or up
+    to 1024 lanes x ROW_MAX_FLOATS // vec chunks (rows with several stages)."""
     nv = -(-N // vec)
     nch = max(1, -(-nv // 256))
     t = 64 * -(-(-(-nv // nch)) // 64)
-    while t > 1024:
-        nch += 1
-        t = 64 * -(-(-(-nv // nch)) // 64)
-    if nch > 16:
-        if not streaming_ok:
-            raise NotImplementedError(f"row length {N} needs {nch} chunks per lane")
-        t = 1024
-        nch = -(-nv // t)
-        return t, nch, True
-    return t, nch, False
+    if nch <= 16:
+        return t, nch, False
+    if streaming_ok:
+        return 1024, -(-nv // 1024), True
+    nch = -(-nv // 1024)
+    if nch * vec > ROW_MAX_FLOATS:
+        raise NotImplementedError(f"row length {N} needs {nch} chunks of {vec} per lane at 1024 lanes")
+    return 64 * -(-(-(-nv // nch)) // 64), nch, False
 
 
 # Row layouts, chosen by row size in 16-byte chunks (nv), measured on MI355X against a
@@ -411,7 +416,7 @@ def row_geometry(N: int, vec: int, streaming_ok: bool) -> tuple[int, int, bool]:
 #   up to a whole wave).  Streaming copies run fastest with a single 16-byte load per lane
 #   (two or more per lane lose 6-12%): RMSNorm bf16 [65536, 4096] 167 us against 173 us
 #   with 256 lanes x 2 chunks.
-# * longer rows: row_geometry (up to 1024 lanes x 16 chunks, then a rolled loop).
+# * longer rows: row_geometry (256 lanes x up to 16 chunks, then 1024 lanes).
 WAVE_ROW_MAX_CHUNKS = 4
 WAVE_ROWS_PER_BLOCK = 4
 ONE_CHUNK_MAX_LANES = 1024

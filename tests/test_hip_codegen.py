@@ -451,3 +451,29 @@ def test_split_reductions_generate_and_compile(case, tj_env):
     if red == "mean":
         assert f"acc / {float(shapes[0][-1])!r}f" in src
     hb.compile_source(src, "gfx950")
+
+
+def test_long_rows_with_several_stages_fit_one_workgroup(tj_env):
+    """Rows with several stages up to the hip row-fusion limit (32768) get one row kernel:
+    256 lanes x up to 16 chunks, then up to 1024 lanes x 32 values per lane per row array
+    (odd lengths load one element per chunk), and the kernels compile for gfx950."""
+    from tensorjit.backends import hip_kernels as hk
+
+    assert hk.row_geometry(16384, 4, False) == (256, 16, False)
+    assert hk.row_geometry(32768, 4, False) == (1024, 8, False)
+    assert hk.row_geometry(4097, 1, False) == (832, 5, False)
+    assert hk.row_geometry(5001, 1, False) == (1024, 5, False)
+    assert hk.row_geometry(32767, 1, False) == (1024, 32, False)
+    assert hk.row_geometry(1 << 20, 4, True) == (1024, 256, True)      # a reduction streams
+    with pytest.raises(NotImplementedError):
+        hk.row_geometry(32769, 1, False)
+    for n, dt in [(5001, DType.f32), (32767, DType.f32), (32768, DType.f32), (32768, DType.bf16), (20000, DType.f16)]:
+        fn = lambda x, g: (tj.layer_norm(x, g), tj.softmax(x))  # noqa: E731
+        p = C.lower(tj.trace(fn, [TensorType((4, n), dt), TensorType((n,), dt)]), "hip")
+        assert [k.kind for k in p.kernels] == ["row", "row"], (n, dt)
+        src, launches = hb.generate(p)
+        for launch in launches:
+            vec, T, nch = launch.meta["vec"], launch.meta["threads"], launch.meta["chunks"]
+            assert T <= 1024 and T * nch * vec >= n and (T <= 256 or nch * vec <= hk.ROW_MAX_FLOATS)
+        if n in (5001, 32768):
+            hb.compile_source(src, "gfx950")

@@ -236,6 +236,12 @@ SPLIT_CASES = {
     "max": (lambda x: tj.max(x, axis=-1, keepdim=True) * 2.0, [(4, 262144)], torch.float32),
     # an odd row length: scalar lanes (one element per lane)
     "odd": (lambda x: tj.sum(tj.abs(x), axis=-1), [(2, 300001)], torch.float32),
+    # an epilogue reading a per-row input in the combine launch
+    "epi_input": (lambda x, b: tj.sum(x, axis=-1) * b, [(3, 300000), (3,)], torch.float32),
+    # two outputs of the epilogue (keepdim), both stored by the combine launch
+    "two_outputs": (lambda x, b: (tj.mean(x * x, axis=-1, keepdim=True) + tj.abs(b),
+                                  tj.sqrt(tj.mean(x * x, axis=-1, keepdim=True) + tj.abs(b))), [(3, 300000), (3, 1)],
+                    torch.float32),
     # a prologue value stored as a second output beside the row sum
     "vec_out": (lambda x: (tj.exp(tj.tanh(x)), tj.sum(tj.exp(tj.tanh(x)), axis=-1)), [(2, 262144)], torch.float32),
 }
@@ -274,7 +280,7 @@ def test_split_row_reductions_vs_oracle(case):
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 def test_norms_over_rows_past_the_row_fusion_limit(dt):
     """LayerNorm / RMSNorm / softmax over 3 rows of 300000: the plan gives their reductions
-    and pointwise steps kernels of their own (rows past 8192 are not row-fused), and
+    and pointwise steps kernels of their own (rows past 32768 are not row-fused), and
     each reduction splits its rows over workgroups."""
     torch.manual_seed(0)
     x = (torch.randn(3, 300000, device=DEV) * 2).to(dt)
@@ -331,6 +337,12 @@ def test_softmax_layernorm_rmsnorm(shape):
     (257, 4096, torch.bfloat16),     # 8 KiB rows: 512 lanes x 1 chunk
     (64, 4096, torch.float32),       # 16 KiB rows: 1024 lanes x 1 chunk
     (16, 12288, torch.float32),      # longer rows: several chunks per lane
+    (37, 4097, torch.float32),       # odd length: scalar lanes, 832 lanes x 5 elements
+    (8, 16384, torch.float32),       # 256 lanes x 16 chunks
+    (6, 32767, torch.float32),       # 1024 scalar lanes x 32 elements, the last lane part-used
+    (3, 32768, torch.float32),       # 1024 lanes x 8 chunks
+    (4, 32768, torch.bfloat16),      # 256 lanes x 16 chunks of 8
+    (5, 20000, torch.float16),       # 256 lanes x 10 chunks, a ragged last chunk
 ])
 def test_row_layouts_vs_oracle(rows, n, dt):
     """Every row layout (wave per row with a ragged last workgroup, one chunk per lane with idle

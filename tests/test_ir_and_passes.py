@@ -135,7 +135,17 @@ def test_row_fusion_respects_dependencies_through_matmul():
 
 
 def test_row_fusion_limit_keeps_long_rows_apart():
-    kinds, _ = _plan(lambda x: tj.softmax(x), (4, 10000))
+    """Row fusion keeps rows longer than its limit apart: with the reference's GPU limit
+    (8192) a softmax over 10000 stays four kernels; the hip backend's limit is 32768, so
+    there it is one row kernel, and a softmax over 40000 is four again."""
+    from tensorjit.passes import row_fuse
+
+    g = optimize(_graph(lambda x: tj.softmax(x), (4, 10000)))
+    assert [k.kind for k in row_fuse(fuse(g), max_n=8192).kernels] == ["reduce", "elementwise", "reduce", "elementwise"]
+    assert C.ROW_FUSION_MAX_N["hip"] == 32768
+    assert [k for k, _ in _plan(lambda x: tj.softmax(x), (4, 10000))[0]] == ["row"]
+    assert [k for k, _ in _plan(lambda x: tj.softmax(x), (4, 32768))[0]] == ["row"]
+    kinds, _ = _plan(lambda x: tj.softmax(x), (4, 40000))
     assert kinds[0][0] == "reduce" and len(kinds) == 4
 
 
