@@ -8,10 +8,11 @@ bias, batched products, transposes and reshapes -- with one or two outputs.  Eve
 op takes inputs in its domain (logs and roots of ``|v| + 1``, exponents of bounded
 values), so the programs are finite and the oracle's float32 results are
 well-conditioned.  ``attention_program``, ``layer_program``, ``broadcast_program``,
-``block_program`` and ``reduction_program`` draw attention cores, pre-norm residual
-layers, 3-D / 4-D broadcast-and-permute programs, transformer stacks and reductions over
-few long rows the same way; ``transpose_case`` draws permutes for the tiled copy.  The
-same seed always gives the same program.
+``block_program``, ``reduction_program`` and ``wide_row_program`` draw attention cores,
+pre-norm residual layers, 3-D / 4-D broadcast-and-permute programs, transformer stacks,
+reductions over few long rows and row-op chains over wide rows the same way;
+``transpose_case`` draws permutes for the tiled copy.  The same seed always gives the same
+program.
 """
 from __future__ import annotations
 
@@ -293,3 +294,40 @@ def transpose_case(seed: int):
         for d in (perm[-1], nd - 1):
             shape[d] = 8 * rng.choice([1, 3, 8, 9, 16, 33])
         return tuple(shape), tuple(perm)
+
+
+def wide_row_program(seed: int):
+    """(fn, shapes) of a random chain of row ops over wide rows (4097-32768 elements, odd
+    lengths among them; 1-64 rows): softmax / LayerNorm / RMSNorm (with a gain or not),
+    pointwise ops with a second input of the same shape or broadcast over the rows, and
+    row maxima or means broadcast back, which row fusion keeps in one row kernel."""
+    rng = random.Random(seed)
+    R = rng.choice([1, 3, 16, 64])
+    N = rng.choice([4097, 8193, 12288, 16383, 24576, 32768])
+    ys = (R, N) if rng.random() < 0.5 else (N,)
+    steps = [rng.random() for _ in range(rng.randint(2, 5))]
+    choices = [rng.randrange(1 << 30) for _ in range(32)]
+
+    def fn(x, y, g):
+        c = iter(choices)
+
+        def pick(seq):
+            return seq[next(c) % len(seq)]
+
+        v = x
+        for u in steps:
+            if u < 0.35:
+                op = pick(["softmax", "layer_norm", "rms_norm", "layer_norm_g", "rms_norm_g"])
+                v = {"softmax": tj.softmax, "layer_norm": tj.layer_norm, "rms_norm": tj.rms_norm,
+                     "layer_norm_g": lambda t: tj.layer_norm(t, g), "rms_norm_g": lambda t: tj.rms_norm(t, g)}[op](v)
+            elif u < 0.6:
+                v = _unary(pick(["tanh", "gelu", "silu", "exp_tanh", "sigmoid"]), v)
+            elif u < 0.8:
+                v = _binary(pick(["add", "sub", "mul"]), v, y)
+            elif u < 0.9:
+                v = v - tj.max(v, axis=-1, keepdim=True)
+            else:
+                v = v * tj.rsqrt(tj.mean(v * v, axis=-1, keepdim=True) + 1.0)
+        return v
+
+    return fn, [(R, N), ys, (N,)]

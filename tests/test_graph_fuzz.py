@@ -248,3 +248,30 @@ def test_random_transposes_are_bit_exact(seed):
         y = x.to(dt).cuda()
         out = tj.jit(lambda t: tj.permute(t, *perm))(y)
         assert torch.equal(out, y.permute(*perm).contiguous()), (seed, dt)
+
+
+WIDE_SEEDS = range(24)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_wide_row_program_is_one_row_kernel(seed, tj_env):
+    """Random chains of row ops over rows of 4097-32768 elements plan as one row kernel
+    (the hip row-fusion limit is 32768) and compile."""
+    fn, shapes = graph_fuzz.wide_row_program(seed)
+    for dt in (DType.f32, DType.bf16):
+        p = lower(tj.trace(fn, [TensorType(s, dt) for s in shapes]), "hip")
+        q = hb.sink_epilogue_into_rows(hb.fold_elementwise_into_gemm(hb.fuse_attention(p)))
+        assert [k.kind for k in q.kernels] == ["row"], (seed, dt)
+        src, _ = hb.generate(q)
+        hb.compile_source(src, "gfx950")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", WIDE_SEEDS)
+def test_random_wide_row_program_matches_the_oracle(seed, monkeypatch):
+    """Wide-row chains (1024-lane and 256-lane layouts, odd lengths on scalar lanes), fp32
+    within 1e-5 and bf16 within 5e-2, against the oracle."""
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    fn, shapes = graph_fuzz.wide_row_program(seed)
+    print(f"random wide-row program {seed} {shapes}", flush=True)
+    _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])
