@@ -34,7 +34,7 @@ from ..runtime.dtypes import TORCH_DTYPE
 from ..runtime.pool import BufferPool
 from .hip_attention import fuse_attention, gen_attention
 from .hip_gemm import compute_dtype, config_ok, gen_matmul, matmul_dims
-from .hip_kernels import KernelGen, Launch, gen_copy, gen_elementwise, gen_row
+from .hip_kernels import KernelGen, Launch, gen_colreduce, gen_copy, gen_elementwise, gen_row
 from .hip_prelude import PRELUDE
 
 log = logging.getLogger("tensorjit")
@@ -105,6 +105,8 @@ def generate_kernel(k: Kernel, idx: int, cfg: MatmulConfig | None = None) -> tup
         return gen_matmul(g, cfg or analytic_config(k))
     if k.kind == "attention":
         return gen_attention(k, idx)
+    if k.kind == "colreduce":
+        return gen_colreduce(g)
     raise NotImplementedError(k.kind)
 
 
@@ -269,6 +271,111 @@ def fold_elementwise_into_gemm(program: Program) -> Program:
     return Program(program.graph, kernels, program.aliases) if changed else program
 
 
+COL_MIN_BYTES = 512       # a column block's row (64 lanes) must hold at least this many bytes
+
+
+def fold_transpose_into_reduce(program: Program) -> Program:
+    """Turn a transpose kernel whose every reader is a stand-alone reduction of its last
+    axis into ``colreduce`` kernels that reduce the source's axis in place.
+
+    The reference plan reduces a non-last axis by copying it last (a transpose kernel)
+    and reducing rows: the tensor crosses HBM three times (read, write, read), four with
+    two reductions of it.  Each column reduction reads it once.  It applies when the
+    transpose keeps every other axis in order (the source is then [A, Rd, B] with the
+    reduced axis Rd in the middle, and the outputs' order is [A, B]), each reduction's
+    prologue is elementwise on the transposed value alone, nothing but the reductions'
+    values and epilogues escape, and a row of B holds at least COL_MIN_BYTES bytes.  With
+    one reduction, an elementwise kernel whose only output is the transposed source, read
+    by nothing else, becomes its prologue too.  ``TENSORJIT_HIP_COLREDUCE=0`` keeps the
+    reference plan."""
+    if os.environ.get("TENSORJIT_HIP_COLREDUCE", "1") == "0":
+        return program
+    kernels = list(program.kernels)
+    outs = {id(program.resolve(o)) for o in program.graph.outputs}
+    changed = False
+    c = 0
+    while c < len(kernels):
+        folded = _col_fold(kernels, c, outs)
+        if folded is None:
+            c += 1
+            continue
+        new, drop = folded
+        for i, k in new.items():
+            kernels[i] = k
+        for d in sorted(drop, reverse=True):
+            del kernels[d]
+        changed = True
+        c = 0           # the drops shift the indices: scan again from the start
+    return Program(program.graph, kernels, program.aliases) if changed else program
+
+
+def _col_fold(kernels: list[Kernel], c: int, outs: set) -> tuple[dict[int, Kernel], list[int]] | None:
+    """Column reductions replacing transpose kernel ``c`` and its readers, or None."""
+    ck = kernels[c]
+    if ck.kind != "copy" or len(ck.nodes) != 1 or ck.nodes[0].op != "transpose" or ck.outputs != ck.nodes:
+        return None
+    t = ck.nodes[0]
+    if id(t) in outs:
+        return None
+    perm = tuple(t.attrs["perm"])
+    a = perm[-1]
+    if a == len(perm) - 1 or list(perm[:-1]) != sorted(perm[:-1]):
+        return None
+    X = t.inputs[0]
+    Sx = tuple(X.shape)
+    A, Rd, B = math.prod(Sx[:a]), Sx[a], math.prod(Sx[a + 1:])
+    if B * X.dtype.itemsize < COL_MIN_BYTES:
+        return None
+    owner = {id(n): i for i, k in enumerate(kernels) for n in k.nodes}
+    readers = sorted({owner.get(id(u), -1) for u in t.users})
+    if not readers or any(r < 0 or not _col_reduce_ok(kernels[r], t) for r in readers):
+        return None
+    producer = {id(o): j for j, k in enumerate(kernels) for o in k.outputs}
+    drop = [c]
+    xnodes: list[Node] = []
+    xins = [X]
+    e = producer.get(id(X))
+    if len(readers) == 1 and e is not None and kernels[e].kind == "elementwise":
+        ek = kernels[e]
+        if (ek.outputs == [X] and id(X) not in outs and all(u is t for u in X.users)
+                and all(tuple(n.shape) == Sx and n.kind == OpKind.ELEMENTWISE for n in ek.nodes)):
+            xnodes, xins = list(ek.nodes), list(ek.inputs)
+            drop.append(e)
+    new = {}
+    for r in readers:
+        rk = kernels[r]
+        ins = list(xins)
+        for n in rk.inputs:
+            if n is not t and all(n is not x for x in ins):
+                ins.append(n)
+        k = Kernel("colreduce", nodes=xnodes + list(rk.nodes), anchor=rk.anchor, inputs=ins, outputs=list(rk.outputs))
+        k.src, k.tnode, k.col, k.xnodes = X, t, (A, Rd, B), xnodes  # type: ignore[attr-defined]
+        new[r] = k
+    return new, drop
+
+
+def _col_reduce_ok(rk: Kernel, t: Node) -> bool:
+    """``rk`` is a stand-alone sum / mean / max of ``t``'s last axis whose prologue reads
+    only ``t`` (and scalar constants), whose epilogue reads only the reduction, itself and
+    outside inputs, and which lets only per-output values escape."""
+    if rk.kind != "reduce" or rk.anchor.op not in ("sum", "mean", "max"):
+        return False
+    red = rk.anchor
+    pos = rk.nodes.index(red)
+    prologue, epilogue = rk.nodes[:pos], rk.nodes[pos + 1:]
+    inside = {id(n) for n in rk.nodes}
+    vec_in = [n for n in rk.inputs if any(n in m.inputs for m in prologue + [red])]
+    if len(vec_in) != 1 or vec_in[0] is not t:
+        return False
+    for n in prologue:
+        if any(id(x) not in inside and x is not t and not (x.op == "const" and x.shape == ()) for x in n.inputs):
+            return False
+    pro = {id(n) for n in prologue}
+    if any(id(x) in pro or x is t for n in epilogue for x in n.inputs):
+        return False
+    return not any(id(o) in pro for o in rk.outputs)
+
+
 def sink_epilogue_into_rows(program: Program) -> Program:
     """Move a GEMM epilogue value whose only readers are one stage of a later row kernel
     into that stage, when everything it reads the row kernel can read too.
@@ -338,8 +445,8 @@ class HipProgram:
         reject_zero_size(list(program.graph.inputs) + [n for k in program.kernels for n in k.nodes])
         # backend-level rewrites of the planned program: attention chains -> one kernel,
         # elementwise kernels behind a GEMM -> its epilogue, epilogue values only a row
-        # kernel reads -> that row kernel
-        program = sink_epilogue_into_rows(fold_elementwise_into_gemm(fuse_attention(program)))
+        # kernel reads -> that row kernel, transpose -> reduce -> one column reduction
+        program = fold_transpose_into_reduce(sink_epilogue_into_rows(fold_elementwise_into_gemm(fuse_attention(program))))
         self.program = program
         self.device = torch.device(device)
         if self.device.type != "cuda":

@@ -41,7 +41,7 @@ from dataclasses import dataclass, field
 from ..ir import DType, Node
 from ..passes import Kernel
 from ..runtime.autotune import CU_COUNT
-from .common import access_strides, emit_expr, inner_stride, merged_dims, offset_expr
+from .common import access_strides, broadcast_strides, emit_expr, inner_stride, merged_dims, offset_expr
 from .hip_prelude import CTYPE, vec_width
 
 THREADS = 256
@@ -767,3 +767,156 @@ def _block_reduce_lines(acc: str, is_max: bool, nwaves: int, slot: int) -> list[
             comb = f"fmaxf({acc}, tj_red[{slot}][{w}])" if is_max else f"{acc} + tj_red[{slot}][{w}]"
             out.append(f"  {acc} = {comb};")
     return out
+
+
+# ---------------------------------------------------------------------------
+# column reductions (hip-backend rewrite of transpose -> reduce)
+# ---------------------------------------------------------------------------
+
+# A reduction over a non-last axis: the plan transposes the reduced axis last (a copy
+# kernel) and reduces rows.  The ``colreduce`` kernel reads the source in place instead,
+# viewed as [A, Rd, B] with the reduced axis Rd in the middle: the 64 lanes of a wave own
+# 64 consecutive 16-byte vectors along B, so each row of Rd is a coalesced 1 KiB load per
+# wave; the workgroup's 4 waves take interleaved rows of its slice of Rd and combine their
+# partials through LDS.  Rd is split over S workgroups to reach about 4 x CU_COUNT
+# workgroups (each walking at least COL_MIN_ROWS rows, at most COL_MAX_SPLITS splits);
+# with S > 1 the partials go to the workspace as [S][A*B] and a combine launch adds them
+# in a fixed order and runs the reduction's finish and epilogue: one lane per output, the
+# S partials of 64 outputs spread over up to 16 waves and combined through LDS.
+COL_WAVES = 4
+COL_MIN_ROWS = 16
+COL_MAX_SPLITS = 512
+
+
+def col_layout(A: int, Rd: int, B: int, vec: int) -> tuple[int, int, int]:
+    """(column blocks per A-slice nb, rows per workgroup RS, splits S) of a column reduction."""
+    L = -(-B // vec)
+    nb = -(-L // 64)
+    base = A * nb
+    forced = os.environ.get("TENSORJIT_HIP_COL_SPLITS")
+    if forced and forced.isdigit():
+        S = max(1, min(int(forced), Rd))
+    else:
+        S = max(1, min(-(-4 * CU_COUNT // base), Rd // COL_MIN_ROWS, COL_MAX_SPLITS))
+    RS = -(-Rd // S)
+    return nb, RS, -(-Rd // RS)
+
+
+def gen_colreduce(g: KernelGen) -> tuple[str, Launch | list[Launch]]:
+    k = g.k
+    X, t, red = k.src, k.tnode, k.anchor          # type: ignore[attr-defined]
+    A, Rd, B = k.col                              # type: ignore[attr-defined]
+    xnodes = k.xnodes                             # type: ignore[attr-defined]
+    pos = k.nodes.index(red)
+    tnodes = k.nodes[len(xnodes):pos]
+    epilogue = k.nodes[pos + 1:]
+    Sx = tuple(X.shape)
+    dt = _kernel_dtype(k)
+    vec = _vec_for(Sx[-1], A * Rd * B, dt)
+    nb, RS, S = col_layout(A, Rd, B, vec)
+    L = -(-B // vec)
+    AB = A * B
+    idx_t = _index_type(A * Rd * B)
+    is_max = red.op == "max"
+    init = "(-__builtin_inff())" if is_max else "0.0f"
+    escaping = {id(o): j for j, o in enumerate(k.outputs)}
+    nm = lambda n: g.names[id(n)]  # noqa: E731
+
+    # inputs read per element of X: the folded elementwise kernel's inputs, or X itself
+    xin = [n for n in k.inputs if n is X or any(n in m.inputs for m in xnodes)]
+    xstr = {id(n): broadcast_strides(n.shape, Sx) for n in xin}
+    nt = _nt_loads(sum(math.prod(n.shape) * n.dtype.itemsize for n in xin if _streamed(Sx, xstr[id(n)])))
+
+    def fold(acc: str, v: str) -> str:
+        return f"{acc} = fmaxf({acc}, {v});" if is_max else f"{acc} += {v};"
+
+    def finish_lines(r: str, acc: str, ind: str) -> list[str]:
+        """The reduction's value at output ``r`` from ``acc``, its epilogue, the stores."""
+        out, local = [], {}
+        val = f"{acc} / {float(Rd)!r}f" if red.op == "mean" else acc
+        out.append(f"{ind}const float {nm(red)}_v = {val};")
+        local[id(red)] = f"{nm(red)}_v"
+        loaded = set()
+        for n in [red] + epilogue:
+            if n is not red:
+                for i in n.inputs:
+                    if id(i) in local or (i.op == "const" and i.shape == ()) or id(i) in loaded:
+                        continue
+                    off = offset_expr(r, tuple(red.shape), access_strides(i, n, tuple(red.shape)))
+                    out.append(f"{ind}const float {nm(i)}_s = tj_ld({nm(i)}_p[{off}]);")
+                    local[id(i)] = f"{nm(i)}_s"
+                    loaded.add(id(i))
+                out.append(f"{ind}const float {nm(n)}_v = {emit_expr(n, local)};")
+                local[id(n)] = f"{nm(n)}_v"
+            if id(n) in escaping:
+                out.append(f"{ind}tj_st(out{escaping[id(n)]}_p + {r}, {nm(n)}_v);")
+        return out
+
+    ws_param = ", float* __restrict__ ws_p" if S > 1 else ""
+    C = [f'extern "C" __global__ __launch_bounds__({64 * COL_WAVES}) void {g.fname}({g.params()}{ws_param}) {{',
+         f"  __shared__ float tj_col[{COL_WAVES}][{64 * vec}];",
+         "  const unsigned int blk = blockIdx.x, lane = threadIdx.x & 63u, w = threadIdx.x >> 6;",
+         f"  const unsigned int bb = blk % {nb}u, ai = (blk / {nb}u) % {A}u, s = blk / {nb * A}u;",
+         "  const unsigned int lv = bb * 64u + lane;",
+         f"  const unsigned int j0 = s * {RS}u, j1 = j0 + {RS}u < {Rd}u ? j0 + {RS}u : {Rd}u;",
+         f"  float acc[{vec}];",
+         "#pragma unroll",
+         f"  for (int q = 0; q < {vec}; ++q) acc[q] = {init};",
+         f"  if (lv < {L}u) {{",
+         "#pragma unroll 4",
+         f"    for (unsigned int j = j0 + w; j < j1; j += {COL_WAVES}u) {{",
+         f"      const {idx_t} e = (({idx_t})ai * {Rd}u + j) * {B}u + lv * {vec}u;"]
+    for n in xin:
+        C.append(f"      float {nm(n)}_l[{vec}];")
+        C += ["      " + s for s in _load_lines(nm(n), CTYPE[n.dtype], offset_expr("e", Sx, xstr[id(n)]),
+                                                inner_stride(Sx, xstr[id(n)]), vec, f"{nm(n)}_l",
+                                                nt and _streamed(Sx, xstr[id(n)]))]
+    C += ["#pragma unroll", f"      for (int q = 0; q < {vec}; ++q) {{"]
+    local = {id(n): f"{nm(n)}_l[q]" for n in xin}
+    for n in xnodes + tnodes:
+        C.append(f"        const float {nm(n)}_e = {emit_expr(n, local)};")
+        local[id(n)] = f"{nm(n)}_e"
+        if n is X:
+            local[id(t)] = local[id(X)]
+    if id(t) not in local:
+        local[id(t)] = local[id(X)]
+    C.append("        " + fold("acc[q]", local[id(red.inputs[0])]))
+    C += ["      }", "    }", "  }"]
+    # the 4 waves' partials through LDS, combined by wave 0 in a fixed order
+    C += ["#pragma unroll", f"  for (int q = 0; q < {vec}; ++q) tj_col[w][lane * {vec}u + q] = acc[q];",
+          "  __syncthreads();", f"  if (w != 0u || lv >= {L}u) return;",
+          "#pragma unroll", f"  for (int q = 0; q < {vec}; ++q) {{", "    float a = tj_col[0][lane * %du + q];" % vec]
+    for w in range(1, COL_WAVES):
+        C.append("    " + fold("a", f"tj_col[{w}][lane * {vec}u + q]"))
+    C.append(f"    const {idx_t} r = ({idx_t})ai * {B}u + lv * {vec}u + q;")
+    if S == 1:
+        C += finish_lines("r", "a", "    ")
+    else:
+        C.append(f"    ws_p[({idx_t})s * {AB}u + r] = a;")
+    C += ["  }", "}"]
+    meta = {"family": "colreduce", "vec": vec, "A": A, "Rd": Rd, "B": B, "splits": S, "rows_per_wg": RS}
+    main = Launch(g.fname, (nb * A * S, 1, 1), (64 * COL_WAVES, 1, 1), 0, meta)
+    if S == 1:
+        return "\n".join(C), main
+    meta.update({"workspace": S * AB * 4, "ws_arg": True})
+    CW = min(16, S)
+    D = [f'extern "C" __global__ __launch_bounds__({64 * CW}) void {g.fname}_combine({g.params()}, '
+         "const float* __restrict__ ws_p) {",
+         f"  __shared__ float tj_cmb[{CW}][64];",
+         "  const unsigned int lane = threadIdx.x & 63u, w = threadIdx.x >> 6;",
+         f"  const {idx_t} r = ({idx_t})blockIdx.x * 64u + lane;",
+         f"  float a = {init};",
+         f"  if (r < {AB}u) {{",
+         "#pragma unroll 4",
+         f"    for (unsigned int s = w; s < {S}u; s += {CW}u) " + fold("a", f"ws_p[({idx_t})s * {AB}u + r]"),
+         "  }",
+         "  tj_cmb[w][lane] = a;",
+         "  __syncthreads();",
+         f"  if (w != 0u || r >= {AB}u) return;",
+         "  a = tj_cmb[0][lane];"]
+    D += ["  " + fold("a", f"tj_cmb[{w}][lane]") for w in range(1, CW)]
+    D += finish_lines("r", "a", "  ")
+    D.append("}")
+    comb = Launch(g.fname + "_combine", (-(-AB // 64), 1, 1), (64 * CW, 1, 1), 0,
+                  {"family": "colreduce_combine", "splits": S, "ws_arg": True, "outputs": AB})
+    return "\n".join(C) + "\n\n" + "\n".join(D), [main, comb]

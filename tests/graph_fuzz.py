@@ -8,9 +8,10 @@ bias, batched products, transposes and reshapes -- with one or two outputs.  Eve
 op takes inputs in its domain (logs and roots of ``|v| + 1``, exponents of bounded
 values), so the programs are finite and the oracle's float32 results are
 well-conditioned.  ``attention_program``, ``layer_program``, ``broadcast_program``,
-``block_program``, ``reduction_program`` and ``wide_row_program`` draw attention cores,
-pre-norm residual layers, 3-D / 4-D broadcast-and-permute programs, transformer stacks,
-reductions over few long rows and row-op chains over wide rows the same way;
+``block_program``, ``reduction_program``, ``wide_row_program`` and ``column_program``
+draw attention cores, pre-norm residual layers, 3-D / 4-D broadcast-and-permute programs,
+transformer stacks, reductions over few long rows, row-op chains over wide rows and
+reductions over a non-last axis the same way;
 ``transpose_case`` draws permutes for the tiled copy.  The same seed always gives the same
 program.
 """
@@ -331,3 +332,45 @@ def wide_row_program(seed: int):
         return v
 
     return fn, [(R, N), ys, (N,)]
+
+
+def column_program(seed: int):
+    """(fn, shapes) of a random reduction over a non-last axis of a 2-4 dim tensor whose
+    inner dims span at least 256 elements: an elementwise prologue on one or two inputs
+    (the second full-shape or broadcast), sum / mean / max with or without keepdim, at
+    times a second reduction of the same axis, and an epilogue that may read an input of
+    the output's shape."""
+    rng = random.Random(seed)
+    nd = rng.choice([2, 3, 4])
+    axis = rng.randrange(nd - 1)
+    shape = [rng.choice([1, 2, 3, 5]) for _ in range(nd)]
+    shape[axis] = rng.choice([7, 64, 300, 1000, 4096])
+    shape[-1] = rng.choice([256, 260, 301, 512, 1024, 1032])
+    full = tuple(shape)
+    ys = full if rng.random() < 0.5 else full[-1:]
+    out = tuple(d for i, d in enumerate(full) if i != axis)
+    steps = [rng.random() for _ in range(rng.randint(0, 2))]
+    red = rng.choice(["sum", "mean", "max"])
+    keep = rng.random() < 0.4
+    second = rng.random() < 0.3
+    epi = rng.random() < 0.5 and not keep
+    choices = [rng.randrange(1 << 30) for _ in range(16)]
+
+    def fn(x, y, g):
+        c = iter(choices)
+
+        def pick(seq):
+            return seq[next(c) % len(seq)]
+
+        v = x
+        for u in steps:
+            v = _unary(pick(["tanh", "abs", "exp_tanh", "sigmoid"]), v) if u < 0.5 else \
+                _binary(pick(["add", "mul", "sub"]), v, y)
+        r = getattr(tj, red)(v, axis=axis, keepdim=keep)
+        if epi:
+            r = tj.tanh(r) * g + 0.5
+        if second:
+            return r, tj.max(v, axis=axis, keepdim=keep) if red != "max" else tj.mean(v, axis=axis, keepdim=keep)
+        return r
+
+    return fn, [full, ys, out]

@@ -275,3 +275,31 @@ def test_random_wide_row_program_matches_the_oracle(seed, monkeypatch):
     fn, shapes = graph_fuzz.wide_row_program(seed)
     print(f"random wide-row program {seed} {shapes}", flush=True)
     _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])
+
+
+COL_SEEDS = range(24)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_column_reduction_folds_and_compiles(seed, tj_env):
+    """Random reductions over a non-last axis: every reduction of the transposed value
+    becomes a column reduction and the module compiles, in fp32 and bf16."""
+    fn, shapes = graph_fuzz.column_program(seed)
+    for dt in (DType.f32, DType.bf16):
+        p = lower(tj.trace(fn, [TensorType(s, dt) for s in shapes]), "hip")
+        q = hb.fold_transpose_into_reduce(hb.sink_epilogue_into_rows(hb.fold_elementwise_into_gemm(hb.fuse_attention(p))))
+        kinds = [k.kind for k in q.kernels]
+        assert "copy" not in kinds and kinds.count("colreduce") == [k.kind for k in p.kernels].count("reduce"), (seed, dt)
+        src, _ = hb.generate(q)
+        hb.compile_source(src, "gfx950")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", COL_SEEDS)
+def test_random_column_reduction_matches_the_oracle(seed, monkeypatch):
+    """Column reductions with random prologues, axes, keepdim, shared transposes and
+    epilogues, fp32 (1e-5) and bf16 (5e-2), against the oracle."""
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    fn, shapes = graph_fuzz.column_program(seed)
+    print(f"random column reduction {seed} {shapes}", flush=True)
+    _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])

@@ -477,3 +477,62 @@ def test_long_rows_with_several_stages_fit_one_workgroup(tj_env):
             assert T <= 1024 and T * nch * vec >= n and (T <= 256 or nch * vec <= hk.ROW_MAX_FLOATS)
         if n in (5001, 32768):
             hb.compile_source(src, "gfx950")
+
+
+def test_transpose_then_reduce_folds_into_a_column_reduction(tj_env, monkeypatch):
+    """A transpose whose only reader is a reduction of its last axis becomes one column
+    reduction (with a folded elementwise prologue and the reduction's epilogue), unless the
+    transpose reorders other axes, has another reader, or a row of B is under 512 bytes.
+    Its block, column and row-slice decode (replayed on the CPU) visits every element of
+    every (A, Rd, B) source once, and every partial lands in its own workspace slot."""
+    import numpy as np
+    from tensorjit.backends import hip_kernels as hk
+
+    def plan(fn, shapes, dt=DType.f32):
+        p = C.lower(tj.trace(fn, [TensorType(s, dt) for s in shapes]), "hip")
+        return hb.fold_transpose_into_reduce(p)
+
+    q = plan(lambda x: tj.max(x * 2.0 + 1.0, axis=0, keepdim=True), [(4096, 4096)])
+    assert [k.kind for k in q.kernels] == ["colreduce"] and q.kernels[0].col == (1, 4096, 4096)
+    q = plan(lambda x, g: tj.tanh(tj.mean(x, axis=1) * 0.5) + g, [(8, 4096, 1024), (8, 1024)], DType.bf16)
+    assert [k.kind for k in q.kernels] == ["colreduce"] and q.kernels[0].col == (8, 4096, 1024)
+    src, launches = hb.generate(q)
+    assert [l.meta["family"] for l in launches] == ["colreduce", "colreduce_combine"]
+    hb.compile_source(src, "gfx950")
+    q = plan(lambda x: tj.sum(x, axis=1), [(2048, 8, 256)])
+    src, (launch,) = hb.generate(q)                      # one slice of Rd: no combine launch
+    assert launch.meta["splits"] == 1
+    hb.compile_source(src, "gfx950")
+    # not folded: a transpose that reorders the kept axes, a second reader, narrow rows, row kernels
+    assert [k.kind for k in plan(lambda x: tj.sum(tj.permute(x, 2, 0, 1), axis=-1), [(3, 64, 256)]).kernels] == \
+        ["copy", "reduce"]
+    assert "colreduce" not in [k.kind for k in plan(
+        lambda x: (tj.sum(tj.transpose(x, 0, 1), axis=-1), tj.transpose(x, 0, 1)), [(64, 256)]).kernels]
+    assert "colreduce" not in [k.kind for k in plan(lambda x: tj.sum(x, axis=1), [(4, 300, 96)]).kernels]
+    assert "colreduce" not in [k.kind for k in plan(lambda x, g: x - tj.mean(x, axis=0) * g,
+                                                     [(512, 512), (512,)]).kernels]
+    monkeypatch.setenv("TENSORJIT_HIP_COLREDUCE", "0")
+    assert [k.kind for k in plan(lambda x: tj.sum(x, axis=0), [(4096, 4096)]).kernels] == ["copy", "reduce"]
+
+    for A, Rd, B, vec in [(1, 600, 1024, 4), (8, 1000, 1024, 8), (5, 37, 168, 4), (3, 100, 200, 1), (512, 8, 256, 4)]:
+        nb, RS, S = hk.col_layout(A, Rd, B, vec)
+        L = -(-B // vec)
+        seen = np.zeros(A * Rd * B, dtype=np.int64)
+        slots = np.zeros(S * A * B, dtype=np.int64)
+        for blk in range(nb * A * S):
+            bb, ai, s = blk % nb, (blk // nb) % A, blk // (nb * A)
+            j0, j1 = s * RS, min(s * RS + RS, Rd)
+            assert j0 < j1
+            for lane in range(64):
+                lv = bb * 64 + lane
+                if lv >= L:
+                    continue
+                for w in range(hk.COL_WAVES):
+                    for j in range(j0 + w, j1, hk.COL_WAVES):
+                        e = (ai * Rd + j) * B + lv * vec
+                        seen[e:e + vec] += 1
+                r = ai * B + lv * vec
+                slots[s * A * B + r:s * A * B + r + vec] += 1
+        assert (seen == 1).all() and (slots == 1).all(), (A, Rd, B, vec)
+        cw = min(16, S)          # the combine launch's waves split each output's S partials
+        assert sorted(s for w in range(cw) for s in range(w, S, cw)) == list(range(S))

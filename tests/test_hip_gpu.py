@@ -311,6 +311,68 @@ def test_forced_split_of_short_ragged_rows(monkeypatch):
     assert torch.equal(split[0].double(), x.double().sum(-1))
 
 
+COL_CASES = {
+    # sum over the leading axis: 64 slices of 64 rows, a combine launch
+    "sum_axis0": (lambda x: tj.sum(x, axis=0), [(4096, 4096)], torch.float32),
+    # mean-pooling over a sequence in bf16, an epilogue reading a per-output input
+    "mean_pool": (lambda x, g: tj.tanh(tj.mean(x, axis=1) * 0.5) + g, [(8, 1024, 1024), (8, 1024)], torch.bfloat16),
+    # an elementwise prologue folded in, max with keepdim
+    "max_prologue": (lambda x: tj.max(x * 2.0 + 1.0, axis=0, keepdim=True), [(2048, 2048)], torch.float32),
+    # one slice of the reduced axis: no combine launch
+    "one_slice": (lambda x: tj.sum(x, axis=1), [(2048, 8, 256)], torch.float32),
+    # a middle axis of a 4-D tensor, ragged against the 64-lane column blocks
+    "middle_4d": (lambda x: tj.sum(x, axis=1), [(5, 37, 7, 24)], torch.float32),
+    # odd inner dim: one element per lane
+    "odd_inner": (lambda x: tj.mean(x, axis=0), [(999, 301)], torch.float32),
+    "fp16": (lambda x: tj.sum(x * x, axis=0), [(3000, 520)], torch.float16),
+}
+
+
+@pytest.mark.parametrize("case", sorted(COL_CASES))
+def test_column_reductions_vs_oracle(case):
+    """Reductions over a non-last axis as one column reduction (the transpose kernel
+    folded away): against the oracle, sums of small integers bit for bit against the
+    exact sum, and the max bit for bit against the reference plan's kernels."""
+    fn, shapes, dt = COL_CASES[case]
+    torch.manual_seed(0)
+    print(f"column reduction {case} {shapes} {dt}", flush=True)
+    args = [torch.randn(s, device=DEV).to(dt) for s in shapes]
+    f = tj.jit(fn)
+    assert f.compiled(*args).launches[0].meta["family"] == "colreduce"
+    n = shapes[0][1] if case in ("mean_pool", "one_slice", "middle_4d") else shapes[0][0]
+    out = f(*args)
+    ref = oracle.run(fn, *[a.float().cpu() for a in args])[0]
+    assert out.shape == ref.shape
+    if dt == torch.float32:
+        close_f32(out, ref, scale=1e-5 * math.sqrt(n / 64))
+    else:
+        close_lowp(out, ref)
+    if case == "max_prologue":
+        assert torch.equal(out, (args[0] * 2.0 + 1.0).amax(0, keepdim=True).t())
+    if case in ("sum_axis0", "one_slice", "middle_4d"):
+        xi = torch.randint(-3, 4, shapes[0], device=DEV).float()
+        axis = 0 if case == "sum_axis0" else 1
+        assert torch.equal(f(xi).double(), xi.double().sum(axis))
+
+
+def test_column_reduction_matches_the_reference_plan(monkeypatch):
+    """The same max and mean with the fold switched off (transpose kernel + row
+    reduction): the max bit for bit, the mean to rounding."""
+    torch.manual_seed(0)
+    x = torch.randn(3000, 1000, device=DEV)
+    fn = lambda t: (tj.max(t, axis=0), tj.mean(t, axis=0))  # noqa: E731
+    f = tj.jit(fn)
+    fams = [l.meta["family"] for l in f.compiled(x).launches]
+    assert fams.count("colreduce") == 2
+    col = f(x)
+    monkeypatch.setenv("TENSORJIT_HIP_COLREDUCE", "0")
+    g = tj.jit(lambda t: (tj.max(t, axis=0), tj.mean(t, axis=0)))
+    assert "colreduce" not in [l.meta["family"] for l in g.compiled(x).launches]
+    ref = g(x)
+    assert torch.equal(col[0], ref[0])
+    torch.testing.assert_close(col[1], ref[1], rtol=1e-5, atol=1e-6)
+
+
 def test_reduce_non_last_axis_via_transpose():
     torch.manual_seed(0)
     x = torch.randn(4, 5, 6, device=DEV)
