@@ -58,6 +58,18 @@ def _fn_rms(x, g):
     return tj.rms_norm(x, g)
 
 
+def _fn_sum_all(x):
+    import tensorjit as tj
+
+    return tj.sum(x)
+
+
+def _fn_sum_axis0(x):
+    import tensorjit as tj
+
+    return tj.sum(x, axis=0)
+
+
 def _fn_softmax(s):
     import tensorjit as tj
 
@@ -374,6 +386,19 @@ def secondary(torch, dev, quick):
     s = torch.randn(65536, 2048, device=dev, generator=gen) * 3
     row("c3_softmax_f32", _fn_softmax, [s], 2 * 65536 * 2048 * 4)
     del s
+    # reductions and rows past the reference plan's shapes: one long row split over
+    # workgroups, a reduction over the leading axis read in place, a row-fused LayerNorm
+    # over rows of 16384
+    xr = torch.randn(1 << 26, device=dev, generator=gen)
+    row("reduce_sum_f32_1x67108864_split", _fn_sum_all, [xr], (1 << 26) * 4 + 4)
+    del xr
+    xc = torch.randn(16384, 4096, device=dev, generator=gen)
+    row("colreduce_sum_axis0_f32_16384x4096", _fn_sum_axis0, [xc], 16384 * 4096 * 4 + 4096 * 4)
+    del xc
+    xw = torch.randn(8192, 16384, device=dev, generator=gen)
+    gw = 1 + 0.1 * torch.randn(16384, device=dev, generator=gen)
+    row("layernorm_f32_8192x16384_one_row_kernel", _fn_ln, [xw, gw], 2 * 8192 * 16384 * 4 + 16384 * 4)
+    del xw, gw
     if quick:
         return out
     # config 4: GEMMs
