@@ -1526,7 +1526,8 @@ def hb_config_ok(cfg, mm):
 
 def test_tensors_past_two_to_the_31_elements():
     """Iteration spaces of 2^31 elements and more take 64-bit offsets: a pointwise
-    chain and an RMSNorm over [2^21 + 3, 1024] bf16, and a GEMM whose [65536, 32768]
+    chain, an RMSNorm, a column sum and a split full sum over [2^21 + 3, 1024] bf16, and a
+    GEMM whose [65536, 32768]
     output has 2^31 elements, each checked against the oracle on its first rows and on
     the rows whose offsets are past 2^31."""
     torch.manual_seed(0)
@@ -1541,6 +1542,17 @@ def test_tensors_past_two_to_the_31_elements():
         close_lowp(y[sl], ry, tol=1e-2)
         close_lowp(r[sl], rr, tol=2e-2)
     del x, y, r
+    # a column reduction and a split full reduction over the same 2^31 + 3072 elements:
+    # small integers keep every partial exact, so both match torch bit for bit
+    xi = torch.randint(-3, 4, (rows, 1024), device=DEV).bfloat16()
+    print("past 2^31: column sum and split sum", flush=True)
+    fc = tj.jit(lambda t: tj.sum(t, axis=0))
+    assert fc.compiled(xi).launches[0].meta["family"] == "colreduce"
+    assert torch.equal(fc(xi), xi.float().sum(0).bfloat16())
+    fs = tj.jit(lambda t: tj.sum(tj.reshape(t, rows * 1024)))
+    assert fs.compiled(xi).launches[0].meta["splits"] > 1
+    assert torch.equal(fs(xi).float().reshape(()), xi.float().sum().bfloat16().float())
+    del xi
     torch.cuda.empty_cache()
     a = torch.randn(65536, 64, device=DEV).bfloat16()
     w = torch.randn(32768, 64, device=DEV).bfloat16()
