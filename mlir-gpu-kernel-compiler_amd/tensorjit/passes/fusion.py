@@ -282,6 +282,8 @@ def row_fuse(program: Program, max_n: int | None = None) -> Program:
                     continue
                 if cls == "vec" and k.iter_shape not in (rows + (n,), rows + (1,), rows):
                     continue
+                if not _reads_rows_per_row(k, grp, resolve, rows, n):
+                    continue
                 if not _joinable(k, grp, producer, upstream, resolve):
                     continue
                 grp.append(k)
@@ -309,6 +311,27 @@ def row_fuse(program: Program, max_n: int | None = None) -> Program:
         merged.append(rk)
     producer2 = {id(o): k for k in merged for o in k.outputs}
     return Program(program.graph, _schedule(merged, producer2, resolve), aliases)
+
+
+def _reads_rows_per_row(k: Kernel, grp: list[Kernel], resolve, rows: tuple, n: int) -> bool:
+    """Every node of ``k`` that runs over whole rows (shape ``rows + (n,)``) reads the
+    group's values whole-row or one per row (shape ``rows + (1,)``).  A per-row value of
+    shape ``rows`` broadcasts along the *last* axis of ``rows + (n,)`` (numpy rules align
+    trailing dims; possible when ``rows[-1] == n``), so it is a column value, which a row
+    kernel, holding one value per row, would apply to the wrong elements.  The reference's
+    ``row_fuse`` (``tensorjit/passes/fusion.py:290-295``) checks only the kernels' shapes
+    and fuses such a pair: ``x - mean(x, axis=0) * g`` over a square ``x`` then subtracts
+    each column's mean along its row.  Such a kernel stays out of the group here."""
+    outs = {id(o) for g in grp for o in g.outputs}
+    ok = {rows + (n,), rows + (1,)} | ({()} if rows == () else set())
+    full = rows + (n,)
+    for nd in k.nodes:
+        if tuple(nd.shape) != full and not (nd is k.anchor and k.kind == "reduce"):
+            continue
+        for i in nd.inputs:
+            if id(resolve(i)) in outs and tuple(i.shape) not in ok:
+                return False
+    return True
 
 
 def _joinable(k: Kernel, grp: list[Kernel], producer: dict, upstream: dict, resolve) -> bool:

@@ -373,6 +373,28 @@ def test_column_reduction_matches_the_reference_plan(monkeypatch):
     torch.testing.assert_close(col[1], ref[1], rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("n,dt", [(64, torch.float32), (4096, torch.float32), (4096, torch.bfloat16)])
+def test_column_values_over_square_rows_match_eager(n, dt):
+    """``x - mean(x, axis=0) * g`` and a row sum of ``x * mean(x, axis=-1)`` over square
+    ``x``: the per-column value broadcasts along the last axis, so row fusion must not
+    apply it per row.  Checked against eager torch in float64 (not only the oracle, which
+    shares the plan)."""
+    torch.manual_seed(0)
+    x = torch.randn(n, n, device=DEV).to(dt)
+    g = torch.randn(n, device=DEV).to(dt)
+    xd, gd = x.double(), g.double()
+    print(f"column values over square rows {n} {dt}", flush=True)
+    out = tj.jit(lambda t, w: t - tj.mean(t, axis=0) * w)(x, g)
+    ref = xd - xd.mean(0) * gd
+    out2 = tj.jit(lambda t, w: tj.sum(t * tj.mean(t, axis=-1), axis=-1) + w)(x, g)
+    ref2 = (xd * xd.mean(-1)).sum(-1) + gd
+    for o, r in ((out, ref), (out2, ref2)):
+        if dt == torch.float32:
+            close_f32(o, r, scale=1e-5 * math.sqrt(n / 64))
+        else:
+            close_lowp(o, r)
+
+
 def test_reduce_non_last_axis_via_transpose():
     torch.manual_seed(0)
     x = torch.randn(4, 5, 6, device=DEV)

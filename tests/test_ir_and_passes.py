@@ -216,3 +216,32 @@ def test_plan_transformer_block_config5():
     assert [n.op for n in p.kernels[8].nodes] == ["max", "sub", "exp", "sum", "div"]
     assert [n.op for n in p.kernels[11].nodes] == ["matmul", "add", "mul"]                  # residual (+ next x*x) fused
     assert [n.op for n in p.kernels[13].nodes] == ["matmul", "gelu"]
+
+
+def test_row_fusion_keeps_column_broadcasts_out_of_row_kernels():
+    """A reduced value without keepdim, shape ``rows``, broadcasts along the last axis
+    of ``rows + (N,)`` when ``rows[-1] == N``: it is a column value, and a row kernel
+    holding one value per row would apply it to the wrong elements.  The reference's
+    shape-only check fuses such pairs; here they stay apart, and the oracle agrees with
+    eager torch (float64) where the fused plan was off by O(1)."""
+    import oracle
+
+    torch.manual_seed(0)
+    cases = [
+        # per-column mean subtracted from a square matrix (column normalisation)
+        (lambda t, w: t - tj.mean(t, axis=0) * w, [(64, 64), (64,)],
+         lambda t, w: t - t.mean(0) * w),
+        # a reduction whose prologue reads the row means as a column broadcast
+        (lambda t, w: tj.sum(t * tj.mean(t, axis=-1), axis=-1) + w, [(48, 48), (48,)],
+         lambda t, w: (t * t.mean(-1)).sum(-1) + w),
+    ]
+    for fn, shapes, ref_fn in cases:
+        kinds, _ = _plan(fn, *shapes)
+        assert not any(k == "row" for k, _ in kinds), kinds
+        args = [torch.randn(s) for s in shapes]
+        out = oracle.run(fn, *args)[0]
+        ref = ref_fn(*[a.double() for a in args])
+        assert float((out.double() - ref).abs().max()) <= 1e-4 * float(ref.abs().max()), fn
+    # with keepdim the same chain is per row and row-fuses
+    kinds, _ = _plan(lambda t, w: t - tj.mean(t, axis=-1, keepdim=True) * w, (64, 64), (64,))
+    assert [k for k, _ in kinds] == ["row"]
