@@ -514,9 +514,12 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
         elif tuple(st.iter_shape) != vec_shape:
             scalar_ids |= {id(n) for n in st.nodes}
     is_vec = lambda n: id(n) not in scalar_ids  # noqa: E731
-    # vec values read by a later stage stay in registers
+    # vec values read by a later stage stay in registers, and so do those a per-row node
+    # reads (possible only with N == 1, where the row is one element)
+    anchors = {id(st.anchor) for st in stages if st.kind == "reduce"}   # read their input in the row loop
     kept = [n for si, st in enumerate(stages) for n in st.nodes
-            if is_vec(n) and any(stage_of.get(id(u), si) != si for u in n.users if id(u) in inside)]
+            if is_vec(n) and any(stage_of.get(id(u), si) != si or not (is_vec(u) or id(u) in anchors)
+                                 for u in n.users if id(u) in inside)]
     kept_ids = {id(n) for n in kept}
     scalars = [n for n in k.nodes if not is_vec(n)]
     nred = sum(st.kind == "reduce" for st in stages)
@@ -589,7 +592,8 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
             nm = g.names[id(n)]
             L.append(f"  float {nm}_r[{NCH}][{vec}];")
         for n in kept:
-            L.append(f"  float {g.names[id(n)]}_r[{NCH}][{vec}];")
+            # lanes past the row's end never write theirs: start them at zero
+            L.append(f"  float {g.names[id(n)]}_r[{NCH}][{vec}]{'' if full else ' = {}'};")
     preload_lines = []
     if preload and vec_ext:
         preload_lines.append("#pragma unroll")
@@ -665,8 +669,16 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
         """Per-row scalar nodes (uniform across the workgroup)."""
         out = []
         local: dict[int, str] = {id(anchor): g.names[id(anchor)]} if anchor is not None else {}
-        for n in st.inputs:
-            if id(n) in inside:
+        for n in st.inputs + [i for nd in nodes for i in nd.inputs if id(i) in inside and is_vec(i)]:
+            if id(n) in local or not any(n in m.inputs for m in nodes):
+                continue
+            if id(n) in inside and is_vec(n):
+                # a row value read per row: N == 1, and the row's one element is held by
+                # the row's first lane; every lane takes that lane's value
+                assert N == 1 and id(n) in kept_ids, (g.fname, n.name)
+                local[id(n)] = (f"__builtin_bit_cast(float, __builtin_amdgcn_readfirstlane("
+                                f"__builtin_bit_cast(int, {g.names[id(n)]}_r[0][0])))")
+            elif id(n) in inside:
                 local[id(n)] = g.names[id(n)]
             elif any(n in m.inputs for m in nodes):
                 strides = access_strides(n, g.consumer(n, [m for m in nodes if n in m.inputs]), shape)

@@ -180,17 +180,21 @@ def _gen_rows(kk: _K, stages, rows, N) -> str:
         elif tuple(st.iter_shape) != vshape:
             scalar_ids |= {id(n) for n in st.nodes}
     is_vec = lambda n: id(n) in inside and id(n) not in scalar_ids  # noqa: E731
+    # row values another stage reads, or a per-row node reads (only with N == 1, where a
+    # row is one element), go through a row buffer
+    anchors = {id(st.anchor) for st in stages if st.kind == "reduce"}   # read their input in the row loop
     temps = [n for si, st in enumerate(stages) for n in st.nodes
              if is_vec(n) and id(n) not in out_of
-             and any(stage_of.get(id(u), si) != si for u in n.users if id(u) in inside)]
+             and any(stage_of.get(id(u), si) != si or not (is_vec(u) or id(u) in anchors)
+                     for u in n.users if id(u) in inside)]
     temp_of = {id(n): i for i, n in enumerate(temps)}
     rstr = _strides(rows)
     ridx = [f"r{d}" for d in range(len(rows))]
 
-    def vec_ref(n):
+    def vec_ref(n, i="n"):
         if id(n) in out_of:
-            return f"y{out_of[id(n)]}p[r * {N}L + n]"
-        return f"w{temp_of[id(n)]}[n]"
+            return f"y{out_of[id(n)]}p[r * {N}L + {i}]"
+        return f"w{temp_of[id(n)]}[{i}]"
 
     L = kk.header()
     L.append("  #pragma omp parallel")
@@ -221,10 +225,12 @@ def _gen_rows(kk: _K, stages, rows, N) -> str:
     def scalar_loads(st, used_nodes, shape, local):
         out = []
         idx = ridx + (["0"] * (len(shape) - len(rows)))
-        for n in st.inputs:
+        for n in list(st.inputs) + [i for m in used_nodes for i in m.inputs if is_vec(i)]:
             if id(n) in local or not any(n in m.inputs for m in used_nodes):
                 continue
-            if id(n) in inside:
+            if id(n) in inside and is_vec(n):
+                local[id(n)] = vec_ref(n, "0")      # N == 1: the row's one element
+            elif id(n) in inside:
                 local[id(n)] = kk.name[id(n)]
             else:
                 strd = _read_strides(n, kk.consumer(n, used_nodes), shape)
@@ -243,6 +249,10 @@ def _gen_rows(kk: _K, stages, rows, N) -> str:
             for n in pro:
                 body.append(f"const float {kk.name[id(n)]} = {kk.expr(n, local)};")
                 local[id(n)] = kk.name[id(n)]
+                if id(n) in out_of:
+                    body.append(f"y{out_of[id(n)]}p[r * {N}L + n] = {kk.name[id(n)]};")
+                elif id(n) in temp_of:
+                    body.append(f"w{temp_of[id(n)]}[n] = {kk.name[id(n)]};")
             xv = local[id(red.inputs[0])]
             if red.op == "max":
                 init, upd, clause = "-INFINITY", f"acc = fmaxf(acc, {xv});", "max"

@@ -303,3 +303,38 @@ def test_random_column_reduction_matches_the_oracle(seed, monkeypatch):
     fn, shapes = graph_fuzz.column_program(seed)
     print(f"random column reduction {seed} {shapes}", flush=True)
     _check_vs_oracle(fn, shapes, seed, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2)])
+
+
+def test_rows_of_one_element_read_per_row(tj_env):
+    """Random program 144 has rows of one element ([2, 37, 1]): a per-row epilogue reads
+    a value of an earlier whole-row stage, which a row is then just one element of.  The
+    hip generator and the oracle both emitted a read of a loop-local name there; now the
+    hip kernel compiles and the oracle's row-fused plan agrees with its unfused plan."""
+    import os
+
+    import oracle
+
+    fn, shapes = graph_fuzz.program(144)
+    assert shapes[0][-1] == 1
+    p = lower(tj.trace(fn, [TensorType(s, DType.f32) for s in shapes]), "hip")
+    assert any(k.kind == "row" for k in p.kernels)
+    src, _ = hb.generate(hb.sink_epilogue_into_rows(hb.fold_elementwise_into_gemm(hb.fuse_attention(p))))
+    hb.compile_source(src, "gfx950")
+    g = torch.Generator().manual_seed(144)
+    ins = [torch.randn(s, generator=g) for s in shapes]
+    fused = oracle.run(fn, *ins)
+    os.environ["TENSORJIT_NO_ROW_FUSION"] = "1"
+    try:
+        plain = oracle.run(fn, *ins)
+    finally:
+        del os.environ["TENSORJIT_NO_ROW_FUSION"]
+    for a, b in zip(fused, plain):
+        torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.gpu
+def test_rows_of_one_element_read_per_row_on_the_gpu(monkeypatch):
+    monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
+    fn, shapes = graph_fuzz.program(144)
+    print(f"random program 144 {shapes}", flush=True)
+    _check_vs_oracle(fn, shapes, 144, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2), (torch.float16, 1e-2)])
