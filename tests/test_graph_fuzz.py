@@ -338,3 +338,29 @@ def test_rows_of_one_element_read_per_row_on_the_gpu(monkeypatch):
     fn, shapes = graph_fuzz.program(144)
     print(f"random program 144 {shapes}", flush=True)
     _check_vs_oracle(fn, shapes, 144, [(torch.float32, 1e-5), (torch.bfloat16, 5e-2), (torch.float16, 1e-2)])
+
+
+DIFF_CASES = ([("program", s) for s in range(0, 200, 5)] + [("broadcast", s) for s in range(0, 60, 5)]
+              + [("column", s) for s in range(0, 24, 3)] + [("wide_row", s) for s in range(0, 24, 4)]
+              + [("program", 144)])
+
+
+@pytest.mark.parametrize("gen,seed", DIFF_CASES)
+def test_row_fusion_matches_the_unfused_plan(gen, seed, monkeypatch):
+    """The oracle with row fusion against the oracle without it, on random programs: the
+    parity tests compare the hip path with an oracle that shares its plan, so a plan that
+    computes the wrong thing (column values applied per row) or a generator that cannot
+    express a fused row (rows of one element) shows only here.  fp32, within 1e-5."""
+    import oracle
+
+    r = {"program": graph_fuzz.program, "broadcast": graph_fuzz.broadcast_program,
+         "column": graph_fuzz.column_program, "wide_row": graph_fuzz.wide_row_program}[gen](seed)
+    fn, shapes = r[0], r[1]
+    g = torch.Generator().manual_seed(seed)
+    ins = [torch.randn(s, generator=g) for s in shapes]
+    fused = oracle.run(fn, *ins)
+    monkeypatch.setenv("TENSORJIT_NO_ROW_FUSION", "1")
+    plain = oracle.run(fn, *ins)
+    for a, b in zip(fused, plain):
+        scale = float(b.abs().max()) or 1.0
+        assert float(((a - b).abs() / (b.abs() + scale)).max()) <= 1e-5, (gen, seed)
