@@ -364,3 +364,46 @@ def test_row_fusion_matches_the_unfused_plan(gen, seed, monkeypatch):
     for a, b in zip(fused, plain):
         scale = float(b.abs().max()) or 1.0
         assert float(((a - b).abs() / (b.abs() + scale)).max()) <= 1e-5, (gen, seed)
+
+
+EVAL_CASES = ([("program", s) for s in range(0, 300, 10)] + [("broadcast", s) for s in range(0, 100, 10)]
+              + [("attention", s) for s in range(0, 30, 5)] + [("column", s) for s in range(0, 30, 5)]
+              + [("wide_row", s) for s in range(0, 16, 4)] + [("block", 0), ("reduction", 0)])
+
+
+@pytest.mark.parametrize("gen,seed", EVAL_CASES)
+def test_oracle_matches_the_float64_graph_evaluation(gen, seed):
+    """The oracle (the reference plan as C) against the traced graph evaluated node by
+    node in float64 (tests/graph_eval.py: no fusion, no plan): a plan or oracle that
+    computes something other than the ops' meaning fails here, whatever the hip path
+    does.  Within 2e-5 of the output's magnitude (fp32 accumulation; the largest seen
+    over 510 programs was 9.4e-6)."""
+    import graph_eval
+    import oracle
+
+    r = {"program": graph_fuzz.program, "broadcast": graph_fuzz.broadcast_program,
+         "attention": graph_fuzz.attention_program, "column": graph_fuzz.column_program,
+         "wide_row": graph_fuzz.wide_row_program, "block": graph_fuzz.block_program,
+         "reduction": graph_fuzz.reduction_program}[gen](seed)
+    fn, shapes = r[0], r[1]
+    scales = r[2] if len(r) > 2 else None
+    g = torch.Generator().manual_seed(seed)
+    ins = [torch.randn(s, generator=g) * (scales[i] if scales else 1.0) for i, s in enumerate(shapes)]
+    ref = graph_eval.evaluate(tj.trace(fn, [TensorType(s, DType.f32) for s in shapes]), *ins)
+    out = oracle.run(fn, *ins)
+    for o, rf in zip(out, ref):
+        scale = float(rf.abs().max()) or 1.0
+        assert float(((o.double() - rf).abs() / (rf.abs() + scale)).max()) <= 2e-5, (gen, seed)
+
+
+def test_graph_evaluation_catches_a_column_value_applied_per_row(tj_env):
+    """The float64 evaluation tells the two readings of a no-keepdim column mean apart:
+    over a square x, the column reading (the ops' meaning) and the per-row reading (what
+    a row kernel would compute) differ by O(1)."""
+    import graph_eval
+
+    x, w = torch.randn(64, 64, dtype=torch.float64), torch.randn(64, dtype=torch.float64)
+    (ref,) = graph_eval.evaluate(tj.trace(lambda t, v: t - tj.mean(t, axis=0) * v,
+                                          [TensorType((64, 64), DType.f32), TensorType((64,), DType.f32)]), x, w)
+    torch.testing.assert_close(ref, x - x.mean(0) * w)
+    assert float((ref - (x - (x.mean(0) * w)[:, None])).abs().max()) > 0.1
