@@ -8,6 +8,12 @@ use this package, as the checker / CPU timing baseline.  The product path
 tensorjit's own passes (the shared upstream of every backend) and executes the
 resulting kernel program through the C restatement of the reference ``c``
 backend (``oracle/c_backend.py``).
+
+What pins it: float64 closed forms per op family (``tests/test_oracle.py``), and a
+plan-free float64 evaluation of the traced graph node by node
+(``tests/graph_eval.py``) that random programs of every fuzz generator must match
+(``tests/test_graph_fuzz.py``), so a fusion plan that computes something other than
+the ops' meaning fails even though the oracle and the hip path share it.
 """
 from __future__ import annotations
 
