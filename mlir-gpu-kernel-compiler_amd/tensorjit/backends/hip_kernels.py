@@ -41,7 +41,8 @@ from dataclasses import dataclass, field
 from ..ir import DType, Node
 from ..passes import Kernel
 from ..runtime.autotune import CU_COUNT
-from .common import access_strides, broadcast_strides, emit_expr, inner_stride, merged_dims, offset_expr
+from .common import (access_strides, broadcast_strides, contiguous_strides, emit_expr, inner_stride, merged_dims,
+                     offset_expr)
 from .hip_prelude import CTYPE, vec_width
 
 THREADS = 256
@@ -140,6 +141,14 @@ def _vec_for(row_len: int, numel: int, dtype: DType) -> int:
 MALL_BYTES = 256 << 20
 
 
+def _flat_access(shape, strides) -> bool:
+    """Are ``strides`` over ``shape`` the row-major strides of ``shape`` itself, or all
+    zero (one scalar)?  Dims of size 1 take any stride."""
+    contiguous = contiguous_strides(shape)
+    return (all(d == 1 or s == c for d, s, c in zip(shape, strides, contiguous))
+            or all(d == 1 or s == 0 for d, s in zip(shape, strides)))
+
+
 def _streamed(shape, strides) -> bool:
     """Every element of the input is read once over ``shape``: no broadcast (stride-0) dim."""
     return all(st != 0 for d, st in zip(shape, strides) if d > 1)
@@ -183,7 +192,12 @@ def gen_pointwise(g: KernelGen, nodes: list[Node], iter_shape: tuple[int, ...]) 
     reduction-free row groups)."""
     k = g.k
     numel = math.prod(iter_shape) if iter_shape else 1
-    row_len = iter_shape[-1] if iter_shape else 1
+    in_st = {id(n): access_strides(n, g.consumer(n, nodes), iter_shape) for n in k.inputs}
+    # every input read contiguously over the whole iteration space (or as one scalar):
+    # element e sits at offset e of each, so a vector may cross rows and its width
+    # depends on the element count alone ([16384, 4095] fp32: 16-byte vectors, not scalars)
+    flat = all(_flat_access(iter_shape, st) for st in in_st.values())
+    row_len = numel if flat else (iter_shape[-1] if iter_shape else 1)
     vec = _vec_for(row_len, numel, _kernel_dtype(k))
     nvec = numel // vec
     unroll = POINTWISE_UNROLL
@@ -192,7 +206,6 @@ def gen_pointwise(g: KernelGen, nodes: list[Node], iter_shape: tuple[int, ...]) 
     idx_t = _index_type(numel)
     guard = nvec % per_block != 0
     inside = {id(n) for n in nodes}
-    in_st = {id(n): access_strides(n, g.consumer(n, nodes), iter_shape) for n in k.inputs}
     streamed = {id(n) for n in k.inputs if _streamed(iter_shape, in_st[id(n)])}
     nt = _nt_loads(sum(math.prod(n.shape or (1,)) * n.dtype.itemsize for n in k.inputs if id(n) in streamed)
                    + sum(numel * o.dtype.itemsize for o in k.outputs))

@@ -538,3 +538,22 @@ def test_transpose_then_reduce_folds_into_a_column_reduction(tj_env, monkeypatch
         assert (seen == 1).all() and (slots == 1).all(), (A, Rd, B, vec)
         cw = min(16, S)          # the combine launch's waves split each output's S partials
         assert sorted(s for w in range(cw) for s in range(w, S, cw)) == list(range(S))
+
+
+def test_contiguous_pointwise_kernels_vectorise_across_rows(tj_env):
+    """A pointwise kernel whose inputs all read the whole iteration space contiguously (or
+    as one scalar) takes 16-byte vectors by element count, whatever the row length; a
+    row-broadcast or transposed input keeps the row structure (and odd rows scalar)."""
+    def vec_of(fn, shapes, dt=DType.f32):
+        p = C.lower(tj.trace(fn, [TensorType(s, dt) for s in shapes]), "hip")
+        src, launches = hb.generate(p)
+        return [l.meta["vec"] for l in launches], src
+
+    assert vec_of(lambda x, y: x * 2.0 + y, [(16384, 4095)] * 2)[0] == [4]
+    assert vec_of(lambda x, y: x * 2.0 + y, [(16384, 4095)] * 2, DType.bf16)[0] == [8]
+    v, src = vec_of(lambda x: tj.gelu(x), [(1000, 1001)])
+    assert v == [4]
+    hb.compile_source(src, "gfx950")
+    assert vec_of(lambda x, y: x * 2.0 + y, [(16384, 4095), (4095,)])[0] == [1]
+    assert vec_of(lambda x: x * 2.0, [(999, 1001)])[0] == [1]                 # 999999 elements
+    assert vec_of(lambda x: x * 2.0, [(64, 4096)])[0] == [4]

@@ -132,6 +132,22 @@ def test_tiled_transposes_are_bit_exact(shape, perm, dt):
     assert torch.equal(out, y.permute(*perm).contiguous())
 
 
+@pytest.mark.parametrize("shape", [(16384, 4095), (1000, 1001), (3, 5, 7, 9)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16, torch.int32])
+def test_odd_rows_of_contiguous_operands_vectorise_bit_exact(shape, dt):
+    """Same-shape pointwise kernels over odd row lengths run 16-byte vectors across rows:
+    bit for bit against torch (x * 2 + y is exact in every dtype: the product by 2 is
+    exact, one rounding for the sum)."""
+    g = torch.Generator(device=DEV).manual_seed(11)
+    x = (torch.randn(shape, device=DEV, generator=g) * 100).to(dt)
+    y = (torch.randn(shape, device=DEV, generator=g) * 100).to(dt)
+    f = tj.jit(lambda a, b: a * 2.0 + b)
+    out = f(x, y)
+    numel = math.prod(shape)
+    assert f.compiled(x, y).launches[0].meta["vec"] == (16 // x.element_size() if numel % (16 // x.element_size()) == 0 else 1)
+    assert torch.equal(out, x * 2 + y)
+
+
 def test_int32_arithmetic_and_max_are_exact_below_2_24():
     """int32 storage: pointwise ops evaluate in fp32, as the reference's expressions do, and
     convert on store, so integer results below 2^24 in magnitude are exact -- a pointwise chain
