@@ -17,7 +17,7 @@ from tensorjit.compiler import lower
 from tensorjit.ir import DType, TensorType
 
 CPU_SEEDS = range(16)
-GPU_SEEDS = range(40)
+GPU_SEEDS = range(80)
 
 
 @pytest.mark.parametrize("seed", CPU_SEEDS)
