@@ -975,6 +975,36 @@ def test_torch_compile_op_coverage_strict(monkeypatch):
         torch.testing.assert_close(g_, r_, atol=2e-4, rtol=2e-4)
 
 
+def test_torch_compile_reaches_column_split_and_wide_row_kernels(monkeypatch):
+    """Under torch.compile (TENSORJIT_STRICT=1, no eager fallback): a batch mean over dim 0
+    (a column reduction), an MSE loss over a whole [2048, 1024] tensor (one long row, split
+    over workgroups) and a LayerNorm over rows of 16384 (one row kernel) match eager."""
+    from tensorjit.backends import hip_backend as hb
+
+    monkeypatch.setenv("TENSORJIT_STRICT", "1")
+    torch.manual_seed(0)
+    torch._dynamo.reset()
+    fams = []
+    orig = hb.HipProgram.__init__
+
+    def spy(self, *a, **kw):
+        orig(self, *a, **kw)
+        fams.extend(l.meta["family"] for l in self.launches)
+
+    monkeypatch.setattr(hb.HipProgram, "__init__", spy)
+
+    def fn(x, y, z, g):
+        return x.mean(dim=0), ((x - y) ** 2.0).mean(), F.layer_norm(z, (z.shape[-1],), g)
+
+    x, y = torch.randn(2048, 1024, device=DEV), torch.randn(2048, 1024, device=DEV)
+    z, g = torch.randn(64, 16384, device=DEV), 1 + 0.1 * torch.randn(16384, device=DEV)
+    c = torch.compile(fn, backend=tj.torch_compile_backend)
+    got, ref = c(x, y, z, g), fn(x, y, z, g)
+    for g_, r_ in zip(got, ref):
+        torch.testing.assert_close(g_, r_, atol=2e-4, rtol=2e-4)
+    assert {"colreduce", "row_combine", "row"} <= set(fams), fams
+
+
 def test_torch_compile_attention_module_runs_the_flash_kernel(monkeypatch):
     """An attention nn.Module in bf16 under torch.compile lands on the fused kernel."""
     monkeypatch.setenv("TENSORJIT_STRICT", "1")
