@@ -102,6 +102,25 @@ def test_static_arena_run_of_split_row_reductions():
     assert sizes[1] < sizes[0]
 
 
+def test_static_arena_run_of_column_reductions():
+    """A column reduction's partials live in the workspace too: in the static arena the
+    column sum and max match the allocating run bit for bit, a program with more partials
+    first and one with fewer after it."""
+    f = tj.jit(lambda t: (tj.sum(t, axis=0), tj.max(t, axis=0)))
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    sizes = []
+    for shape in [(8192, 4096), (3000, 1000)]:
+        x = torch.randn(shape, device=DEV, generator=gen)
+        cp = f.compiled(x)
+        assert [l.meta["family"] for l in cp.launches] == ["colreduce", "colreduce_combine"] * 2
+        assert 0 < cp.arena_bytes <= rt.STATIC_ARENA_BYTES
+        sizes.append(cp.arena_bytes)
+        ref, got = _both(cp, [x])
+        assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
+        assert torch.equal(got[1], x.amax(0))
+    assert sizes[1] < sizes[0]
+
+
 def test_programs_larger_than_the_static_arena_are_refused():
     args = _inputs(16384)          # 48 MiB LayerNorm output + 192 MiB gelu output
     cp = tj.jit(_mlp).compiled(*args)
