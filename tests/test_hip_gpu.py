@@ -847,6 +847,36 @@ def test_graph_replays_match_eager_every_time(monkeypatch):
     assert cp.native_stats()["graph_captures"] <= 3 and cp.stats["graph_replays"] == 6
 
 
+def test_graph_replays_of_split_column_and_wide_row_kernels(monkeypatch):
+    """A program of 13 launches (column sums, maxima and means, split row sums and means,
+    a 16384-wide LayerNorm) replays as a hipGraph by default (12 launches and more): every
+    replay, with eager work in between, matches the first call bit for bit and the eager
+    results to rounding."""
+    monkeypatch.delenv("TENSORJIT_HIP_GRAPH", raising=False)
+    torch.manual_seed(0)
+    x, y = torch.randn(4096, 2048, device=DEV), torch.randn(4, 1 << 20, device=DEV)
+    z, g = torch.randn(32, 16384, device=DEV), 1 + 0.1 * torch.randn(16384, device=DEV)
+
+    def fn(a, b, c, w):
+        return (tj.sum(a, axis=0), tj.max(a, axis=0), tj.mean(a * a, axis=0), tj.sum(b, axis=-1),
+                tj.mean(tj.abs(b), axis=-1), tj.max(b, axis=-1), tj.layer_norm(c, w))
+
+    f = tj.jit(fn)
+    cp = f.compiled(x, y, z, g)
+    assert len(cp.launches) == 13 and cp.use_graph
+    first = [t.clone() for t in f(x, y, z, g)]
+    ref = (x.sum(0), x.amax(0), (x * x).mean(0), y.sum(-1), y.abs().mean(-1), y.amax(-1),
+           F.layer_norm(z, (16384,), g))
+    for r, o in zip(ref, first):
+        torch.testing.assert_close(o, r, rtol=1e-4, atol=1e-4)
+    for i in range(4):
+        outs = f(x, y, z, g)
+        torch.cuda.synchronize()
+        assert all(torch.equal(o, p) for o, p in zip(outs, first)), i
+        _ = (x * 2).sum().item()          # eager work between replays
+    assert cp.stats["graph_replays"] >= 4
+
+
 def test_transformer_block_small():
     torch.manual_seed(0)
     T_, D, H = 12, 32, 64
