@@ -12,12 +12,17 @@ import torch
 
 import graph_fuzz
 import tensorjit as tj
+from parity import compare
 from tensorjit.backends import hip_backend as hb
 from tensorjit.compiler import lower
 from tensorjit.ir import DType, TensorType
 
 CPU_SEEDS = range(16)
 GPU_SEEDS = range(80)
+# norm-wise bounds (tests/parity.py) per storage type: a program stores its intermediates
+# in that type between kernels, each store a rounding of ~1.7e-3 (bf16) or ~2e-4 (fp16)
+# RMS relative that later kernels carry forward
+NORM = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 2e-3}
 
 
 @pytest.mark.parametrize("seed", CPU_SEEDS)
@@ -55,13 +60,8 @@ def test_random_program_matches_the_oracle(seed, monkeypatch):
         outs = outs if isinstance(outs, (tuple, list)) else [outs]
         refs = oracle.run(fn, *[t.to(dt).float() for t in ins])
         assert len(outs) == len(refs)
-        for o, r in zip(outs, refs):
-            o = o.float().cpu()
-            assert o.shape == r.shape
-            assert torch.isfinite(o).all() == torch.isfinite(r).all()
-            scale = float(r.abs().max()) or 1.0
-            err = float(((o - r).abs() / (r.abs() + scale)).max())
-            assert err <= tol, (seed, dt, err)
+        for i, (o, r) in enumerate(zip(outs, refs)):
+            compare(o, r, rtol=tol, scale=tol, norm=NORM[dt], what=f"seed {seed} {dt} output {i}")
 
 
 ATTN_SEEDS = range(24)
@@ -106,12 +106,9 @@ def _check_vs_oracle(fn, shapes, seed, dts, scales=None):
         outs = tj.jit(fn)(*[t.to(dt).cuda() for t in ins])
         outs = outs if isinstance(outs, (tuple, list)) else [outs]
         refs = oracle.run(fn, *[t.to(dt).float() for t in ins])
-        for o, r in zip(outs, refs):
-            o = o.float().cpu()
-            assert o.shape == r.shape and torch.isfinite(o).all()
-            scale = float(r.abs().max()) or 1.0
-            err = float(((o - r).abs() / (r.abs() + scale)).max())
-            assert err <= tol, (seed, dt, err)
+        for i, (o, r) in enumerate(zip(outs, refs)):
+            assert torch.isfinite(o).all()
+            compare(o, r, rtol=tol, scale=tol, norm=NORM[dt], what=f"seed {seed} {dt} output {i}")
 
 
 @pytest.mark.gpu
@@ -345,6 +342,13 @@ DIFF_CASES = ([("program", s) for s in range(0, 200, 5)] + [("broadcast", s) for
               + [("program", 144)])
 
 
+# Programs whose own fp32 evaluation sits far from float64 relative to the output's RMS.
+# Broadcast program 35 layer-normalises a softmax of a softmax: its rows are nearly uniform
+# (~1/96), so x - mean(x) cancels ~7 of fp32's 24 bits and both plans land 2.2e-5 * rms
+# from the float64 graph evaluation at the same element.
+ILL_CONDITIONED = {("broadcast", 35): 3e-5}
+
+
 @pytest.mark.parametrize("gen,seed", DIFF_CASES)
 def test_row_fusion_matches_the_unfused_plan(gen, seed, monkeypatch):
     """The oracle with row fusion against the oracle without it, on random programs: the
@@ -361,9 +365,9 @@ def test_row_fusion_matches_the_unfused_plan(gen, seed, monkeypatch):
     fused = oracle.run(fn, *ins)
     monkeypatch.setenv("TENSORJIT_NO_ROW_FUSION", "1")
     plain = oracle.run(fn, *ins)
-    for a, b in zip(fused, plain):
-        scale = float(b.abs().max()) or 1.0
-        assert float(((a - b).abs() / (b.abs() + scale)).max()) <= 1e-5, (gen, seed)
+    tol = ILL_CONDITIONED.get((gen, seed), 1e-5)
+    for i, (a, b) in enumerate(zip(fused, plain)):
+        compare(a, b, rtol=1e-5, scale=tol, norm=1e-5, what=f"{gen} {seed} output {i}")
 
 
 EVAL_CASES = ([("program", s) for s in range(0, 300, 10)] + [("broadcast", s) for s in range(0, 100, 10)]
@@ -391,9 +395,8 @@ def test_oracle_matches_the_float64_graph_evaluation(gen, seed):
     ins = [torch.randn(s, generator=g) * (scales[i] if scales else 1.0) for i, s in enumerate(shapes)]
     ref = graph_eval.evaluate(tj.trace(fn, [TensorType(s, DType.f32) for s in shapes]), *ins)
     out = oracle.run(fn, *ins)
-    for o, rf in zip(out, ref):
-        scale = float(rf.abs().max()) or 1.0
-        assert float(((o.double() - rf).abs() / (rf.abs() + scale)).max()) <= 2e-5, (gen, seed)
+    for i, (o, rf) in enumerate(zip(out, ref)):
+        compare(o, rf, rtol=2e-5, scale=2e-5, norm=2e-5, what=f"{gen} {seed} output {i}")
 
 
 def test_graph_evaluation_catches_a_column_value_applied_per_row(tj_env):

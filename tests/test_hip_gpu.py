@@ -1,10 +1,10 @@
 """hip backend on a real MI355X: parity with the CPU oracle (the restated reference
 `c` backend) and with eager PyTorch on the same seeded inputs.
 
-Tolerances (north star): fp32 |a-b| <= atol + 1e-5*|b| with atol = 1e-5 * max|b|
-(scaled to the output's magnitude, as the reference's own `_close` pairs atol with
-rtol); bf16/fp16 storage within 2e-2 of the fp32 oracle; integer / max / copy
-results bit-exact.  Case list follows the reference's tests/test_backends.py and
+Tolerances (north star; tests/parity.py): fp32 |a-b| <= 1e-5*rms(b) + 1e-5*|b| per element
+and ||a-b|| <= 1e-5*||b|| over the tensor and over every row; bf16/fp16 storage within 2e-2
+of the fp32 oracle per element (atol 2e-2*rms) and within 5e-3 in norm, whole and per row;
+integer / max / copy results bit-exact.  Case list follows the reference's tests/test_backends.py and
 tests/test_cuda_backend.py.
 """
 import math
@@ -16,6 +16,7 @@ import torch.nn.functional as F
 
 import oracle
 import tensorjit as tj
+from parity import close_f32, close_lowp
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -34,36 +35,17 @@ def _env(monkeypatch, tmp_path_factory):
     yield
 
 
-def _host(t):
-    # float64 for normal sizes; float32 for the full-size configs (1e8+ elements)
-    t = t.detach().cpu()
-    return t.double() if t.numel() < 2**25 else t.float()
-
-
-def close_f32(out, ref, rtol=1e-5, scale=1e-5):
-    out, ref = _host(out), _host(ref)
-    atol = scale * max(float(ref.abs().max()), 1e-30)
-    err = (out - ref).abs() - (atol + rtol * ref.abs())
-    assert float(err.max()) <= 0, f"max excess {float(err.max()):.3e} (atol {atol:.3e})"
-
-
-def close_lowp(out, ref, tol=2e-2):
-    out, ref = _host(out), _host(ref)
-    atol = tol * max(float(ref.abs().max()), 1e-30)
-    assert float(((out - ref).abs() - (atol + tol * ref.abs())).max()) <= 0
-
-
-def check_vs_oracle(fn, *args, rtol=1e-5, scale=1e-5):
+def check_vs_oracle(fn, *args, rtol=1e-5, scale=1e-5, norm=None, lowp_norm=5e-3):
     f = tj.jit(fn)
     outs = f(*args)
     outs = outs if isinstance(outs, tuple) else (outs,)
     refs = oracle.run(fn, *[a.float().cpu() for a in args])
-    for o, r in zip(outs, refs):
+    for i, (o, r) in enumerate(zip(outs, refs)):
         assert o.is_cuda and o.shape == r.shape
         if o.dtype == torch.float32:
-            close_f32(o, r, rtol, scale)
+            close_f32(o, r, rtol, scale, norm=norm, what=f"output {i}")
         else:
-            close_lowp(o, r)
+            close_lowp(o, r, norm=lowp_norm, what=f"output {i}")
     return f, outs
 
 
@@ -847,6 +829,40 @@ def test_graph_replays_match_eager_every_time(monkeypatch):
     assert cp.native_stats()["graph_captures"] <= 3 and cp.stats["graph_replays"] == 6
 
 
+def test_graph_captures_stay_bounded_when_the_caller_keeps_its_outputs(monkeypatch):
+    """A 16-launch program replays hipGraphs by default; a caller that keeps every output
+    presents a new pointer set on each call.  After 4 captures in a row the runtime
+    launches such calls directly (no capture, no instantiation) and captures a pointer
+    set only when it recurs, so graph mode comes back once the caller drops its outputs
+    and the pool hands the same buffer out again.  Every output is bit-identical."""
+    monkeypatch.delenv("TENSORJIT_HIP_GRAPH", raising=False)
+    torch.manual_seed(0)
+    x, w = torch.randn(16, 32, device=DEV), torch.randn(32, 32, device=DEV)
+
+    def fn(a, b):
+        for _ in range(8):
+            a = tj.softmax(tj.matmul(a, b) + 0.5)
+        return a
+
+    f = tj.jit(fn)
+    cp = f.compiled(x, w)
+    assert cp.use_graph and len(cp.launches) == 16
+    kept = [f(x, w) for _ in range(12)]
+    torch.cuda.synchronize()
+    st = cp.stats
+    assert st["graph_captures"] == 4 and st["graph_replays"] == 4 and st["direct_fallbacks"] == 8, st
+    first = kept[0].clone()
+    assert all(torch.equal(k, first) for k in kept)
+    del kept
+    for _ in range(6):
+        out = f(x, w)
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+        del out
+    st2 = cp.stats
+    assert st2["graph_replays"] - st["graph_replays"] >= 4 and st2["graph_captures"] - st["graph_captures"] <= 2, st2
+
+
 def test_graph_replays_of_split_column_and_wide_row_kernels(monkeypatch):
     """A program of 13 launches (column sums, maxima and means, split row sums and means,
     a 16384-wide LayerNorm) replays as a hipGraph by default (12 launches and more): every
@@ -1075,6 +1091,18 @@ def test_config2_full_size_fp32_vs_oracle():
     check_vs_oracle(lambda x, a, b, c: tj.gelu(x * a + b) * tj.sigmoid(c) + x, x, a, b, c)
 
 
+def test_config2_full_size_bf16_vs_oracle():
+    """Config 2 in bf16 at its full shape (the bench's `c2_eltwise_bf16` line): one pointwise
+    kernel, fp32 arithmetic on bf16 loads, one bf16 rounding at the store, against the fp32
+    oracle of the same (upcast) inputs."""
+    torch.manual_seed(0)
+    x = torch.randn(16384, 4096, device=DEV).bfloat16()
+    a, b = torch.randn(4096, device=DEV).bfloat16(), torch.randn(4096, device=DEV).bfloat16()
+    c = (torch.rand(16384, 4096, device=DEV) * 8 - 4).bfloat16()
+    f, _ = check_vs_oracle(lambda x, a, b, c: tj.gelu(x * a + b) * tj.sigmoid(c) + x, x, a, b, c)
+    assert f.compiled(x, a, b, c).num_kernels == 1
+
+
 def test_config3_full_size_rows_vs_oracle():
     torch.manual_seed(0)
     x = torch.randn(65536, 4096, device=DEV).bfloat16()
@@ -1143,16 +1171,8 @@ def test_config5_attention_full_size_sampled_heads():
     assert bool(((o >= lo - 1e-2) & (o <= hi + 1e-2)).all())
 
 
-def test_config5_block_full_size_batch0_vs_fp32():
-    """Config 5's layer at its full shape ([4, 2048, 4096], 32 heads x 128, MLP 11008, bf16) on
-    the packaged tiles, against a float32 torch evaluation of the same layer for batch 0 (the
-    batches are independent)."""
-    import bench
-
-    args = bench.block_inputs(torch, torch.device(DEV))
-    f = tj.jit(bench._fn_block)
-    out = f(*args)
-    assert f.compiled(*args).num_kernels == 9
+def _config5_batch0_fp32(args):
+    """Config 5's layer evaluated in float32 by torch for batch 0."""
     x, g1, wq, wk, wv, wo, g2, w1, w2 = [a.float() for a in args]
     x = x[:1]
     S, D, H = x.shape[1], x.shape[2], 32
@@ -1168,8 +1188,47 @@ def test_config5_block_full_size_batch0_vs_fp32():
     pr = torch.softmax(q @ k.transpose(-1, -2).contiguous() * (D // H) ** -0.5, dim=-1)
     o = (pr @ v).transpose(1, 2).reshape(1, S, D)
     x = x + o @ wo.t().contiguous()
-    ref = x + F.gelu(rms(x, g2) @ w1.t().contiguous()) @ w2.t().contiguous()
-    close_lowp(out[:1], ref, tol=3e-2)
+    return x + F.gelu(rms(x, g2) @ w1.t().contiguous()) @ w2.t().contiguous()
+
+
+def test_config5_block_full_size_batch0_vs_fp32():
+    """Config 5's layer at its full shape ([4, 2048, 4096], 32 heads x 128, MLP 11008, bf16) on
+    the packaged tiles, against a float32 torch evaluation of the same layer for batch 0 (the
+    batches are independent).  Norm bound 1e-2: the layer stores bf16 between its 9 kernels
+    (q, k, v, attention output, residual stream, normed activations, gelu output), each a
+    rounding of ~1.7e-3 RMS relative that later kernels carry forward."""
+    import bench
+
+    args = bench.block_inputs(torch, torch.device(DEV))
+    f = tj.jit(bench._fn_block)
+    out = f(*args)
+    assert f.compiled(*args).num_kernels == 9
+    close_lowp(out[:1], _config5_batch0_fp32(args), tol=3e-2, norm=1e-2)
+
+
+def test_config5_block_full_size_under_graph_replay(monkeypatch):
+    """Config 5's layer at full size as the bench times it under ``TENSORJIT_HIP_GRAPH=1``:
+    two hipGraph replays (eager work between them) bit-identical to direct launches of the
+    same program, and batch 0 against the float32 evaluation."""
+    import bench
+
+    monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "1")
+    args = bench.block_inputs(torch, torch.device(DEV))
+    f = tj.jit(bench._fn_block)
+    cp = f.compiled(*args)
+    assert cp.use_graph and cp.num_kernels == 9
+    cp.use_graph = False
+    direct = cp(*args)[0].clone()
+    cp.use_graph = True
+    replays = []
+    for _ in range(2):
+        replays.append(cp(*args)[0].clone())
+        torch.cuda.synchronize()
+        _ = (args[0] * 2).sum().item()          # eager work between replays
+    assert cp.stats["graph_replays"] >= 2
+    for r in replays:
+        assert torch.equal(r, direct)
+    close_lowp(replays[-1][:1], _config5_batch0_fp32(args), tol=3e-2, norm=1e-2)
 
 
 def test_config5_block_with_fused_attention_vs_oracle():
@@ -1485,8 +1544,10 @@ def test_k_split_gemm_matches_reference(case):
         first = None
         for _ in range(2):
             out = _run_with_config(fn, args, cfg).float()
-            err = float(((out - ref).abs() - tol * ref.abs()).max() / ref.abs().max())
-            assert err < tol, (case, vals, err)
+            if tol == 1e-5:
+                close_f32(out, ref, what=f"{case} {vals}")
+            else:
+                close_lowp(out, ref, tol=tol, what=f"{case} {vals}")
             if first is None:
                 first = out
             else:
@@ -1547,8 +1608,7 @@ def test_direct_lds_gemm_matches_reference(case, dtype):
         assert hb.config_ok(cfg, hb.compute_dtype(mm), mm), (case, cfg)
         for _ in range(2):      # twice: a race between loads and reads shows as run-to-run differences
             out = _run_with_config(fn, args, cfg).float()
-            err = float((out - ref).abs().max() / ref.abs().max())
-            assert err < 2e-2, (case, dtype, cfg, err)
+            close_lowp(out, ref, what=f"{case} {dtype} {cfg}")
 
 
 def C_lower(fn, *args):
@@ -1612,8 +1672,7 @@ def test_persistent_direct_gemm_matches_the_direct_kernel(case):
         got = _run_with_config(fn, args, pers)
         assert torch.equal(got, want), case
     # both round the exact fp32 sums to 16 bits once: within half an ulp of the reference
-    err = float((want.float() - ref).abs().max() / ref.abs().max())
-    assert err < 2e-2, (case, err)
+    close_lowp(want.float(), ref, what=case)
 
 
 def hb_config_ok(cfg, mm):

@@ -3,8 +3,9 @@
 Same kernels, same launch order, intermediates in the library's static per-GPU
 arena instead of the program's own: outputs must equal tj_hip_program_run's bit for
 bit, on two calls in a row with the second program smaller than the first (the
-static arena then still holds the first call's larger contents), and a program whose
-arena exceeds the static one is refused before any launch.
+static arena then still holds the first call's larger contents), a fresh program's
+first call issued under stream capture, and a program whose arena exceeds the static
+one is refused before any launch.
 """
 import pytest
 import torch
@@ -60,6 +61,30 @@ def test_static_arena_run_matches_the_allocating_run():
         for r, o in zip(ref, got):
             assert torch.equal(r, o)
         torch.testing.assert_close(got[0], cp(*args)[0], atol=0, rtol=0)
+
+
+def test_first_static_run_of_a_fresh_program_under_stream_capture():
+    """tj_hip_program_create looks the static arena up, so a fresh program's very first
+    tj_hip_program_run_static may be issued under stream capture (torch.cuda.graph):
+    every replay of that graph, with eager work in between, equals tj_hip_program_run's
+    output bit for bit."""
+    cp = tj.jit(_mlp).compiled(*_inputs(256, seed=6))
+    args = _inputs(256, seed=6)
+    assert cp.native.stats()["calls"] == 0 and 0 < cp.arena_bytes <= rt.STATIC_ARENA_BYTES
+    ip = [a.data_ptr() for a in args]
+    got = [torch.empty(s, dtype=d, device=DEV) for s, d in cp._out_specs]
+    want = [torch.empty(s, dtype=d, device=DEV) for s, d in cp._out_specs]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cp.native.run_static(ip, [t.data_ptr() for t in got], torch.cuda.current_stream().cuda_stream)
+    cp.native.run(ip, [t.data_ptr() for t in want], torch.cuda.current_stream().cuda_stream)
+    for _ in range(3):
+        for t in got:
+            t.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(got, want))
+        _ = (args[0] * 2).sum().item()          # eager work between replays
 
 
 def test_static_arena_run_of_key_split_attention():
