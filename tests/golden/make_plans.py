@@ -5,11 +5,13 @@ benchmark workloads.
 
 It imports the reference's ``tensorjit`` (pure Python: tracer, cleanup passes,
 ``fuse``/``row_fuse``, ``plan_memory``; nothing is compiled or run on a device), traces
-each workload of ``plan_cases.CASES`` with it, lowers it for the reference's ``cuda``
-backend (row-fusion limit 8192, the same as ``hip``) and records the result through
-``plan_cases.describe``.  The tests compare this repository's plans with the file; they
-never import the reference.  Run in the build container only (the reference is not on
-the GPU box).
+each workload of ``plan_cases.CASES`` and ``plan_cases.DIVERGENT`` with it, lowers it with
+the reference's own ``fuse(optimize(graph))`` and ``row_fuse`` at the hip backend's
+row-fusion limit (``plan_cases.ROW_FUSION_MAX_N``, 32768; the reference's cuda backend
+uses 8192, which gives the same plans for rows of at most 8192 elements) and records the
+result through ``plan_cases.describe``.  The tests compare this repository's plans with
+the file; they never import the reference.  Run in the build container only (the
+reference is not on the GPU box).
 """
 from __future__ import annotations
 
@@ -30,7 +32,7 @@ def main(ref_root: str) -> None:
     if not Path(tj.__file__).resolve().is_relative_to(ref):
         raise SystemExit(f"imported {tj.__file__}, not the reference under {ref}")
     from tensorjit import ir
-    from tensorjit.compiler import lower
+    from tensorjit.passes import fuse, optimize, row_fuse
     from tensorjit.passes.memory_planner import plan_memory
 
     # bench.py's workload functions run `import tensorjit` when called: the module
@@ -40,22 +42,31 @@ def main(ref_root: str) -> None:
     import bench
     import plan_cases
 
+    def lower(graph):
+        # the reference's lower() (reference tensorjit/compiler.py:37-42) at the hip limit
+        program = fuse(optimize(graph))
+        if os.environ.get("TENSORJIT_NO_ROW_FUSION") != "1":
+            program = row_fuse(program, max_n=plan_cases.ROW_FUSION_MAX_N)
+        return program
+
     out = {"generator": "tests/golden/make_plans.py", "reference_backend": plan_cases.REFERENCE_BACKEND,
-           "cases": {}}
-    for name, fn_name, args, env in plan_cases.CASES:
+           "row_fusion_max_n": plan_cases.ROW_FUSION_MAX_N, "cases": {}, "divergent": {}}
+    cases = [(c, "cases", getattr(bench, c[1])) for c in plan_cases.CASES]
+    cases += [((name, fn_name, args, {}), "divergent", getattr(plan_cases, fn_name))
+              for name, fn_name, args, _, _ in plan_cases.DIVERGENT]
+    for (name, _, args, env), where, fn in cases:
         saved = {k: os.environ.get(k) for k in env}
         os.environ.update(env)
         try:
-            program = lower(plan_cases.trace_case(tj, ir, getattr(bench, fn_name), args),
-                            plan_cases.REFERENCE_BACKEND)
-            out["cases"][name] = plan_cases.describe(program, plan_memory(program))
+            program = lower(plan_cases.trace_case(tj, ir, fn, args))
+            out[where][name] = plan_cases.describe(program, plan_memory(program))
         finally:
             for k, v in saved.items():
                 if v is None:
                     os.environ.pop(k, None)
                 else:
                     os.environ[k] = v
-        print(f"{name}: {len(program.kernels)} kernels, arena {out['cases'][name]['memory']['arena_bytes']} B")
+        print(f"{name}: {len(program.kernels)} kernels, arena {out[where][name]['memory']['arena_bytes']} B")
     (HERE / "plans.json").write_text(json.dumps(out, separators=(",", ":"), sort_keys=True) + "\n")
 
 

@@ -33,12 +33,49 @@ CASES = [
                                     ((4096, 4096), "bf16"), ((4096, 4096), "bf16"), ((4096, 4096), "bf16"),
                                     ((4096,), "bf16"), ((11008, 4096), "bf16"), ((4096, 11008), "bf16")], {}),
     ("overhead_chain_f32", "_fn_chain", [((16, 32), "f32"), ((32, 32), "f32")], {}),
+    # rows past the reference's GPU row-fusion limit (8192) and up to the hip limit:
+    # one row kernel each, the odd lengths on scalar lanes; 32769 is one past the limit
+    # (the norms then plan as reductions and pointwise kernels)
+    ("ln_bf16_512x16384", "_fn_ln", [((512, 16384), "bf16"), ((16384,), "bf16")], {}),
+    ("ln_f32_256x32768", "_fn_ln", [((256, 32768), "f32"), ((32768,), "f32")], {}),
+    ("ln_f32_1024x12000", "_fn_ln", [((1024, 12000), "f32"), ((12000,), "f32")], {}),
+    ("ln_f32_64x32769", "_fn_ln", [((64, 32769), "f32"), ((32769,), "f32")], {}),
+    ("rms_bf16_512x16384", "_fn_rms", [((512, 16384), "bf16"), ((16384,), "bf16")], {}),
+    ("rms_f32_256x32768", "_fn_rms", [((256, 32768), "f32"), ((32768,), "f32")], {}),
+    ("rms_bf16_1024x12001", "_fn_rms", [((1024, 12001), "bf16"), ((12001,), "bf16")], {}),
+    ("softmax_f32_512x16384", "_fn_softmax", [((512, 16384), "f32")], {}),
+    ("softmax_bf16_256x32768", "_fn_softmax", [((256, 32768), "bf16")], {}),
+    ("softmax_f32_1024x12000", "_fn_softmax", [((1024, 12000), "f32")], {}),
+    ("softmax_f32_64x32769", "_fn_softmax", [((64, 32769), "f32")], {}),
 ]
 
-# the reference's cuda backend and this repository's hip backend share the row-fusion
-# limit (8192), so their plans are the same function of the graph
+# Every case is lowered by the reference's own passes -- ``fuse(optimize(graph))`` and then
+# ``row_fuse(program, max_n=ROW_FUSION_MAX_N)`` -- with the hip backend's row-fusion limit.
+# The reference's cuda backend passes 8192 (reference tensorjit/compiler.py:34); below
+# 8193 elements per row the two limits give the same plan.
+ROW_FUSION_MAX_N = 32768
 REFERENCE_BACKEND = "cuda"
 BACKEND = "hip"
+
+
+def _fn_column_centre(x, g):
+    """A no-keepdim mean over axis 0 (one value per column) read along the rows of a
+    square x: the reference's row fusion applies it per row."""
+    import tensorjit as tj
+
+    return x - tj.mean(x, axis=0) * g
+
+
+# Cases where this repository's plan departs from the reference's on purpose: the
+# reference's row_fuse (reference tensorjit/passes/fusion.py:279-295) joins kernels by
+# their (rows, N) shapes only, so over a square x the column value above lands in a row
+# kernel that holds one value per row; the hip plan keeps that pair as a reduction and a
+# pointwise kernel.  (case, function in this module, [(shape, dtype)], reference kernel
+# kinds, hip kernel kinds)
+DIVERGENT = [
+    ("column_centre_f32_64x64", "_fn_column_centre", [((64, 64), "f32"), ((64,), "f32")],
+     ["copy", "row"], ["copy", "reduce", "elementwise"]),
+]
 
 
 def _attr(v):
