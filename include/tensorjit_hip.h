@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TJ_HIP_ABI_VERSION 2
+#define TJ_HIP_ABI_VERSION 3
 
 /* Where a kernel argument points: caller input i, arena + offset, caller output j. */
 enum { TJ_ARG_INPUT = 0, TJ_ARG_ARENA = 1, TJ_ARG_OUTPUT = 2 };
@@ -61,10 +61,11 @@ typedef struct tj_launch {
 } tj_launch;
 
 typedef struct tj_stats {
-  uint64_t calls;          /* run + replay calls */
+  uint64_t calls;            /* run + replay calls */
   uint64_t graph_replays;
   uint64_t graph_captures;
-  uint64_t host_ns;        /* host time spent inside run/replay (launch overhead) */
+  uint64_t host_ns;          /* host time spent inside run/replay (launch overhead) */
+  uint64_t direct_fallbacks; /* replay calls that launched directly (pointer sets not recurring) */
 } tj_stats;
 
 typedef struct tj_device_info {
@@ -110,9 +111,11 @@ int tj_hip_program_run(void* handle, const void* const* inputs, void* const* out
  * serving loops, harnesses that forbid hipMalloc).  The program's intermediates and
  * split-K partials go to a static device array of TJ_HIP_STATIC_ARENA_BYTES per GPU
  * instead of the program's own arena; a program whose arena is larger is rejected
- * with an error.  The call allocates nothing (the first call on a device looks the
- * array's address up once).  Every call on one GPU shares that array, which keeps the
- * last call's contents: calls that overlap on one GPU (two streams, two threads) race.
+ * with an error.  The call allocates nothing: tj_hip_program_create looks the
+ * array's address up (once per device), so even a program's first call may be
+ * issued under stream capture.  Every call on one GPU shares that array, which keeps
+ * the last call's contents: calls that overlap on one GPU (two streams, two threads)
+ * race.
  * Nothing in it needs clearing -- every call writes each intermediate before reading it. */
 #define TJ_HIP_STATIC_ARENA_BYTES ((size_t)64 << 20)
 int tj_hip_program_run_static(void* handle, const void* const* inputs, void* const* outputs, void* stream);
@@ -122,7 +125,10 @@ int tj_hip_program_run_static(void* handle, const void* const* inputs, void* con
 int tj_hip_program_capture(void* handle, const void* const* inputs, void* const* outputs);
 
 /* Replay the graph captured for this pointer set on `stream`, capturing it first if
- * this pointer set has not been seen. */
+ * this pointer set has not been seen.  After 4 captures in a row with no replay of a
+ * cached exec (the caller keeps its outputs or passes fresh inputs), a pointer set is
+ * captured on its second sighting only; calls in between launch the kernels directly
+ * (counted in direct_fallbacks), so captures stay bounded. */
 int tj_hip_program_replay(void* handle, const void* const* inputs, void* const* outputs, void* stream);
 
 int tj_hip_program_stats(void* handle, tj_stats* out);

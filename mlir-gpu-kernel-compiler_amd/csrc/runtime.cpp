@@ -10,7 +10,11 @@
 // single hipMalloc owned by the program and reused by every call.  A call
 // can instead replay a hipGraph exec captured for its exact pointer set;
 // execs are cached per pointer set, so alternating output buffers (the
-// caller's pool) replay without re-capture.
+// caller's pool) replay without re-capture.  A caller whose pointer sets do
+// not recur (it keeps every output, or passes fresh inputs) would pay a
+// capture and an instantiation per call: after kMissLimit captures in a row
+// with no replay of a cached exec, a pointer set is captured only on its
+// second sighting, and calls in between launch directly.
 //
 // Design follows the reference's pybind11 executor (csrc/runtime.cpp:31-129:
 // pre-resolved INPUT/ARENA/OUTPUT references, one call per program, bounds
@@ -60,6 +64,8 @@ int hip_fail(hipError_t e, const char* what) {
 
 constexpr int kMaxArgs = 64;
 constexpr size_t kMaxGraphs = 8;
+constexpr int kMissLimit = 4;        // captures in a row before pointer sets must recur
+constexpr size_t kMaxSightings = 8;  // pointer sets seen once since then, most recent first
 
 struct KernelRec {
   hipFunction_t fn = nullptr;
@@ -102,6 +108,12 @@ struct Program {
   int n_in = 0, n_out = 0;
   hipStream_t capture_stream = nullptr;
   std::list<GraphRec> graphs;  // most recently used first
+  int miss_streak = 0;         // captures since the last replay of a cached exec
+  std::list<std::vector<const void*>> sightings;
+  // device address of the static arena for tj_hip_program_run_static, looked up at
+  // creation (null when the arena does not fit it or the lookup failed: static_error)
+  char* static_base = nullptr;
+  std::string static_error;
   tj_stats stats{};
 
   ~Program() {
@@ -163,11 +175,32 @@ struct Program {
     return nullptr;
   }
 
-  int capture(const void* const* in, void* const* out, GraphRec** rec_out) {
+  // True when `key` was seen once before (and forgets it); otherwise remembers it.
+  bool seen_before(const std::vector<const void*>& key) {
+    for (auto it = sightings.begin(); it != sightings.end(); ++it) {
+      if (*it == key) {
+        sightings.erase(it);
+        return true;
+      }
+    }
+    sightings.push_front(key);
+    if (sightings.size() > kMaxSightings) sightings.pop_back();
+    return false;
+  }
+
+  // The exec for this pointer set, captured now if needed; *rec_out stays null when the
+  // miss policy says to launch directly instead (only when `may_skip`).
+  int capture(const void* const* in, void* const* out, GraphRec** rec_out, bool may_skip = false) {
+    *rec_out = nullptr;
     std::vector<const void*> key = key_of(in, out);
     if (GraphRec* hit = find(key)) {
+      miss_streak = 0;
       *rec_out = hit;
       return 0;
+    }
+    if (may_skip) {
+      if (miss_streak >= kMissLimit && !seen_before(key)) return 0;
+      miss_streak++;
     }
     if (!capture_stream) TJ_HIP(hipStreamCreateWithFlags(&capture_stream, hipStreamNonBlocking));
     bind(in, out, arena);
@@ -206,7 +239,7 @@ std::mutex g_static_mu;
 std::atomic<char*> g_static_arena[kMaxDevices];
 
 // Device address of `scratch` on `device`, which must be the current device; looked up
-// with hipGetSymbolAddress on the first call for that device and kept.
+// with hipGetSymbolAddress the first time a program is created on that device, and kept.
 int static_arena(int device, char** out) {
   if (device < 0 || device >= kMaxDevices) return fail("static arena: device index out of range");
   char* ptr = g_static_arena[device].load(std::memory_order_acquire);
@@ -369,6 +402,17 @@ int tj_hip_program_create(int device, const void* code, size_t code_size, int nk
     TJ_HIP(hipMalloc(&a, arena_bytes));
     p->arena = static_cast<char*>(a);
   }
+  // tj_hip_program_run_static's arena: looked up here, where loading and allocating are
+  // expected, so that entry point never makes the runtime load or place anything.  A
+  // failed lookup leaves the program usable through the other entry points.
+  if (arena_bytes && arena_bytes <= TJ_HIP_STATIC_ARENA_BYTES) {
+    const std::string saved = g_error;
+    if (static_arena(device, &p->static_base) != 0) {
+      p->static_error = g_error;
+      p->static_base = nullptr;
+      g_error = saved;
+    }
+  }
   *handle = p.release();
   return 0;
 }
@@ -395,14 +439,12 @@ int tj_hip_program_run_static(void* handle, const void* const* inputs, void* con
     return fail("tj_hip_program_run_static: the program's intermediates need " + std::to_string(p->arena_bytes) +
                 " bytes, more than the " + std::to_string(static_cast<size_t>(TJ_HIP_STATIC_ARENA_BYTES)) +
                 "-byte static arena (use tj_hip_program_run)");
+  if (p->arena_bytes && !p->static_base)
+    return fail("tj_hip_program_run_static: no static arena on device " + std::to_string(p->device) + ": " +
+                p->static_error);
   const uint64_t t0 = now_ns();
   DeviceScope scope(p->device);
-  char* base = nullptr;
-  if (p->arena_bytes) {
-    int rc = static_arena(p->device, &base);
-    if (rc) return rc;
-  }
-  p->bind(inputs, outputs, base);
+  p->bind(inputs, outputs, p->static_base);
   int rc = p->launch_all(static_cast<hipStream_t>(stream));
   if (rc) return rc;
   p->stats.calls++;
@@ -426,11 +468,18 @@ int tj_hip_program_replay(void* handle, const void* const* inputs, void* const* 
   const uint64_t t0 = now_ns();
   DeviceScope scope(p->device);
   GraphRec* rec = nullptr;
-  int rc = p->capture(inputs, outputs, &rec);
+  int rc = p->capture(inputs, outputs, &rec, /*may_skip=*/true);
   if (rc) return rc;
-  TJ_HIP(hipGraphLaunch(rec->exec, static_cast<hipStream_t>(stream)));
+  if (rec) {
+    TJ_HIP(hipGraphLaunch(rec->exec, static_cast<hipStream_t>(stream)));
+    p->stats.graph_replays++;
+  } else {
+    p->bind(inputs, outputs, p->arena);
+    rc = p->launch_all(static_cast<hipStream_t>(stream));
+    if (rc) return rc;
+    p->stats.direct_fallbacks++;
+  }
   p->stats.calls++;
-  p->stats.graph_replays++;
   p->stats.host_ns += now_ns() - t0;
   return 0;
 }

@@ -487,7 +487,7 @@ class HipProgram:
         if use_graph is None:
             use_graph = env == "1" if env in ("0", "1") else len(self.launches) >= GRAPH_MIN_LAUNCHES
         self.use_graph = use_graph
-        self.stats = {"calls": 0, "graph_replays": 0}
+        self._calls = 0
 
     # -- construction helpers -------------------------------------------------------
     def _ref(self, n: Node) -> tuple[int, ...]:
@@ -555,6 +555,15 @@ class HipProgram:
 
     # -- protocol ---------------------------------------------------------------
     @property
+    def stats(self) -> dict:
+        """Calls, and of the graph-mode calls: hipGraph replays, captures, and calls that
+        launched directly because their pointer sets did not recur (the native runtime's
+        counters; the reference's ``CudaProgram.stats`` has the first two)."""
+        n = self._native.stats() if self._native is not None else {}
+        return {"calls": self._calls, "graph_replays": n.get("graph_replays", 0),
+                "graph_captures": n.get("graph_captures", 0), "direct_fallbacks": n.get("direct_fallbacks", 0)}
+
+    @property
     def num_kernels(self) -> int:
         """Fused kernels of the plan (a split-K GEMM is one kernel with two launches)."""
         return len(self.program.kernels)
@@ -609,11 +618,10 @@ class HipProgram:
         take, dev = self.pool.take_output, self._dev
         outs = [take(shape, dtype, dev) for shape, dtype in self._out_specs]
         stream = _current_stream(self.device_index)
-        self.stats["calls"] += 1
+        self._calls += 1
         if self.launches:
             if self.use_graph:
                 self._native.replay_tensors(ins, outs, stream)
-                self.stats["graph_replays"] += 1
             else:
                 self._native.run_tensors(ins, outs, stream)
         return self._results(ins, outs)

@@ -14,7 +14,7 @@ from typing import Sequence
 
 LIB_NAME = "libtjhip.so"
 LIB_PATH = Path(__file__).resolve().parents[1] / LIB_NAME
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 INPUT, ARENA, OUTPUT = 0, 1, 2
 STATIC_ARENA_BYTES = 64 << 20   # TJ_HIP_STATIC_ARENA_BYTES
@@ -36,7 +36,8 @@ class LaunchDesc(ctypes.Structure):
 
 class Stats(ctypes.Structure):
     _fields_ = [("calls", ctypes.c_uint64), ("graph_replays", ctypes.c_uint64),
-                ("graph_captures", ctypes.c_uint64), ("host_ns", ctypes.c_uint64)]
+                ("graph_captures", ctypes.c_uint64), ("host_ns", ctypes.c_uint64),
+                ("direct_fallbacks", ctypes.c_uint64)]
 
 
 class DeviceInfo(ctypes.Structure):
@@ -211,7 +212,7 @@ class NativeHipProgram:
         s = Stats()
         check(self._lib.tj_hip_program_stats(self.handle, ctypes.byref(s)), "tj_hip_program_stats")
         return {"calls": s.calls, "graph_replays": s.graph_replays, "graph_captures": s.graph_captures,
-                "host_us": s.host_ns / 1e3}
+                "direct_fallbacks": s.direct_fallbacks, "host_us": s.host_ns / 1e3}
 
     def arena(self) -> tuple[int, int]:
         p, n = ctypes.c_void_p(), ctypes.c_size_t()
