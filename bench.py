@@ -20,6 +20,7 @@ BASELINE.json configurations (row kernels, GEMMs, MLP block per-call time).
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -173,6 +174,92 @@ def overhead_chain(torch, dev) -> dict:
     return res
 
 
+def _ref_workloads():
+    """The reference's GPU benchmark workloads (reference benchmarks/bench.py:20-52): name ->
+    (tensorjit function, eager PyTorch function, shapes at sequence length T and hidden D)."""
+    import torch
+    import torch.nn.functional as F
+
+    import tensorjit as tj
+
+    return {
+        "bias_gelu": (lambda x, b: tj.gelu(x + b), lambda x, b: F.gelu(x + b),
+                      lambda T, D: [(T, 4 * D), (4 * D,)]),
+        # the reference times softmax over [8, min(T, 2048), min(T, 2048)] (its bench.py:97-98)
+        "softmax": (lambda t: tj.softmax(t), lambda t: torch.softmax(t, -1),
+                    lambda T, D: [(8, min(T, 2048), min(T, 2048))]),
+        "layernorm": (lambda x, g, b: tj.layer_norm(x, g, b), lambda x, g, b: F.layer_norm(x, (x.shape[-1],), g, b),
+                      lambda T, D: [(T, D), (D,), (D,)]),
+        "rmsnorm": (lambda x, g: tj.rms_norm(x, g),
+                    lambda x, g: x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * g,
+                    lambda T, D: [(T, D), (D,)]),
+        "linear_gelu": (lambda x, w, b: tj.gelu(tj.linear(x, w, b)), lambda x, w, b: F.gelu(F.linear(x, w, b)),
+                        lambda T, D: [(T, D), (4 * D, D), (4 * D,)]),
+        "mlp_block": (lambda x, g, w1, b1, w2, b2: x + tj.linear(tj.gelu(tj.linear(tj.layer_norm(x, g), w1, b1)), w2, b2),
+                      lambda x, g, w1, b1, w2, b2: x + F.linear(F.gelu(F.linear(F.layer_norm(x, (x.shape[-1],), g),
+                                                                               w1, b1)), w2, b2),
+                      lambda T, D: [(T, D), (D,), (4 * D, D), (4 * D,), (D, 4 * D), (D,)]),
+    }
+
+
+def reference_gpu_table(torch, dev, seqs=(256, 1024, 4096), hidden=1024) -> dict:
+    """The reference's GPU comparison (reference benchmarks/bench.py:55-70, README.md:188-193)
+    for the hip backend: each workload at hidden 1024 and seq 256 / 1024 / 4096, in fp32 and
+    bf16, timed the reference's way (hipEvents on the current stream around 50 calls after 10
+    warmup calls) for eager PyTorch-ROCm, hip with direct launches and hip with hipGraph
+    replay of the same compiled program.  Inputs are plain ``torch.randn`` as in the
+    reference.  GEMM tiles come from the packaged table or the CDNA4 cost model (no
+    on-device tuning inside the benchmark).  torch.compile (inductor) is not timed: it
+    would generate Triton kernels at run time.  ``max_abs_err`` is the reference's check,
+    hip against eager."""
+
+    def timeit(fn, iters=50, warmup=10):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / iters
+
+    import tensorjit as tj
+
+    saved = os.environ.get("TENSORJIT_NO_AUTOTUNE")
+    os.environ["TENSORJIT_NO_AUTOTUNE"] = "1"
+    rows = []
+    for dtname, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+        for name, (tj_fn, torch_fn, shapes) in _ref_workloads().items():
+            for T in seqs:
+                g = torch.Generator(device=dev).manual_seed(T)
+                args = [torch.randn(*sh, device=dev, generator=g).to(dt) for sh in shapes(T, hidden)]
+                jf = tj.jit(tj_fn)
+                out = jf(*args)
+                cp = jf.compiled(*args)
+                err = float((out.float() - torch_fn(*args).float()).abs().max())
+                t_eager = timeit(lambda: torch_fn(*args))
+                cp.use_graph = False
+                t_direct = timeit(lambda: jf(*args))
+                cp.use_graph = True
+                t_graph = timeit(lambda: jf(*args))
+                cp.use_graph = len(cp.launches) >= 12
+                rows.append({"workload": name, "seq": T, "dtype": dtname, "eager_ms": round(t_eager, 4),
+                             "hip_ms": round(t_direct, 4), "hip_graph_ms": round(t_graph, 4),
+                             "speedup_vs_eager": round(t_eager / min(t_direct, t_graph), 2),
+                             "kernels": cp.num_kernels, "launches": len(cp.launches), "max_abs_err": float(f"{err:.3g}")})
+                del args, out, jf, cp
+    if saved is None:
+        os.environ.pop("TENSORJIT_NO_AUTOTUNE", None)
+    else:
+        os.environ["TENSORJIT_NO_AUTOTUNE"] = saved
+    readme = {f"{r['workload']} T={r['seq']} {r['dtype']}": {k: r[k] for k in ("eager_ms", "hip_ms", "hip_graph_ms")}
+              for r in rows if (r["workload"], r["seq"]) in (("mlp_block", 4096), ("softmax", 4096))}
+    return {"hidden": hidden, "timing": "hipEvents, warmup 10, iters 50 (reference benchmarks/bench.py:55-70)",
+            "inductor": None, "rows": rows, "readme_rows": readme}
+
+
 def block_inputs(torch, dev, B=4, S=2048, D=4096, F=11008, dt=None):
     dt = dt or torch.bfloat16
     g = torch.Generator(device=dev).manual_seed(0)
@@ -245,15 +332,26 @@ def kernel_ms_settled(cp, args, k=None, rounds=3, iters=10, settle_s=0.5):
     return total
 
 
-def load_traffic(workload: str):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+def source_sha16(cp) -> str:
+    """Digest of a compiled program's HIP source: names the exact kernels a profile measured."""
+    return hashlib.sha256(cp.source.encode()).hexdigest()[:16]
+
+
+def load_traffic(workload: str, sha16: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, when it was taken
+    of this very kernel source (the summary records each program's source digest);
+    otherwise (None, why)."""
     p = ROOT / "profiles" / "hbm_traffic.json"
     try:
         data = json.loads(p.read_text())
     except (OSError, ValueError):
-        return None
+        return None, "no PMC summary"
     entry = data.get(workload)
-    return None if entry is None else entry.get("traffic_bytes")
+    if entry is None:
+        return None, "workload not in the PMC summary"
+    if entry.get("source_sha16") != sha16:
+        return None, f"PMC summary is of source {entry.get('source_sha16')}, this kernel is {sha16}"
+    return entry.get("traffic_bytes"), None
 
 
 def host_cpus() -> dict:
@@ -448,16 +546,23 @@ def secondary(torch, dev, quick):
     os.environ.pop("TENSORJIT_HIP_GRAPH", None)
     cp = f.compiled(*bargs)
     flops = 2851.9e9
+    # per-kernel device time inside calls of the whole layer (hipEvents between its
+    # launches; the median call of 7 by total), and each kernel repeated alone
+    incall = [cp.kernel_times_in_call_ms(*bargs) for _ in range(7)]
+    mid = sorted(incall, key=sum)[len(incall) // 2]
     kernels = []
     for i, l in enumerate(cp.launches):
         kus = kernel_ms_settled(cp, bargs, i, rounds=2, iters=5) * 1e3
-        entry = {"kernel": l.name, "us": round(kus, 1)}
+        entry = {"kernel": l.name, "us_in_call": round(mid[i] * 1e3, 1), "us_alone": round(kus, 1)}
         if "flops" in l.meta:
-            entry["TFLOP/s"] = round(l.meta["flops"] / kus / 1e6, 1)
+            entry["TFLOP/s_in_call"] = round(l.meta["flops"] / (mid[i] * 1e3) / 1e6, 1)
+            entry["TFLOP/s_alone"] = round(l.meta["flops"] / kus / 1e6, 1)
         kernels.append(entry)
     best = min(res.values())
     out["c5_block_bf16"] = {**res, "TFLOP/s": round(flops / best / 1e6, 1), "frac_peak": round(flops / best / 1e6 / BF16_PEAK_TFLOPS, 4),
                             "kernels": len(cp.launches), "arena_MiB": round(cp.plan.arena_bytes / 2**20, 1),
+                            "sum_in_call_us": round(sum(mid) * 1e3, 1),
+                            "sum_alone_us": round(sum(k["us_alone"] for k in kernels), 1),
                             "per_kernel": kernels}
     log(f"c5_block: {out['c5_block_bf16']}")
     del bargs, f, cp
@@ -483,6 +588,8 @@ def secondary(torch, dev, quick):
     log(f"c5_attention: {res}")
     out["mfma_sustained_bf16"] = mfma_sustained(torch)
     log(f"mfma_sustained: {out['mfma_sustained_bf16']}")
+    out["reference_gpu_table"] = reference_gpu_table(torch, dev)
+    log(f"reference GPU table: {out['reference_gpu_table']['readme_rows']}")
     return out
 
 
@@ -569,58 +676,58 @@ def mfma_sustained(torch) -> dict:
     return res
 
 
-def profile_set(torch, dev, steps) -> None:
-    """Kernels for rocprofv3 counter runs: the headline kernel, a plain copy-like
+def profile_set(torch, dev, steps, which="all") -> None:
+    """Kernels for rocprofv3 runs.  ``all``: the headline kernel, a plain copy-like
     calibration kernel of known traffic (y = x + 0.5, fp32 [16384,4096]: 256 MiB
     read + 256 MiB written), the row configs, the config-4 bf16 GEMM and its decode
-    shape, config 5's bf16 softmax rows and fused attention, ``steps`` launches each."""
+    shape, config 5's bf16 softmax rows and fused attention, ``steps`` launches each.
+    ``c5``: ``steps`` calls of config 5's whole layer (direct launches), for a kernel
+    trace of the layer in its own context.  Each program's source digest is logged, so
+    a counter summary names the kernel source it measured."""
     import tensorjit as tj
 
+    def run(fn, fargs):
+        jf = tj.jit(fn)
+        for _ in range(steps):
+            jf(*fargs)
+        cp = jf.compiled(*fargs)
+        log("profile_source " + json.dumps({"launches": [l.name for l in cp.launches], "sha16": source_sha16(cp)}))
+
+    if which == "c5":
+        os.environ["TENSORJIT_HIP_GRAPH"] = "0"
+        run(_fn_block, block_inputs(torch, dev))
+        torch.cuda.synchronize()
+        log(f"profile set c5 done ({steps} calls)")
+        return
     args = c2_inputs(torch, torch.float32, dev)
-    f = tj.jit(_fn_c2)
-    for _ in range(steps):
-        f(*args)
+    run(_fn_c2, args)
     x = args[0]
-    cal = tj.jit(lambda t: t + 0.5)
-    for _ in range(steps):
-        cal(x)
+    run(lambda t: t + 0.5, [x])
     del args, x
     gen = torch.Generator(device=dev).manual_seed(0)
     xb = torch.randn(65536, 4096, device=dev, generator=gen).bfloat16()
     gb = (1 + 0.1 * torch.randn(4096, device=dev, generator=gen)).bfloat16()
     for fn, fargs in ((_fn_ln, [xb, gb]), (_fn_rms, [xb, gb])):
-        jf = tj.jit(fn)
-        for _ in range(steps):
-            jf(*fargs)
+        run(fn, fargs)
     del xb
     s = torch.randn(65536, 2048, device=dev, generator=gen) * 3
-    jf = tj.jit(_fn_softmax)
-    for _ in range(steps):
-        jf(s)
+    run(_fn_softmax, [s])
     del s
     xg = torch.randn(8192, 8192, device=dev, generator=gen).bfloat16()
     wg = (0.02 * torch.randn(8192, 8192, device=dev, generator=gen)).bfloat16()
     bg = (0.02 * torch.randn(8192, device=dev, generator=gen)).bfloat16()
-    jf = tj.jit(_fn_gemm)
-    for _ in range(steps):
-        jf(xg, wg, bg)
+    run(_fn_gemm, [xg, wg, bg])
     del xg, wg, bg
     xs = torch.randn(16, 8192, device=dev, generator=gen).bfloat16()
     ws = (0.02 * torch.randn(8192, 8192, device=dev, generator=gen)).bfloat16()
     bs = (0.02 * torch.randn(8192, device=dev, generator=gen)).bfloat16()
-    jf = tj.jit(_fn_gemm)
-    for _ in range(steps):
-        jf(xs, ws, bs)
+    run(_fn_gemm, [xs, ws, bs])
     del xs, ws, bs
     s5 = (torch.randn(262144, 2048, device=dev, generator=gen) * 3).bfloat16()
-    jf = tj.jit(_fn_softmax)
-    for _ in range(steps):
-        jf(s5)
+    run(_fn_softmax, [s5])
     del s5
     qkv = [torch.randn(4, 32, 2048, 128, device=dev, generator=gen).bfloat16() for _ in range(3)]
-    jf = tj.jit(_fn_attn)
-    for _ in range(steps):
-        jf(*qkv)
+    run(_fn_attn, qkv)
     torch.cuda.synchronize()
     log(f"profile set done ({steps} launches per kernel)")
 
@@ -634,8 +741,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--quick", action="store_true", help="skip the GEMM / MLP secondaries")
-    ap.add_argument("--profile-set", action="store_true",
-                    help="only launch the kernels used for rocprofv3 counter runs (no JSON line)")
+    ap.add_argument("--profile-set", nargs="?", const="all", choices=["all", "c5"], default=None,
+                    help="only launch the kernels used for rocprofv3 runs (no JSON line): 'all' (default) "
+                         "the counter set, 'c5' config 5's whole layer")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one MI355X); "
@@ -653,7 +761,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(0)}")
     if a.profile_set:
-        profile_set(torch, dev, a.steps)
+        profile_set(torch, dev, a.steps, a.profile_set)
         return 0
 
     args = c2_inputs(torch, torch.float32, dev)
@@ -669,6 +777,8 @@ def main() -> int:
     achieved = nbytes / (kms / 1e3) / 1e9
     log(f"c2 fp32: {value:.1f} GB/s per step ({ms_step * 1e3:.1f} us), kernel {kms * 1e3:.1f} us = {achieved:.1f} GB/s")
     workload = "c2_eltwise_f32"
+    sha = source_sha16(cp)
+    traffic, traffic_note = load_traffic(workload, sha)
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -687,9 +797,11 @@ def main() -> int:
                    "algorithmic_bytes": nbytes, "kernels": cp.num_kernels,
                    "hip_graph": cp.use_graph, "kernel": cp.launches[0].name},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(workload),
-                     "kernel_us": round(kms * 1e3, 2)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel_us": round(kms * 1e3, 2), "source_sha16": sha},
     }
+    if traffic_note:
+        line["roofline"]["traffic_note"] = traffic_note
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(torch, args, nbytes, a.cpu_seconds)
         log(f"cpu baseline: {line['cpu_baseline']}")

@@ -29,6 +29,8 @@
  *                           reference's build-cache keys  tensorjit/backends/cuda_backend.py:474
  *   tj_hip_kernel_time      (no counterpart: hipEvent timing of one kernel of a program, used
  *                           by the autotuner and the benchmark)
+ *   tj_hip_program_time_kernels  (no counterpart: one call of a program with a hipEvent between
+ *                           its kernels, for per-kernel times in the program's own context)
  */
 #ifndef TENSORJIT_HIP_H_
 #define TENSORJIT_HIP_H_
@@ -138,6 +140,14 @@ int tj_hip_program_arena(void* handle, void** ptr, size_t* bytes);
  * `stream`, measured with hipEvents recorded on that stream (synchronises). */
 int tj_hip_kernel_time(void* handle, int k, const void* const* inputs, void* const* outputs, void* stream,
                        int warmup, int iters, float* avg_ms);
+
+/* One call of the program, launched exactly as tj_hip_program_run (own arena, same
+ * order, `stream`), with a hipEvent recorded before the first kernel and after each
+ * one; synchronises and writes each kernel's elapsed time (ms) to ms_per_kernel[k]
+ * (one float per launch).  The kernels see the caches and clocks of the program's
+ * own sequence, unlike repeated launches of one kernel. */
+int tj_hip_program_time_kernels(void* handle, const void* const* inputs, void* const* outputs, void* stream,
+                                float* ms_per_kernel);
 
 int tj_hip_program_destroy(void* handle);
 

@@ -534,6 +534,37 @@ int tj_hip_kernel_time(void* handle, int k, const void* const* inputs, void* con
   return 0;
 }
 
+int tj_hip_program_time_kernels(void* handle, const void* const* inputs, void* const* outputs, void* stream,
+                                float* ms_per_kernel) {
+  Program* p = as_program(handle);
+  if (!p || !ms_per_kernel) return fail("tj_hip_program_time_kernels: null argument");
+  if ((p->n_in && !inputs) || (p->n_out && !outputs)) return fail("tj_hip_program_time_kernels: null pointer table");
+  const size_t n = p->kernels.size();
+  if (n == 0) return 0;
+  DeviceScope scope(p->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  std::vector<hipEvent_t> ev(n + 1, nullptr);
+  hipError_t e = hipSuccess;
+  for (size_t i = 0; i <= n && e == hipSuccess; ++i) e = hipEventCreate(&ev[i]);
+  int rc = 0;
+  if (e == hipSuccess) {
+    p->bind(inputs, outputs, p->arena);
+    e = hipEventRecord(ev[0], s);
+    for (size_t k = 0; k < n && e == hipSuccess && rc == 0; ++k) {
+      rc = p->launch_one(p->kernels[k], s);
+      if (rc == 0) e = hipEventRecord(ev[k + 1], s);
+    }
+    if (e == hipSuccess && rc == 0) e = hipEventSynchronize(ev[n]);
+    for (size_t k = 0; k < n && e == hipSuccess && rc == 0; ++k) e = hipEventElapsedTime(&ms_per_kernel[k], ev[k], ev[k + 1]);
+  }
+  for (hipEvent_t x : ev)
+    if (x) (void)hipEventDestroy(x);
+  if (rc) return rc;
+  if (e != hipSuccess) return hip_fail(e, "tj_hip_program_time_kernels events");
+  p->stats.calls++;
+  return 0;
+}
+
 int tj_hip_program_destroy(void* handle) {
   delete as_program(handle);
   return 0;

@@ -648,6 +648,15 @@ class HipProgram:
         return self._native.kernel_time(k, [t.data_ptr() for t in ins], [t.data_ptr() for t in outs], stream,
                                         warmup, iters)
 
+    def kernel_times_in_call_ms(self, *inputs: torch.Tensor) -> list[float]:
+        """Device time of every launch within one call of the whole program (hipEvents
+        between the launches on torch's current stream), in launch order."""
+        ins = self._prepare(inputs)
+        outs = [torch.empty(s, dtype=d, device=self.device) for s, d in self._out_specs]
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        return self._native.time_kernels([t.data_ptr() for t in ins], [t.data_ptr() for t in outs], stream,
+                                         len(self.launches))
+
     def native_stats(self) -> dict:
         return self._native.stats()
 

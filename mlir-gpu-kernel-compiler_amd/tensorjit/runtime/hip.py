@@ -69,6 +69,7 @@ SIGNATURES = {
     "tj_hip_program_arena": (ctypes.c_int, [_VP, _PP, ctypes.POINTER(ctypes.c_size_t)]),
     "tj_hip_kernel_time": (ctypes.c_int, [_VP, ctypes.c_int, _PP, _PP, _VP, ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(ctypes.c_float)]),
+    "tj_hip_program_time_kernels": (ctypes.c_int, [_VP, _PP, _PP, _VP, ctypes.POINTER(ctypes.c_float)]),
     "tj_hip_program_destroy": (ctypes.c_int, [_VP]),
 }
 
@@ -207,6 +208,13 @@ class NativeHipProgram:
         check(self._lib.tj_hip_kernel_time(self.handle, k, *self._tables(ins, outs), stream, warmup, iters,
                                            ctypes.byref(ms)), "tj_hip_kernel_time")
         return ms.value
+
+    def time_kernels(self, ins: Sequence[int], outs: Sequence[int], stream: int, n: int) -> list[float]:
+        """ms of each of the program's ``n`` launches within one call of the whole program."""
+        ms = (ctypes.c_float * max(n, 1))()
+        check(self._lib.tj_hip_program_time_kernels(self.handle, *self._tables(ins, outs), stream, ms),
+              "tj_hip_program_time_kernels")
+        return list(ms[:n])
 
     def stats(self) -> dict:
         s = Stats()

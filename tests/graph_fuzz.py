@@ -122,12 +122,13 @@ def attention_program(seed: int):
     form = rng.choice(["mul", "lmul", "div", "none"])
     c = rng.choice([0.05, 0.125, 0.3])
 
-    def fn(q, k, v):
-        s = tj.matmul(q, tj.transpose(k, -1, -2))
-        s = {"mul": lambda t: t * c, "lmul": lambda t: c * t, "div": lambda t: t / (1.0 / c),
-             "none": lambda t: t}[form](s)
-        return tj.matmul(tj.softmax(s), v)
+    scale = {"mul": lambda t: t * c, "lmul": lambda t: c * t, "div": lambda t: t / (1.0 / c),
+             "none": lambda t: t}[form]
 
+    def fn(q, k, v):
+        return tj.matmul(tj.softmax(scale(tj.matmul(q, tj.transpose(k, -1, -2)))), v)
+
+    fn.scores = scale       # the same scaling, for references that evaluate the scores themselves
     return fn, [(*lead, sq, d), (*lead, sk, d), (*lead, sk, dv)]
 
 

@@ -87,6 +87,8 @@ int main() {
   expect(tj_hip_program_stats(nullptr, &st) != 0, "stats null");
   float ms = 0.f;
   expect(tj_hip_kernel_time(nullptr, 0, nullptr, nullptr, nullptr, 1, 1, &ms) != 0, "kernel_time null");
+  expect(tj_hip_program_time_kernels(nullptr, nullptr, nullptr, nullptr, &ms) != 0 && error_has("null argument"),
+         "time_kernels null");
   expect(tj_hip_program_destroy(nullptr) == 0, "destroy null");
   std::printf("%s (%d failures)\n", failures ? "FAILED" : "OK", failures);
   return failures ? 1 : 0;

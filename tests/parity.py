@@ -100,3 +100,22 @@ def close_f32(out, ref, rtol: float = F32_TOL, scale: float = F32_TOL, norm: flo
 def close_lowp(out, ref, tol: float = LOWP_ELEM, norm: float = LOWP_NORM, what: str = ""):
     """bf16 / fp16 output against the fp32 reference of the same (upcast) inputs."""
     return compare(out, ref, rtol=tol, scale=tol, norm=norm, what=what)
+
+
+def stored(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """``t`` (float64) as a kernel stores it in ``dtype``: rounded to fp32 where the kernel
+    computes, then to ``dtype`` (round to nearest even), back in float64."""
+    return t.float().to(dtype).double()
+
+
+def attention_plan_reference(q, k, v, scores, dtype) -> torch.Tensor:
+    """The reference plan's unfused attention (scores kernel -> softmax row kernel -> PV
+    kernel) in float64 with its two intermediate stores rounded to the storage type:
+    ``scores(q @ k^T)`` and ``softmax(.)``.  At bf16 a stored logit ``s`` is off by up to
+    2^-8 |s|, which moves its probability by that much relative: for logits of a few units
+    this error exceeds the output's own rounding several times over, so a plan that stores
+    scores is compared with this emulation rather than with the fp32 oracle alone."""
+    qd, kd, vd = (t.detach().cpu().double() for t in (q, k, v))
+    s = stored(scores(qd @ kd.transpose(-1, -2).contiguous()), dtype)
+    p = stored(torch.softmax(s, dim=-1), dtype)
+    return p @ vd

@@ -12,7 +12,7 @@ import torch
 
 import graph_fuzz
 import tensorjit as tj
-from parity import compare
+from parity import LOWP_NORM, attention_plan_reference, compare
 from tensorjit.backends import hip_backend as hb
 from tensorjit.compiler import lower
 from tensorjit.ir import DType, TensorType
@@ -115,11 +115,26 @@ def _check_vs_oracle(fn, shapes, seed, dts, scales=None):
 @pytest.mark.parametrize("seed", ATTN_SEEDS)
 def test_random_attention_matches_the_oracle(seed, monkeypatch):
     """The fused flash kernel on random shapes, bf16 and fp16, against the fp32 oracle
-    of the reference plan (2e-2, the bound of the hand-written attention tests)."""
+    of the reference plan (2e-2, the bound of the hand-written attention tests).  Head
+    dims that are not multiples of 32 keep the reference plan's three kernels, which store
+    the scores and probabilities in the storage type: those are held to the float64
+    emulation of that plan's stores (at bf16 a stored logit of a few units moves its
+    probability by more than the output's own rounding)."""
     monkeypatch.setenv("TENSORJIT_NO_AUTOTUNE", "1")
     fn, shapes = graph_fuzz.attention_program(seed)
     print(f"random attention {seed} {shapes}", flush=True)
-    _check_vs_oracle(fn, shapes, seed, [(torch.bfloat16, 2e-2), (torch.float16, 2e-2)])
+    if shapes[0][-1] % 32 == 0:
+        _check_vs_oracle(fn, shapes, seed, [(torch.bfloat16, 2e-2), (torch.float16, 2e-2)])
+    else:
+        g = torch.Generator().manual_seed(seed)
+        ins = [torch.randn(s, generator=g) for s in shapes]
+        for dt in (torch.bfloat16, torch.float16):
+            args = [t.to(dt) for t in ins]
+            f = tj.jit(fn)
+            out = f(*[t.cuda() for t in args])
+            assert [k.kind for k in f.compiled(*[t.cuda() for t in args]).program.kernels].count("attention") == 0
+            compare(out, attention_plan_reference(*args, fn.scores, dt), rtol=2e-2, scale=2e-2, norm=LOWP_NORM,
+                    what=f"seed {seed} {dt} unfused vs emulated plan")
     if shapes[0][-1] % 64 == 0 and shapes[2][-1] % 64 == 0:
         # the same cores on the ping-pong schedule (the layout rule keeps it for grids of
         # at least 256 workgroups, which these shapes do not reach)

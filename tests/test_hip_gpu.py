@@ -16,7 +16,7 @@ import torch.nn.functional as F
 
 import oracle
 import tensorjit as tj
-from parity import close_f32, close_lowp
+from parity import attention_plan_reference, close_f32, close_lowp
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -585,12 +585,14 @@ def test_fused_attention_vs_oracle_and_unfused_plan(shapes, dt, monkeypatch):
     cp = f.compiled(q, k, v)
     assert cp.num_kernels == 1 and "attention" in cp.launches[0].name
     (ref,) = oracle.run(ATTN, *[t.float().cpu() for t in (q, k, v)])
-    close_lowp(out, ref, tol=2e-2)
+    close_lowp(out, ref, tol=2e-2, what="fused vs fp32 oracle")
     monkeypatch.setenv("TENSORJIT_HIP_ATTENTION", "0")
     f3 = tj.jit(ATTN)
     out3 = f3(q, k, v)
     assert f3.compiled(q, k, v).num_kernels == 3
-    close_lowp(out, out3, tol=2e-2)
+    # the unfused plan stores its scores and probabilities in the storage type (the fused
+    # kernel keeps both in fp32): it is held to the float64 emulation of those stores
+    close_lowp(out3, attention_plan_reference(q, k, v, lambda t: t * 0.125, dt), what="unfused vs emulated plan")
 
 
 def _mha(x, wq, wk, wv, heads):
@@ -618,7 +620,9 @@ def test_fused_attention_reads_and_writes_head_interleaved_layout(B, S, Dm, head
     cp = f.compiled(x, *ws)
     assert [l.meta["family"] for l in cp.launches].count("attention") == 1 and cp.num_kernels == 4
     (ref,) = oracle.run(fn, *[t.float().cpu() for t in (x, *ws)])
-    close_lowp(out, ref, tol=2e-2)
+    # norm bound 1e-2: q and k are stored in bf16 by their projection kernels, and a logit
+    # rounded by up to 2^-8 relative moves its probability by that times |s|
+    close_lowp(out, ref, tol=2e-2, norm=1e-2)
 
 
 def test_fused_attention_scale_written_as_division():
@@ -1194,16 +1198,16 @@ def _config5_batch0_fp32(args):
 def test_config5_block_full_size_batch0_vs_fp32():
     """Config 5's layer at its full shape ([4, 2048, 4096], 32 heads x 128, MLP 11008, bf16) on
     the packaged tiles, against a float32 torch evaluation of the same layer for batch 0 (the
-    batches are independent).  Norm bound 1e-2: the layer stores bf16 between its 9 kernels
-    (q, k, v, attention output, residual stream, normed activations, gelu output), each a
-    rounding of ~1.7e-3 RMS relative that later kernels carry forward."""
+    batches are independent), at the default bf16 bounds: the layer stores bf16 between its
+    9 kernels (q, k, v, attention output, residual stream, normed activations, gelu output)
+    and lands 3.3e-3 from float32 in norm, 3.9e-3 in its worst row."""
     import bench
 
     args = bench.block_inputs(torch, torch.device(DEV))
     f = tj.jit(bench._fn_block)
     out = f(*args)
     assert f.compiled(*args).num_kernels == 9
-    close_lowp(out[:1], _config5_batch0_fp32(args), tol=3e-2, norm=1e-2)
+    close_lowp(out[:1], _config5_batch0_fp32(args), tol=3e-2)
 
 
 def test_config5_block_full_size_under_graph_replay(monkeypatch):
@@ -1228,7 +1232,7 @@ def test_config5_block_full_size_under_graph_replay(monkeypatch):
     assert cp.stats["graph_replays"] >= 2
     for r in replays:
         assert torch.equal(r, direct)
-    close_lowp(replays[-1][:1], _config5_batch0_fp32(args), tol=3e-2, norm=1e-2)
+    close_lowp(replays[-1][:1], _config5_batch0_fp32(args), tol=3e-2)
 
 
 def test_config5_block_with_fused_attention_vs_oracle():
