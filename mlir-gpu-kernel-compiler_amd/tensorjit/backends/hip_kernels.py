@@ -433,6 +433,19 @@ def row_geometry(N: int, vec: int, streaming_ok: bool) -> tuple[int, int, bool]:
 WAVE_ROW_MAX_CHUNKS = 4
 WAVE_ROWS_PER_BLOCK = 4
 ONE_CHUNK_MAX_LANES = 1024
+# Rows of 257-1024 chunks with two or more reductions take this many lanes and several
+# chunks per lane instead, when the rows are longer than 512 chunks (8 KiB) or every input
+# the row kernel reads per element is a whole [rows, N] tensor: every reduction is a
+# barrier across the row's waves, and fewer waves per row wait less.  Measured on one box
+# through the generator (us, 512 or 1024 lanes x 1 chunk -> 256 lanes x 2-4 chunks):
+# softmax fp32 [65536, 2048] 171.6 -> 161.6, bf16 [65536, 4096] 192.8 -> 169.4, fp16
+# 200.8 -> 180.2, bf16 [32768, 8192] 197.0 -> 165.8, fp32 [32768, 4096] 172.1 -> 167.9;
+# LayerNorm (with a gain broadcast over rows) bf16 [32768, 8192] 186.3 -> 173.4, fp32
+# [32768, 4096] 186.3 -> 172.7, but over 8 KiB rows it loses: bf16 [65536, 4096] 169.0 ->
+# 173.0, fp16 171.2 -> 173.4, fp32 [65536, 2048] 164.4 -> 172.1.  128 lanes was slower
+# than 256 on 10 of those 12 cases.  A plain copy of 8 KiB rows runs 163.0 us at 512 x 1
+# and 178.1 at 256 x 2, so single-reduction and reduction-free rows keep one chunk.
+MULTI_REDUCTION_LANES = 256
 
 
 @dataclass(frozen=True)
@@ -443,11 +456,16 @@ class RowShape:
     rows_per_block: int
 
 
-def row_shape(N: int, vec: int, streaming_ok: bool) -> RowShape:
+def row_shape(N: int, vec: int, streaming_ok: bool, reductions: int = 1, whole_row_inputs: bool = False) -> RowShape:
+    """Lanes and chunks of a row kernel over rows of ``N`` elements in ``vec``-element
+    chunks; ``reductions``: reduction stages in the row kernel; ``whole_row_inputs``: every
+    input read per element is a whole [rows, N] tensor (none is broadcast over rows)."""
     nv = -(-N // vec)
     if nv <= 64 * WAVE_ROW_MAX_CHUNKS:
         return RowShape(64, -(-nv // 64), False, WAVE_ROWS_PER_BLOCK)
     if nv <= ONE_CHUNK_MAX_LANES:
+        if reductions >= 2 and nv > MULTI_REDUCTION_LANES and (nv > 512 or whole_row_inputs):
+            return RowShape(MULTI_REDUCTION_LANES, -(-nv // MULTI_REDUCTION_LANES), False, 1)
         return RowShape(64 * -(-nv // 64), 1, False, 1)
     t, nch, streaming = row_geometry(N, vec, streaming_ok)
     return RowShape(t, nch, streaming, 1)
@@ -503,18 +521,6 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
 
     dt = _kernel_dtype(k)
     vec = _vec_for(N, N, dt)
-    split = row_split(nrows, N, vec, dt.itemsize) if len(stages) == 1 and stages[0].kind == "reduce" else None
-    if split:
-        T, NCH, streaming, R = SPLIT_THREADS, split.chunks, False, 1
-    else:
-        shape = row_shape(N, vec, streaming_ok=len(stages) == 1)
-        T, NCH, streaming, R = shape.lanes, shape.chunks, shape.streaming, shape.rows_per_block
-    if R > 1 and nrows < R * 256:
-        # too few rows to fill the chip with R-row workgroups: one row per workgroup
-        R = 1
-    nwaves = T // 64
-    # every chunk in bounds: whole rows of chunks, and with a split whole segments
-    full = N % (T * vec * (NCH if split else 1)) == 0
     inside = {id(n) for n in k.nodes}
     escaping = {id(o): j for j, o in enumerate(k.outputs)}
     stage_of = {id(n): si for si, st in enumerate(stages) for n in st.nodes}
@@ -560,6 +566,20 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
     ext_streamed = {i for i, (n, st_) in vec_ext.items() if _streamed(vec_shape, st_)}
     nt = _nt_loads(sum(math.prod(n.shape) * n.dtype.itemsize for i, (n, _) in vec_ext.items() if i in ext_streamed)
                    + sum(math.prod(o.shape or (1,)) * o.dtype.itemsize for o in k.outputs))
+
+    split = row_split(nrows, N, vec, dt.itemsize) if len(stages) == 1 and stages[0].kind == "reduce" else None
+    if split:
+        T, NCH, streaming, R = SPLIT_THREADS, split.chunks, False, 1
+    else:
+        shape = row_shape(N, vec, streaming_ok=len(stages) == 1, reductions=nred,
+                          whole_row_inputs=len(ext_streamed) == len(vec_ext))
+        T, NCH, streaming, R = shape.lanes, shape.chunks, shape.streaming, shape.rows_per_block
+    if R > 1 and nrows < R * 256:
+        # too few rows to fill the chip with R-row workgroups: one row per workgroup
+        R = 1
+    nwaves = T // 64
+    # every chunk in bounds: whole rows of chunks, and with a split whole segments
+    full = N % (T * vec * (NCH if split else 1)) == 0
 
     ws_param = ", float* __restrict__ ws_p" if split else ""
     L = [f'extern "C" __global__ __launch_bounds__({T * R}) void {g.fname}({g.params()}{ws_param}) {{']

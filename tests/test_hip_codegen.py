@@ -65,10 +65,16 @@ def test_launch_geometry():
 def test_row_kernel_geometry_for_benchmark_rows():
     from tensorjit.backends.hip_kernels import RowShape, row_geometry, row_shape
 
-    # rows of 8-16 KiB: one workgroup per row, one 16-byte chunk per lane
-    assert row_shape(4096, 8, False) == RowShape(512, 1, False, 1)     # config 3 LN / RMS bf16
-    assert row_shape(2048, 4, False) == RowShape(512, 1, False, 1)     # config 3 softmax fp32
+    # rows of 8-16 KiB: one workgroup per row, one 16-byte chunk per lane; with two or more
+    # reductions 256 lanes and several chunks when the rows pass 8 KiB or no input is
+    # broadcast over rows (softmax; a LayerNorm gain is)
+    assert row_shape(4096, 8, False) == RowShape(512, 1, False, 1)     # config 3 RMS bf16
+    assert row_shape(4096, 8, False, reductions=2) == RowShape(512, 1, False, 1)    # config 3 LN bf16 (gain)
+    assert row_shape(2048, 4, False, reductions=2, whole_row_inputs=True) == RowShape(256, 2, False, 1)  # softmax
     assert row_shape(4096, 4, False) == RowShape(1024, 1, False, 1)    # fp32 N=4096
+    assert row_shape(4096, 4, False, reductions=3) == RowShape(256, 4, False, 1)    # 16 KiB rows, gain or not
+    assert row_shape(1200, 4, False, reductions=2, whole_row_inputs=True) == RowShape(256, 2, False, 1)
+    assert row_shape(1200, 4, False, reductions=2) == RowShape(320, 1, False, 1)
     # rows up to 4 KiB: one wave per row, 4 rows per workgroup
     assert row_shape(2048, 8, False) == RowShape(64, 4, False, 4)      # config 5 softmax bf16
     assert row_shape(768, 4, False) == RowShape(64, 3, False, 4)       # config 1 LayerNorm fp32
@@ -82,7 +88,8 @@ def test_row_kernel_geometry_for_benchmark_rows():
 def test_row_kernel_launch_shapes():
     """Wave-per-row kernels put 4 rows in a workgroup when there are rows enough to fill the
     chip (a ragged last workgroup returns its extra waves), else one row per workgroup; the
-    reductions are wave-only there (no LDS array), and 8 KiB rows take 512-lane workgroups."""
+    reductions are wave-only there (no LDS array), and 8 KiB rows take 512-lane workgroups with
+    one reduction, 256-lane workgroups with two."""
     import tensorjit as tj
     from tensorjit.compiler import lower
 
@@ -99,7 +106,9 @@ def test_row_kernel_launch_shapes():
     src, l = launch((4098, 1000), DType.f32)
     assert l.grid == (1025, 1, 1) and l.block == (256, 1, 1) and "if (r >= 4098u) return;" in src
     src, l = launch((65536, 2048), DType.f32)
-    assert l.grid == (65536, 1, 1) and l.block == (512, 1, 1) and "tj_red" in src
+    assert l.grid == (65536, 1, 1) and l.block == (256, 1, 1) and "tj_red" in src     # two reductions
+    src, l = launch((65536, 2048), DType.f32, fn=lambda s: tj.sum(s * s, axis=-1))
+    assert l.grid == (65536, 1, 1) and l.block == (512, 1, 1) and "tj_red" in src     # one
 
 
 def test_every_candidate_config_generates_valid_code():

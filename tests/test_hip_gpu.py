@@ -417,7 +417,7 @@ def test_softmax_layernorm_rmsnorm(shape):
     (1000, 520, torch.float16),      # too few rows for 4 per workgroup; 65 chunks: a part-used lane
     (300, 1200, torch.float32),      # one chunk per lane, 300 of 320 lanes used
     (257, 4096, torch.bfloat16),     # 8 KiB rows: 512 lanes x 1 chunk
-    (64, 4096, torch.float32),       # 16 KiB rows: 1024 lanes x 1 chunk
+    (64, 4096, torch.float32),       # 16 KiB rows, five reductions: 256 lanes x 4 chunks (the max: 1024 x 1)
     (16, 12288, torch.float32),      # longer rows: several chunks per lane
     (37, 4097, torch.float32),       # odd length: scalar lanes, 832 lanes x 5 elements
     (8, 16384, torch.float32),       # 256 lanes x 16 chunks
@@ -436,12 +436,15 @@ def test_row_layouts_vs_oracle(rows, n, dt):
     x = (torch.randn(rows, n, device=DEV) * 2).to(dt)
     g = (1 + 0.1 * torch.randn(n, device=DEV)).to(dt)
     vec = 16 // x.element_size() if n % (16 // x.element_size()) == 0 else 1
-    shape = row_shape(n, vec, False)
     f, _ = check_vs_oracle(lambda t, w: (tj.layer_norm(t, w), tj.rms_norm(t, w), tj.softmax(t)), x, g)
-    launch = f.compiled(x, g).launches[0]
+    cp = f.compiled(x, g)
+    # the gain is broadcast over rows
+    shape = row_shape(n, vec, False, reductions=sum(st.kind == "reduce" for st in cp.program.kernels[0].stages))
+    launch = cp.launches[0]
     assert launch.meta["threads"] == shape.lanes and launch.meta["chunks"] == shape.chunks
     m = tj.jit(lambda t: tj.max(t))
     assert torch.equal(m(x), x.amax(-1))
+    assert m.compiled(x).launches[0].meta["threads"] == row_shape(n, vec, False).lanes
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
