@@ -682,8 +682,10 @@ def profile_set(torch, dev, steps, which="all") -> None:
     read + 256 MiB written), the row configs, the config-4 bf16 GEMM and its decode
     shape, config 5's bf16 softmax rows and fused attention, ``steps`` launches each.
     ``c5``: ``steps`` calls of config 5's whole layer (direct launches), for a kernel
-    trace of the layer in its own context.  Each program's source digest is logged, so
-    a counter summary names the kernel source it measured."""
+    trace of the layer in its own context.  ``c1``: ``steps`` calls of config 1's MLP
+    block with direct launches, then ``steps`` with hipGraph replay, back to back (the
+    trace's dispatch timestamps show each mode's gaps between kernels).  Each program's
+    source digest is logged, so a counter summary names the kernel source it measured."""
     import tensorjit as tj
 
     def run(fn, fargs):
@@ -698,6 +700,18 @@ def profile_set(torch, dev, steps, which="all") -> None:
         run(_fn_block, block_inputs(torch, dev))
         torch.cuda.synchronize()
         log(f"profile set c5 done ({steps} calls)")
+        return
+    if which == "c1":
+        gen = torch.Generator(device=dev).manual_seed(0)
+        shapes = [(512, 768), (768,), (3072, 768), (3072,), (768, 3072), (768,)]
+        margs = [torch.randn(sh, device=dev, generator=gen) * (1 if i < 2 else 0.02) for i, sh in enumerate(shapes)]
+        for mode in ("0", "1"):
+            os.environ["TENSORJIT_HIP_GRAPH"] = mode
+            run(_fn_mlp, margs)
+            torch.cuda.synchronize()
+            time.sleep(0.05)           # a quiet gap between the two modes in the trace
+        os.environ.pop("TENSORJIT_HIP_GRAPH", None)
+        log(f"profile set c1 done ({steps} calls per mode)")
         return
     args = c2_inputs(torch, torch.float32, dev)
     run(_fn_c2, args)
@@ -741,9 +755,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--quick", action="store_true", help="skip the GEMM / MLP secondaries")
-    ap.add_argument("--profile-set", nargs="?", const="all", choices=["all", "c5"], default=None,
+    ap.add_argument("--profile-set", nargs="?", const="all", choices=["all", "c5", "c1"], default=None,
                     help="only launch the kernels used for rocprofv3 runs (no JSON line): 'all' (default) "
-                         "the counter set, 'c5' config 5's whole layer")
+                         "the counter set, 'c5' config 5's whole layer, 'c1' config 1 direct then replayed")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one MI355X); "
