@@ -130,14 +130,19 @@ def _vec_for(row_len: int, numel: int, dtype: DType) -> int:
 # ---------------------------------------------------------------------------
 
 
-# MI355X's last-level cache (MALL, "infinity cache") holds 256 MB.  A kernel that
-# streams more than that loads its streamed inputs with the nontemporal hint (no
-# allocation in the caches they pass through); measured on MI355X, same kernels,
-# interleaved: config 2 fp32 (805 MB) 128.6 -> 120.3 us, bf16 (403 MB) 66.5 -> 64.5,
-# RMSNorm bf16 (1 GiB) 167.0 -> 163.8, a 1 GiB bf16 add 258.5 -> 241.6; but a 128 MB
-# RMSNorm whose input stays in the MALL between calls 20.0 -> 21.1, and broadcast
-# operands (re-read by every row) lose their cache hits.  TENSORJIT_HIP_NT_LOADS=0 / 1
-# forces the hint off / on for every streamed input.
+# MI355X's last-level cache (MALL, "infinity cache") holds 256 MiB.  A kernel whose
+# streamed inputs (read once, no broadcast dim) exceed that loads them with the
+# nontemporal hint (no allocation in the caches they pass through): they cannot stay
+# cached, and the hint measured faster, same kernels, interleaved: config 2 fp32 (512
+# MiB in) 128.6 -> 120.3 us, RMSNorm bf16 (512 MiB in) 167.0 -> 163.8, a bf16 add of
+# 2 x 512 MiB 258.5 -> 241.6.  Inputs that fit stay plain loads: whatever produced them
+# (or the previous call) may have left them in the MALL.  Same box, both rounds, plain
+# vs nontemporal: softmax fp32 [16384, 2048] (128 MiB in, 256 MiB of traffic) 37.6 vs
+# 40.7 us, RMSNorm / LayerNorm bf16 [16384, 4096] 37.1-37.3 vs 42.3-45.1 / 38.2-39.5 vs
+# 43.6-48.6, gelu fp32 [16384, 4096] (256 MiB in) 73.4-74.5 vs 78.3-81.5, config 2
+# bf16 (256 MiB in) 64.1-68.7 vs 67.3-73.8.  Broadcast operands (re-read by every row)
+# never take the hint.  TENSORJIT_HIP_NT_LOADS=0 / 1 forces it off / on for every
+# streamed input.
 MALL_BYTES = 256 << 20
 
 
@@ -154,12 +159,13 @@ def _streamed(shape, strides) -> bool:
     return all(st != 0 for d, st in zip(shape, strides) if d > 1)
 
 
-def _nt_loads(streamed_bytes: int) -> bool:
-    """Nontemporal loads for a kernel that streams ``streamed_bytes`` (inputs read once plus outputs)."""
+def _nt_loads(streamed_input_bytes: int) -> bool:
+    """Nontemporal loads for a kernel whose streamed inputs (each element read once) total
+    ``streamed_input_bytes``."""
     forced = os.environ.get("TENSORJIT_HIP_NT_LOADS")
     if forced in ("0", "1"):
         return forced == "1"
-    return streamed_bytes >= MALL_BYTES
+    return streamed_input_bytes > MALL_BYTES
 
 
 def _load_lines(src: str, ctype_ptr: str, off: str, inner: int, vec: int, dst: str, nt: bool = False) -> list[str]:
@@ -207,8 +213,7 @@ def gen_pointwise(g: KernelGen, nodes: list[Node], iter_shape: tuple[int, ...]) 
     guard = nvec % per_block != 0
     inside = {id(n) for n in nodes}
     streamed = {id(n) for n in k.inputs if _streamed(iter_shape, in_st[id(n)])}
-    nt = _nt_loads(sum(math.prod(n.shape or (1,)) * n.dtype.itemsize for n in k.inputs if id(n) in streamed)
-                   + sum(numel * o.dtype.itemsize for o in k.outputs))
+    nt = _nt_loads(sum(math.prod(n.shape or (1,)) * n.dtype.itemsize for n in k.inputs if id(n) in streamed))
 
     L = [f'extern "C" __global__ __launch_bounds__({POINTWISE_THREADS}) void {g.fname}({g.params()}) {{',
          f"  const {idx_t} vbase = ({idx_t})blockIdx.x * {per_block}u + threadIdx.x;"]
@@ -564,8 +569,7 @@ def gen_row(g: KernelGen, stages: list[Kernel], rows: tuple, N: int) -> tuple[st
                                      vec_shape)
             vec_ext[id(n)] = (n, strides)
     ext_streamed = {i for i, (n, st_) in vec_ext.items() if _streamed(vec_shape, st_)}
-    nt = _nt_loads(sum(math.prod(n.shape) * n.dtype.itemsize for i, (n, _) in vec_ext.items() if i in ext_streamed)
-                   + sum(math.prod(o.shape or (1,)) * o.dtype.itemsize for o in k.outputs))
+    nt = _nt_loads(sum(math.prod(n.shape) * n.dtype.itemsize for i, (n, _) in vec_ext.items() if i in ext_streamed))
 
     split = row_split(nrows, N, vec, dt.itemsize) if len(stages) == 1 and stages[0].kind == "reduce" else None
     if split:

@@ -339,18 +339,22 @@ def _loads(fn, shapes, dt):
 
 
 def test_nontemporal_loads_for_streamed_inputs_past_the_mall(monkeypatch):
-    """Inputs read once (no broadcast dim) get the nontemporal hint when the kernel streams
-    at least the 256 MB MALL; broadcast operands never do, and smaller kernels keep
-    plain loads (their inputs may stay cached between calls)."""
+    """Inputs read once (no broadcast dim) get the nontemporal hint when together they
+    exceed the 256 MiB MALL; broadcast operands never do, and kernels whose streamed
+    inputs fit keep plain loads (their inputs may stay cached from the producer or the
+    previous call), however much they write."""
     monkeypatch.delenv("TENSORJIT_HIP_NT_LOADS", raising=False)
     c2 = lambda x, a, b, c: tj.gelu(x * a + b) * tj.sigmoid(c) + x  # noqa: E731
-    big = [(16384, 4096), (4096,), (4096,), (16384, 4096)]
+    big = [(16384, 4096), (4096,), (4096,), (16384, 4096)]           # 512 MiB streamed in
     assert _loads(c2, big, DType.f32) == ["tj_ldv_nt(in0_p", "tj_ldv_nt(in1_p", "tj_ldv(in2_p", "tj_ldv(in3_p"]
-    small = [(4096, 4096), (4096,), (4096,), (4096, 4096)]          # 201 MB streamed
+    assert all(x.startswith("tj_ldv(") for x in _loads(c2, big, DType.bf16))     # exactly 256 MiB in
+    small = [(4096, 4096), (4096,), (4096,), (4096, 4096)]
     assert all(x.startswith("tj_ldv(") for x in _loads(c2, small, DType.f32))
     rms = lambda x, g: tj.rms_norm(x, g)  # noqa: E731
     assert _loads(rms, [(65536, 4096), (4096,)], DType.bf16) == ["tj_ldv_nt(in0_p", "tj_ldv(in1_p"]
     assert all(x.startswith("tj_ldv(") for x in _loads(rms, [(8192, 4096), (4096,)], DType.bf16))
+    # 128 MiB in, 256 MiB of traffic: plain loads
+    assert all(x.startswith("tj_ldv(") for x in _loads(lambda s: tj.softmax(s), [(16384, 2048)], DType.f32))
     monkeypatch.setenv("TENSORJIT_HIP_NT_LOADS", "1")
     assert _loads(rms, [(8192, 4096), (4096,)], DType.bf16) == ["tj_ldv_nt(in0_p", "tj_ldv(in1_p"]
     monkeypatch.setenv("TENSORJIT_HIP_NT_LOADS", "0")
