@@ -410,12 +410,22 @@ ROW_MAX_FLOATS = 32
 
 def row_geometry(N: int, vec: int, streaming_ok: bool) -> tuple[int, int, bool]:
     """(threads T, chunks per lane NCH, streaming).  Up to 256 lanes x 16 chunks of
-    ``vec`` elements; then a rolled loop over 1024 lanes (single-stage reductions) or up
-    to 1024 lanes x ROW_MAX_FLOATS // vec chunks (rows with several stages)."""
+    ``vec`` elements (rows with several stages: 512 lanes from 12 chunks at 256); then a
+    rolled loop over 1024 lanes (single-stage reductions) or up to 1024 lanes x
+    ROW_MAX_FLOATS // vec chunks (rows with several stages)."""
     nv = -(-N // vec)
     nch = max(1, -(-nv // 256))
     t = 64 * -(-(-(-nv // nch)) // 64)
     if nch <= 16:
+        if nch >= 12 and not streaming_ok and -(-nv // 512) * vec <= ROW_MAX_FLOATS:
+            # rows with several stages that would hold 12-16 chunks per lane take 512 lanes:
+            # same box, generator, 256 x 16 -> 512 x 8 for fp32 [8192, 16384] LayerNorm
+            # 179.7 -> 169.9 us, softmax 181.0 -> 172.1, RMSNorm 181.0 -> 183.8; 256 x 12 ->
+            # 512 x 6 for fp32 [8192, 12288] 131.8 / 132.8 / 131.1 -> 130.0 / 130.3 / 127.0
+            # (bf16 rows of 8 chunks keep 256 lanes: 512 lanes lost 0-3%; past 256 lanes a lane
+            # holds at most ROW_MAX_FLOATS values per row array, as below)
+            nch = -(-nv // 512)
+            return 64 * -(-(-(-nv // nch)) // 64), nch, False
         return t, nch, False
     if streaming_ok:
         return 1024, -(-nv // 1024), True

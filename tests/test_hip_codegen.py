@@ -81,6 +81,8 @@ def test_row_kernel_geometry_for_benchmark_rows():
     assert row_shape(70, 1, False) == RowShape(64, 2, False, 4)        # unvectorised odd rows
     # longer rows: several chunks per lane, then a rolled loop
     assert row_shape(8192, 4, False) == RowShape(256, 8, False, 1)
+    assert row_shape(16384, 4, False) == RowShape(512, 8, False, 1)      # 12+ chunks at 256 lanes
+    assert row_shape(16384, 4, True) == RowShape(256, 16, False, 1)      # a single reduction keeps 256
     assert row_geometry(4096, 8, False) == (256, 2, False)
     assert row_shape(100000, 4, True).streaming is True                # long stand-alone reductions stream
 
@@ -468,11 +470,15 @@ def test_split_reductions_generate_and_compile(case, tj_env):
 
 def test_long_rows_with_several_stages_fit_one_workgroup(tj_env):
     """Rows with several stages up to the hip row-fusion limit (32768) get one row kernel:
-    256 lanes x up to 16 chunks, then up to 1024 lanes x 32 values per lane per row array
-    (odd lengths load one element per chunk), and the kernels compile for gfx950."""
+    256 lanes x up to 11 chunks (512 lanes from 12), then up to 1024 lanes x 32 values per
+    lane per row array (odd lengths load one element per chunk), and the kernels compile
+    for gfx950."""
     from tensorjit.backends import hip_kernels as hk
 
-    assert hk.row_geometry(16384, 4, False) == (256, 16, False)
+    assert hk.row_geometry(16384, 4, False) == (512, 8, False)
+    assert hk.row_geometry(16384, 4, True) == (256, 16, False)
+    assert hk.row_geometry(11264, 4, False) == (256, 11, False)
+    assert hk.row_geometry(32768, 8, False) == (256, 16, False)        # 512 x 8 chunks of 8: too many values
     assert hk.row_geometry(32768, 4, False) == (1024, 8, False)
     assert hk.row_geometry(4097, 1, False) == (832, 5, False)
     assert hk.row_geometry(5001, 1, False) == (1024, 5, False)

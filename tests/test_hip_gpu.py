@@ -418,9 +418,9 @@ def test_softmax_layernorm_rmsnorm(shape):
     (300, 1200, torch.float32),      # one chunk per lane, 300 of 320 lanes used
     (257, 4096, torch.bfloat16),     # 8 KiB rows: 512 lanes x 1 chunk
     (64, 4096, torch.float32),       # 16 KiB rows, five reductions: 256 lanes x 4 chunks (the max: 1024 x 1)
-    (16, 12288, torch.float32),      # longer rows: several chunks per lane
+    (16, 12288, torch.float32),      # longer rows: several chunks per lane (512 x 6)
     (37, 4097, torch.float32),       # odd length: scalar lanes, 832 lanes x 5 elements
-    (8, 16384, torch.float32),       # 256 lanes x 16 chunks
+    (8, 16384, torch.float32),       # 512 lanes x 8 chunks (the max: 256 x 16)
     (6, 32767, torch.float32),       # 1024 scalar lanes x 32 elements, the last lane part-used
     (3, 32768, torch.float32),       # 1024 lanes x 8 chunks
     (4, 32768, torch.bfloat16),      # 256 lanes x 16 chunks of 8
