@@ -1344,8 +1344,9 @@ def test_config5_transformer_block_small_bf16_vs_oracle():
         assert torch.equal(cp(*args)[0], eager)
 
 
-def _run_with_config(fn, args, cfg):
-    """Compile ``fn`` for ``args`` with its single matmul forced to tile config ``cfg``."""
+def _run_with_config(fn, args, cfg, calls=1):
+    """Compile ``fn`` for ``args`` with its single matmul forced to tile config ``cfg``;
+    ``calls`` > 1 runs that one program that many times and returns every output."""
     from tensorjit.backends import hip_backend as hb
     from tensorjit.compiler import lower
     from tensorjit.frontend.tracer import tensor_type_of
@@ -1355,7 +1356,6 @@ def _run_with_config(fn, args, cfg):
     (k,) = p.kernels
     src, launches = hb.generate(p, {0: cfg})
     code = hb.compile_source(src, hb.arch_of(0))
-    out = torch.empty(k.outputs[0].shape, device=DEV, dtype=args[0].dtype)
     # the kernel's parameters follow its own input order, not the traced function's
     gin = {id(n): j for j, n in enumerate(p.graph.inputs)}
     order = [gin[id(p.resolve(n))] for n in k.inputs]
@@ -1364,9 +1364,12 @@ def _run_with_config(fn, args, cfg):
     ws, arena = hb.workspace_layout(launches, 0)          # split-K GEMMs: partials + a sum launch
     prog = rt.NativeHipProgram(0, code, [l.name for l in launches], [(l.grid, l.block, 0) for l in launches],
                                hb.launch_args(launches, refs, ws), arena, len(args), 1)
-    prog.run([a.data_ptr() for a in args], [out.data_ptr()], torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for _ in range(calls):
+        outs.append(torch.empty(k.outputs[0].shape, device=DEV, dtype=args[0].dtype))
+        prog.run([a.data_ptr() for a in args], [outs[-1].data_ptr()], torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-    return out
+    return outs[0] if calls == 1 else outs
 
 
 @pytest.mark.parametrize("tb", [True, False])
@@ -1520,7 +1523,8 @@ def test_on_device_autotune_times_candidates_and_persists_the_winner(dt, monkeyp
 def test_k_split_gemm_matches_reference(case):
     """K split over workgroups: fp32 partial tiles in the arena workspace, summed (in a
     fixed order) by a second launch that applies the fused epilogue; compared with an
-    fp32 reference, twice (the workspace is reused without clearing)."""
+    fp32 reference on three calls of one program (the workspace is reused without
+    clearing), bit-identical."""
     from tensorjit.runtime.autotune import MatmulConfig
 
     torch.manual_seed(0)
@@ -1548,17 +1552,13 @@ def test_k_split_gemm_matches_reference(case):
         cfgs = [(16, 64, 256, 8, 1, 1, 16, 8, 0, 0, 0, 0, 4), (16, 32, 256, 8, 1, 1, 16, 8, 0, 0, 0, 0, 2)]
     for vals in cfgs:
         cfg = MatmulConfig(*vals)
-        first = None
-        for _ in range(2):
-            out = _run_with_config(fn, args, cfg).float()
-            if tol == 1e-5:
-                close_f32(out, ref, what=f"{case} {vals}")
-            else:
-                close_lowp(out, ref, tol=tol, what=f"{case} {vals}")
-            if first is None:
-                first = out
-            else:
-                assert torch.equal(out, first), (case, vals)      # fixed summation order
+        outs = [o.float() for o in _run_with_config(fn, args, cfg, calls=3)]
+        if tol == 1e-5:
+            close_f32(outs[0], ref, what=f"{case} {vals}")
+        else:
+            close_lowp(outs[0], ref, tol=tol, what=f"{case} {vals}")
+        for out in outs[1:]:
+            assert torch.equal(out, outs[0]), (case, vals)      # fixed summation order
 
 
 DIRECT_CFGS = [(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
