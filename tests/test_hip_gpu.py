@@ -1519,6 +1519,32 @@ def test_on_device_autotune_times_candidates_and_persists_the_winner(dt, monkeyp
     assert again.compiled(x, w, b).matmul_configs[0] == cp.matmul_configs[0]
 
 
+def test_bf16_gemm_gelu_epilogue_is_within_its_bound_of_the_exact_gelu():
+    """A bf16 GEMM whose epilogue applies gelu uses tj_gelu16 (erf by A&S 7.1.25).  With
+    identity weights each product is its input exactly, so over every bf16 value of
+    magnitude 2^-100 to 8 (smaller inputs would give fp32 denormals) each output must be
+    the exact gelu of its input to within half a bf16 unit plus the formula's bound,
+    1.3e-5 |x|."""
+    pos = torch.arange(0x0D80, 0x4101, dtype=torch.int32)                # bf16 in [2^-100, 8]
+    bits = torch.cat([pos, pos | 0x8000, torch.zeros(1, dtype=torch.int32)])
+    vals = bits.to(torch.int16).view(torch.bfloat16)
+    n = -(-vals.numel() // 256) * 256
+    x = torch.zeros(n, dtype=torch.bfloat16)
+    x[:vals.numel()] = vals
+    a = x.reshape(-1, 256).to(DEV)
+    w = torch.eye(256, dtype=torch.bfloat16, device=DEV)
+    f = tj.jit(lambda p, q: tj.gelu(tj.linear(p, q)))
+    out = f(a, w)
+    assert "tj_gelu16(" in f.compiled(a, w).source.split("tj_gelu16(float x)")[1]
+    xd = a.double().cpu()
+    exact = 0.5 * xd * torch.special.erfc(-xd / math.sqrt(2.0))
+    err = (out.double().cpu() - exact).abs()
+    bound = 2.0 ** -8 * exact.abs() + 1.3e-5 * xd.abs() + 1e-30
+    worst = int(torch.argmax(err - bound))
+    assert bool((err <= bound).all()), (float(xd.reshape(-1)[worst]), float(out.reshape(-1)[worst]),
+                                        float(exact.reshape(-1)[worst]))
+
+
 @pytest.mark.parametrize("case", ["f32_residual", "f32_ragged_gelu", "bf16_batched", "skinny_bias_gelu"])
 def test_k_split_gemm_matches_reference(case):
     """K split over workgroups: fp32 partial tiles in the arena workspace, summed (in a
