@@ -873,13 +873,47 @@ def _gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str,
     L.append(f"  const unsigned int arow = wm * {BM // WM}u + (lane % {MI}u);")
     L.append(f"  const unsigned int brow = wn * {BN // WN}u + (lane % {MI}u);")
     L.append(f"  const unsigned int kofs = (lane / {MI}u) * {KPL}u;")
+    if dt == DType.f32:
+        L.append(f"  const unsigned int kofs4 = (lane / {MI}u) * 4u;")
 
     KS = BK // KI
+
+    def compute_lines_f32(buf: str) -> list[str]:
+        """fp32 MFMAs of one K step.  An fp32 MFMA takes one k per lane group (16x16x4:
+        lanes l and l + 16 hold k and k + 1), so reading its operands one 4-byte LDS read
+        per MFMA leaves the wave waiting on LDS latency.  Instead lane group g reads 4
+        consecutive k (one 16-byte read) and the 4 MFMAs of a group take element j of
+        them: MFMA j sums A[i][g*4 + j] * B[n][g*4 + j] over the groups g, so the 4 of
+        them together cover every k of the group exactly once (A and B share the
+        mapping; only the order of the fp32 additions changes).  Reads of the next
+        group are issued before the MFMAs of this one."""
+        KG = 4 * KI                                 # k per 16-byte read group: 16 (16x16x4) or 8 (32x32x2)
+        NG = BK // KG
+        def frag_loads(slot: str, gi: str) -> list[str]:
+            return ["#pragma unroll",
+                    f"    for (int x = 0; x < {TMW}; ++x) fa[{slot}][x] = *(const tj_f32x4*)&As[{buf}][arow + x * {MI}u][{gi} * {KG} + kofs4];",
+                    "#pragma unroll",
+                    f"    for (int y = 0; y < {TNW}; ++y) fb[{slot}][y] = *(const tj_f32x4*)&Bs[{buf}][brow + y * {MI}u][{gi} * {KG} + kofs4];"]
+        out = ["  {", f"    tj_f32x4 fa[2][{TMW}], fb[2][{TNW}];"]
+        out += frag_loads("0", "0")
+        out += ["#pragma unroll", f"  for (int gi = 0; gi < {NG}; ++gi) {{"]
+        if NG > 1:
+            out.append(f"    if (gi + 1 < {NG}) {{")
+            out += ["  " + x for x in frag_loads("(gi + 1) & 1", "(gi + 1)")]
+            out.append("    }")
+        out.append("    __builtin_amdgcn_sched_barrier(0);")
+        out += ["#pragma unroll", "    for (int j = 0; j < 4; ++j)", "#pragma unroll",
+                f"      for (int x = 0; x < {TMW}; ++x)", "#pragma unroll",
+                f"        for (int y = 0; y < {TNW}; ++y) acc[x][y] = {builtin}(fa[gi & 1][x][j], fb[gi & 1][y][j], acc[x][y], 0, 0, 0);",
+                "    __builtin_amdgcn_sched_barrier(0);", "  }", "  }"]
+        return out
 
     def compute_lines(buf: str) -> list[str]:
         """MFMAs of one K step.  Fragment registers are double buffered: the LDS reads
         of sub-step ks+1 are issued before the MFMAs of ks, so LDS latency overlaps
         the matrix cores instead of stalling them."""
+        if dt == DType.f32 and BK % (4 * KI) == 0:
+            return compute_lines_f32(buf)
         def frag_loads(slot: str, ks: str) -> list[str]:
             return ["#pragma unroll",
                     f"    for (int x = 0; x < {TMW}; ++x) fa[{slot}][x] = *(const {opvec}*)&As[{buf}][arow + x * {MI}u][{ks} * {KI} + kofs];",
