@@ -1645,6 +1645,32 @@ def test_direct_lds_gemm_matches_reference(case, dtype):
             close_lowp(out, ref, what=f"{case} {dtype} {cfg}")
 
 
+REF_BENCH = {
+    # the reference GPU benchmark's workloads at hidden D (reference benchmarks/bench.py:20-52)
+    "bias_gelu": (lambda x, b: tj.gelu(x + b), lambda T, D: [(T, 4 * D), (4 * D,)], [1.0, 1.0]),
+    "softmax": (lambda t: tj.softmax(t), lambda T, D: [(8, min(T, 2048), min(T, 2048))], [3.0]),
+    "layernorm": (lambda x, g, b: tj.layer_norm(x, g, b), lambda T, D: [(T, D), (D,), (D,)], [1.0, 1.0, 1.0]),
+    "rmsnorm": (lambda x, g: tj.rms_norm(x, g), lambda T, D: [(T, D), (D,)], [1.0, 1.0]),
+    "linear_gelu": (lambda x, w, b: tj.gelu(tj.linear(x, w, b)), lambda T, D: [(T, D), (4 * D, D), (4 * D,)],
+                    [1.0, 0.03, 0.03]),
+}
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("seq", [256, 4096])
+@pytest.mark.parametrize("name", sorted(REF_BENCH))
+def test_reference_benchmark_workloads_vs_oracle(name, seq, dt):
+    """The workloads the reference GPU table times (hidden 1024, seq 256 and 4096), as
+    bench.py's reference_gpu_table runs them, against the fp32 oracle."""
+    fn, shapes, scale = REF_BENCH[name]
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    gen = torch.Generator(device=DEV).manual_seed(seq)
+    args = [(torch.randn(s_, device=DEV, generator=gen) * c).to(tdt) for s_, c in zip(shapes(seq, 1024), scale)]
+    print(f"reference workload {name} seq {seq} {dt}", flush=True)
+    # fp32 GEMM: a 1024-term dot product per output
+    check_vs_oracle(fn, *args, scale=1e-5 * (2 if name == "linear_gelu" else 1))
+
+
 @pytest.mark.parametrize("dt,seq", [("bf16", 256), ("bf16", 1024), ("bf16", 4096), ("f32", 256), ("f32", 4096)])
 def test_reference_table_mlp_block_on_its_packaged_tiles(dt, seq):
     """The reference benchmark's mlp_block at hidden 1024 (reference benchmarks/bench.py:
