@@ -130,7 +130,11 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
         # direct-to-LDS tiles: 16-bit operands, 128-byte K rows (TK 64), 32x32x16 or
         # 16x16x32 MFMAs with wave tiles whose row bases are multiples of 32 (the LDS
         # swizzle's period), 8-row DMA blocks per wave and no other schedule
-        ok = (dt in (DType.bf16, DType.f16) and cfg.TK == 64 and cfg.MI in (16, 32) and not cfg.PINGPONG
+        # (fp32: tiles up to 128x256 -- at 256x256 each wave's 4 passes of 64 MFMAs per
+        # sub-step need ~500 VGPRs, spill in the persistent form and take ~80 s to compile)
+        ok = (((dt in (DType.bf16, DType.f16) and cfg.TK == 64 and cfg.MI in (16, 32))
+               or (dt == DType.f32 and cfg.TK == 32 and cfg.MI == 16 and cfg.TM * cfg.TN <= 128 * 256))
+              and not cfg.PINGPONG
               and not cfg.INTERLEAVE and cfg.SPLIT_K == 1 and cfg.WM * cfg.WN == cfg.num_warps
               and cfg.TM % (cfg.WM * 32) == 0 and cfg.TN % (cfg.WN * 32) == 0
               and cfg.TM % (8 * cfg.num_warps) == 0 and cfg.TN % (8 * cfg.num_warps) == 0
@@ -141,8 +145,8 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
             M, N, K, tb = matmul_dims(mm)
             a, b = mm.inputs
             # buffer descriptors: byte offsets (rows padded to the tile) and ranges in int32
-            ok = (tb and K % 64 == 0 and a.dtype == b.dtype == dt
-                  and (M + cfg.TM) * K * 2 < 2**31 and (N + cfg.TN) * K * 2 < 2**31)
+            ok = (tb and K % cfg.TK == 0 and a.dtype == b.dtype == dt
+                  and (M + cfg.TM) * K * dt.itemsize < 2**31 and (N + cfg.TN) * K * dt.itemsize < 2**31)
         if ok and cfg.PERSIST:
             # persistent tile loop: 16x16x32 MFMAs, 4 waves, a multiple of 8 workgroups
             # (XCD order), an epilogue staging array of its own beside the two stages,
@@ -156,8 +160,8 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
             if ok and mm is not None:
                 M, N, K, _ = matmul_dims(mm)
                 M *= math.prod(mm.shape[:-2])
-                ok = (batch_folds_into_m(mm) and M % cfg.TM == 0 and N % cfg.TN == 0 and K % 128 == 0
-                      and K >= 256 and M * N < 2**31 and M * K * 2 < 2**31)
+                ok = (batch_folds_into_m(mm) and M % cfg.TM == 0 and N % cfg.TN == 0 and K % (2 * cfg.TK) == 0
+                      and K >= 4 * cfg.TK and M * N < 2**31 and M * K * dt.itemsize < 2**31)
         return ok
     if cfg.PINGPONG:
         ks = cfg.TK // ki
@@ -615,6 +619,7 @@ def _gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str,
     TMW, TNW = BM // WM // MI, BN // WN // MI
     lds_t = CTYPE[dt] if dt != DType.f32 else "float"
     esz = dt.itemsize
+    dvec = "tj_f32x4" if dt == DType.f32 else opvec      # a direct-to-LDS fragment read: 16 bytes
     VK = 16 // esz                 # elements per 16-byte global load
     PAD = VK                       # 16 bytes of row padding
     LDK = BK + PAD
@@ -695,7 +700,7 @@ def _gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str,
         G = min(cfg.PERSIST, T)
         persist = {"G": G, "T": T, "K": K, "BM": BM, "BN": BN, "ntm": ntm, "ntn": ntn, "group_m": cfg.GROUP_M,
                    "pre": pre, "epi": body, "stores": stores, "k1_early": early}
-        L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persist)
+        L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, dvec, builtin, persist, esz)
         L.append("}")
         lds = 2 * (BM + BN) * 128 + cfg.num_warps * 16 * TNW * MI * 4
         meta = {"family": "matmul", "config": cfg.as_dict(), "dtype": dt.value, "M": M // batch, "N": N, "K": K,
@@ -703,7 +708,7 @@ def _gen_matmul(g: KernelGen, cfg: MatmulConfig, suffix: str = "") -> tuple[str,
                 "epilogue": "lds-staged", "persistent": G}
         return "\n".join(L), Launch(fname, (G, 1, 1), (THREADS, 1, 1), 0, meta)
     if cfg.DIRECT:
-        L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin)
+        L += direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, dvec, builtin, esz=esz)
         return _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW,
                               TNW, NACC, THREADS, 0, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
 
@@ -1182,7 +1187,8 @@ def _lgkmcnt_only(n: int) -> str:
     return hex(0xC07F | (n << 8))
 
 
-def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persist: dict | None = None) -> list[str]:
+def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persist: dict | None = None,
+                      esz: int = 2) -> list[str]:
     """Main loop for one wave per SIMD with tiles loaded straight into LDS (``DIRECT``).
 
     ``buffer_load_dwordx4 ... lds`` moves 16 bytes per lane from HBM/L2 into LDS
@@ -1221,13 +1227,22 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persis
     on (stage 0 is free from that tile's barrier, as for any tile kt+2), its second
     into stage 1 once the last tile's reads are done, and the epilogue stages through
     an LDS array of its own, so the next tile's MFMAs start without a load wait and the
-    output stores drain under them."""
+    output stores drain under them.
+
+    fp32 (``esz`` 4, 16x16x4 MFMAs, 32-deep K tiles: the same 128-byte rows): a
+    fragment read brings each lane 4 consecutive k, which feed 4 MFMAs (element j of A
+    and B each; the lane groups' k interleave as in the bf16 layout, for A and B alike),
+    so a sub-step runs 4 passes over the accumulators, j outermost (no two consecutive
+    MFMAs share an accumulator); A fragments are re-read after their last pass."""
     nw = cfg.num_warps
     MI = cfg.MI
-    KI = 16 if MI == 32 else 32               # K per MFMA
-    KS = 64 // KI                             # sub-steps per 64-deep tile
+    f32 = esz == 4
+    KI = 16 if MI == 32 else 32               # bf16 / fp16 K per MFMA
+    KS = 64 // KI                             # sub-steps (64 bytes of K per row for 16x16) per tile
     NACC = MI * MI // 64
-    dsp = 64 // MI                            # MFMAs per 64 cycles: 32x32x16 takes 32, 16x16x32 16
+    # MFMAs per 64 cycles: 32x32x16 takes 32 cycles, 16x16x32 16, 16x16x4 f32 32
+    dsp = 2 if f32 else 64 // MI
+    passes = 4 if f32 else 1                  # MFMAs per fragment pair and sub-step
     # Barrier that publishes a stage filled by DMA: each wave first waits for its own
     # DMA loads (vmcnt 0; expcnt and lgkmcnt left at their maxima).  A workgroup-scope
     # fence does not cover loads that write LDS, and the compiler's own vmcnt wait is
@@ -1283,8 +1298,8 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persis
     # compiler treats it as a flat access that may touch LDS and then waits for every
     # outstanding LDS read (lgkmcnt 0) wherever one fragment is needed.
     if not persist:
-        L.append(f"  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, {M * K * 2}, 0x00020000);")
-        L.append(f"  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, {N * K * 2}, 0x00020000);")
+        L.append(f"  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, {M * K * esz}, 0x00020000);")
+        L.append(f"  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, {N * K * esz}, 0x00020000);")
     # persistent: each tile's descriptors start at its first row, so the lane offsets
     # are the same for every tile
     for op, cnt, rows in (("A", a_cnt, "m0"), ("B", b_cnt, "n0")):
@@ -1292,7 +1307,8 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persis
         base = "" if persist else f"{rows} + "
         for i in range(cnt):
             q = f"({i * nw}u + wv)"
-            L.append(f"  vo{op}[{i}] = (({base}{q} * 8u + drow) * {K}u + ((lane & 7u) ^ drow ^ ({q} & 3u)) * 8u) * 2u;")
+            L.append(f"  vo{op}[{i}] = (({base}{q} * 8u + drow) * {K}u + ((lane & 7u) ^ drow ^ ({q} & 3u)) * {16 // esz}u)"
+                     f" * {esz}u;")
 
     def dma(kt: str, stage: int, nxt: bool = False) -> list[str]:
         """The DMA loads of tile ``kt`` into ``stage``, one statement per load (``nxt``:
@@ -1320,9 +1336,13 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persis
                 for y in range(TNW)]
         if MI == 32:
             return list(enumerate([a_rd[0]] + b_rd + a_rd[1:]))
-        return [(4 * y + 2, r) for y, r in enumerate(b_rd)] + [(x * TNW + TNW - 1, r) for x, r in enumerate(a_rd)]
+        last = (passes - 1) * nmm
+        return [(4 * y + 2, r) for y, r in enumerate(b_rd)] + [(last + x * TNW + TNW - 1, r) for x, r in enumerate(a_rd)]
 
     def mfmas(buf: int) -> list[str]:
+        if f32:
+            return [f"acc[{x}][{y}] = {builtin}({fa_ref(buf, x)}[{j}], fb[{buf}][{y}][{j}], acc[{x}][{y}], 0, 0, 0);"
+                    for j in range(passes) for x in range(TMW) for y in range(TNW)]
         return [f"acc[{x}][{y}] = {builtin}({fa_ref(buf, x)}, fb[{buf}][{y}], acc[{x}][{y}], 0, 0, 0);"
                 for x in range(TMW) for y in range(TNW)]
 
@@ -1332,12 +1352,13 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persis
         loads present the 32x32 reads move to the odd slots), then the matching
         sched_group_barrier sequence."""
         slots: dict[int, list[tuple[int, str]]] = {}
+        nm_all = passes * nmm
         for i, ld in enumerate(loads):
-            slots.setdefault(min(i * dsp, nmm - 1), []).append((SG_VMEM_READ, ld))
+            slots.setdefault(min(i * dsp, nm_all - 1), []).append((SG_VMEM_READ, ld))
         for s, rd in reads:
             if MI == 32 and loads:
                 s = 2 * s + 1
-            slots.setdefault(min(s, nmm - 1), []).append((SG_DS_READ, rd))
+            slots.setdefault(min(s, nm_all - 1), []).append((SG_DS_READ, rd))
         code, sched = [], []
         for i, mf in enumerate(mfmas(buf)):
             code.append(mf)
@@ -1387,7 +1408,7 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persis
         return [ind + x for x in out]
 
     if persist:
-        return L + persistent_direct_lines(persist, KT, n_batch, dma, frag_reads, tile, opvec, MI, TMW, TNW)
+        return L + persistent_direct_lines(persist, KT, n_batch, dma, frag_reads, tile, opvec, MI, TMW, TNW, esz)
     # prologue: tiles 0 and 1 in flight, wait for tile 0 only (the 2nd batch may
     # stay outstanding: vmcnt <= its load count)
     L += ["  " + x for x in dma("0", 0)]
@@ -1418,7 +1439,7 @@ def direct_loop_lines(cfg, M, N, K, BM, BN, TMW, TNW, KT, opvec, builtin, persis
 
 
 def persistent_direct_lines(p: dict, KT: int, n_batch: int, dma, frag_reads, tile, opvec: str, MI: int, TMW: int,
-                            TNW: int) -> list[str]:
+                            TNW: int, esz: int = 2) -> list[str]:
     """Tile loop of the persistent direct-to-LDS kernel (after the shared set-up of
     ``direct_loop_lines``).
 
@@ -1444,7 +1465,7 @@ def persistent_direct_lines(p: dict, KT: int, n_batch: int, dma, frag_reads, til
 
     def rsrc(name: str, base: str, row0: str, rows: int) -> str:
         return (f"const __amdgpu_buffer_rsrc_t {name} = __builtin_amdgcn_make_buffer_rsrc("
-                f"(void*)({base} + (unsigned long)({row0}) * {K}u), (short)0, {rows * K * 2}, 0x00020000);")
+                f"(void*)({base} + (unsigned long)({row0}) * {K}u), (short)0, {rows * K * esz}, 0x00020000);")
 
     L = tile_order_lines(ntm, ntn, gm, BM, BN, vid="blockIdx.x", names=("m0i", "n0i"), sfx="i")
     L += ["  unsigned int v = blockIdx.x, m0 = m0i, n0 = n0i;",

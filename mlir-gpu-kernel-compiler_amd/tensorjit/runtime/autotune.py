@@ -124,6 +124,11 @@ HIP_CANDIDATES: list[MatmulConfig] = [
 
 # fp32 candidates (MFMA 32x32x2 / 16x16x4 f32)
 HIP_F32_CANDIDATES: list[MatmulConfig] = [
+    # direct-to-LDS (32-deep K tiles: the bf16 kernel's 128-byte rows), 16x16x4 MFMAs
+    MatmulConfig(128, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1),
+    MatmulConfig(128, 256, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1),
+    MatmulConfig(256, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1),
+    MatmulConfig(128, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, CU_COUNT),
     MatmulConfig(128, 128, 16, 4, 2, 2, 32),
     MatmulConfig(128, 128, 32, 4, 2, 2, 32),
     MatmulConfig(128, 64, 32, 4, 2, 2, 32),

@@ -295,6 +295,34 @@ def test_persistent_gemm_launch_lds_and_waits():
     assert "persistent" not in l.meta and l.grid == (16, 8, 4)
 
 
+def test_fp32_direct_to_lds_tiles():
+    """fp32 operands take the direct-to-LDS schedule with 32-deep K tiles (the bf16 kernel's
+    128-byte rows) and 16x16x4 MFMAs: NT layout, K a multiple of 32, tiles up to 128x256.
+    Each 16-byte fragment read feeds 4 MFMAs (element j of A and B), j the outer pass."""
+    def prog(M, N, K, tb=True):
+        fn = (lambda x, w: tj.linear(x, w)) if tb else (lambda x, w: tj.matmul(x, w))
+        shapes = [(M, K), (N, K) if tb else (K, N)]
+        return C.lower(tj.trace(fn, [TensorType(s, DType.f32) for s in shapes]), "hip")
+
+    d128 = MatmulConfig(128, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1)
+    p = prog(4096, 1024, 4096)
+    mm = p.kernels[0].anchor
+    assert hb.config_ok(d128, DType.f32, mm)
+    assert hb.config_ok(MatmulConfig(128, 256, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1), DType.f32, mm)
+    assert hb.config_ok(MatmulConfig(128, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, 256), DType.f32, mm)
+    assert not hb.config_ok(MatmulConfig(256, 256, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1), DType.f32, mm)
+    assert not hb.config_ok(MatmulConfig(128, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1), DType.f32, mm)
+    assert not hb.config_ok(MatmulConfig(128, 128, 32, 4, 2, 2, 32, 1, 8, 0, 0, 1), DType.f32, mm)
+    assert not hb.config_ok(d128, DType.f32, prog(512, 512, 520).kernels[0].anchor)          # K % 32
+    assert not hb.config_ok(d128, DType.f32, prog(512, 512, 512, tb=False).kernels[0].anchor)  # NN
+    src, _ = hb.generate(p, {0: d128})
+    body = src[len(hb.PRELUDE):]
+    assert "*(const tj_f32x4*)(As0 + arow" in body
+    assert "__builtin_amdgcn_mfma_f32_16x16x4f32(fa[0][3], fb[0][0][3]" in body
+    assert "__builtin_amdgcn_raw_ptr_buffer_load_lds" in body
+    hb.compile_source(src, "gfx950")
+
+
 def test_k_split_gemm_has_a_partial_and_a_sum_launch():
     """K split over workgroups: the partial-product launch owns a workspace of
     batch x splits x M x N fp32 values (placed after the planned intermediates in the

@@ -1399,13 +1399,14 @@ def test_every_bf16_tile_config_is_exact_on_integer_data(tb):
 @pytest.mark.parametrize("tb", [True, False])
 def test_every_fp32_tile_config_is_exact_on_integer_data(tb):
     """Every fp32 candidate tiling -- 32x32x2 and 16x16x4 MFMA tiles, K split over
-    workgroups -- on shapes with ragged M / N / K edges, exact on small-integer data (every
-    partial sum is an integer below 2^24, so any summation order gives the same bits)."""
+    workgroups, direct-to-LDS tiles -- on shapes with ragged M / N / K edges, exact on
+    small-integer data (every partial sum is an integer below 2^24, so any summation order
+    gives the same bits)."""
     from tensorjit.backends import hip_backend as hb
     from tensorjit.runtime.autotune import HIP_F32_CANDIDATES
 
     torch.manual_seed(0)
-    mi32 = ksplit = 0
+    mi32 = ksplit = direct = 0
     for m, n, kk in [(300, 520, 136), (100, 72, 40), (130, 260, 1024)]:
         a = torch.randint(-2, 3, (m, kk), device=DEV).float()
         b = torch.randint(-2, 3, (n, kk) if tb else (kk, n), device=DEV).float()
@@ -1421,14 +1422,15 @@ def test_every_fp32_tile_config_is_exact_on_integer_data(tb):
             tried += 1
             mi32 += cfg.MI == 32
             ksplit += cfg.KSPLIT > 1
+            direct += cfg.DIRECT
         assert tried >= 4, (m, n, kk)
-    assert mi32 >= 4 * 3 and ksplit >= 4
+    assert mi32 >= 4 * 3 and ksplit >= 4 and direct >= (3 if tb else 0)
 
 
 def test_config4_fp32_full_size_on_its_packaged_tile_vs_oracle():
     """Config 4's fp32 variant, gelu(x @ w.T + bias) at 4096^3, through ``tj.jit`` on the tile
-    the packaged table holds for it (128x128x32 with 32x32x2 MFMAs): the oracle on a 64-row
-    sample at the fp32 bound, and a float64 product on the whole output."""
+    the packaged table holds for it (direct-to-LDS 128x128x32 with 16x16x4 MFMAs): the
+    oracle on a 64-row sample at the fp32 bound, and a float64 product on the whole output."""
     from tensorjit.backends import hip_backend as hb
     from tensorjit.runtime.autotune import MatmulConfig
     from tensorjit.runtime.cache import packaged_entry
@@ -1443,7 +1445,7 @@ def test_config4_fp32_full_size_on_its_packaged_tile_vs_oracle():
     cp = f.compiled(x, w, bias)
     entry = packaged_entry(hb.matmul_key(cp.program.kernels[0], cp.arch))
     assert entry is not None and cp.matmul_configs[0] == MatmulConfig.from_dict(entry["config"])
-    assert cp.matmul_configs[0].MI == 32
+    assert cp.matmul_configs[0].DIRECT == 1 and cp.matmul_configs[0].MI == 16
     rows = torch.arange(0, 4096, 64, device=DEV)
     (orc,) = oracle.run(fn, x[rows].cpu(), w.cpu(), bias.cpu())
     close_f32(out[rows], orc)
@@ -1590,9 +1592,12 @@ def test_k_split_gemm_matches_reference(case):
 DIRECT_CFGS = [(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
                (256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1),
                (128, 64, 64, 4, 2, 2, 16, 1, 4, 0, 0, 1), (128, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1)]
+# fp32 operands: 32-deep K tiles (the same 128-byte rows), 16x16x4 MFMAs
+DIRECT_F32_CFGS = [(128, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1), (256, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1),
+                   (128, 256, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1)]
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("case", ["one_tile", "two_tiles", "three_tiles", "ragged", "batched", "shared_weight",
                                   "bias_gelu", "residual"])
 def test_direct_lds_gemm_matches_reference(case, dtype):
@@ -1637,12 +1642,15 @@ def test_direct_lds_gemm_matches_reference(case, dtype):
         fn = lambda x, y: tj.linear(x, y)
         args, ref = [a, b], a.float() @ b.float().t()
     mm = C_lower(fn, *args).kernels[0].anchor
-    for vals in DIRECT_CFGS:
+    for vals in DIRECT_F32_CFGS if dtype == torch.float32 else DIRECT_CFGS:
         cfg = MatmulConfig(*vals)
         assert hb.config_ok(cfg, hb.compute_dtype(mm), mm), (case, cfg)
         for _ in range(2):      # twice: a race between loads and reads shows as run-to-run differences
             out = _run_with_config(fn, args, cfg).float()
-            close_lowp(out, ref, what=f"{case} {dtype} {cfg}")
+            if dtype == torch.float32:
+                close_f32(out, ref, what=f"{case} {dtype} {cfg}")
+            else:
+                close_lowp(out, ref, what=f"{case} {dtype} {cfg}")
 
 
 REF_BENCH = {
