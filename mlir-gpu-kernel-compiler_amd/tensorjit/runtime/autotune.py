@@ -129,6 +129,7 @@ HIP_F32_CANDIDATES: list[MatmulConfig] = [
     MatmulConfig(128, 256, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1),
     MatmulConfig(256, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1),
     MatmulConfig(128, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1, 1, CU_COUNT),
+    MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1),
     MatmulConfig(128, 128, 16, 4, 2, 2, 32),
     MatmulConfig(128, 128, 32, 4, 2, 2, 32),
     MatmulConfig(128, 64, 32, 4, 2, 2, 32),
