@@ -86,6 +86,10 @@ HIP_CANDIDATES: list[MatmulConfig] = [
     MatmulConfig(256, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1),
     MatmulConfig(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
     MatmulConfig(256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),
+    # mid-size products (a few hundred 256x256 tiles or fewer): smaller direct tiles fill the CUs
+    MatmulConfig(128, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1),
+    MatmulConfig(128, 64, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1),
+    MatmulConfig(64, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1),
     MatmulConfig(256, 256, 64, 8, 2, 4, 32, 1, 8, 3),
     MatmulConfig(256, 256, 64, 8, 4, 2, 32, 1, 8, 3),
     MatmulConfig(256, 256, 32, 8, 2, 4, 32, 1, 8, 2),

@@ -1594,7 +1594,7 @@ DIRECT_CFGS = [(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 
                (128, 64, 64, 4, 2, 2, 16, 1, 4, 0, 0, 1), (128, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1)]
 # fp32 operands: 32-deep K tiles (the same 128-byte rows), 16x16x4 MFMAs
 DIRECT_F32_CFGS = [(128, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1), (256, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1),
-                   (128, 256, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1)]
+                   (128, 256, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1), (64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
