@@ -679,8 +679,9 @@ def mfma_sustained(torch) -> dict:
 def profile_set(torch, dev, steps, which="all") -> None:
     """Kernels for rocprofv3 runs.  ``all``: the headline kernel, a plain copy-like
     calibration kernel of known traffic (y = x + 0.5, fp32 [16384,4096]: 256 MiB
-    read + 256 MiB written), the row configs, the config-4 bf16 GEMM and its decode
-    shape, config 5's bf16 softmax rows and fused attention, ``steps`` launches each.
+    read + 256 MiB written), the row configs, the config-4 bf16 GEMM, its decode
+    shape and its fp32 variant, config 5's bf16 softmax rows and fused attention,
+    ``steps`` launches each.
     ``c5``: ``steps`` calls of config 5's whole layer (direct launches), for a kernel
     trace of the layer in its own context.  ``c1``: ``steps`` calls of config 1's MLP
     block with direct launches, then ``steps`` with hipGraph replay, back to back (the
@@ -737,6 +738,11 @@ def profile_set(torch, dev, steps, which="all") -> None:
     bs = (0.02 * torch.randn(8192, device=dev, generator=gen)).bfloat16()
     run(_fn_gemm, [xs, ws, bs])
     del xs, ws, bs
+    xf = torch.randn(4096, 4096, device=dev, generator=gen)
+    wf = 0.02 * torch.randn(4096, 4096, device=dev, generator=gen)
+    bf = 0.02 * torch.randn(4096, device=dev, generator=gen)
+    run(_fn_gemm, [xf, wf, bf])
+    del xf, wf, bf
     s5 = (torch.randn(262144, 2048, device=dev, generator=gen) * 3).bfloat16()
     run(_fn_softmax, [s5])
     del s5
