@@ -36,14 +36,18 @@ DIRECT16 = MatmulConfig(256, 256, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1)
 DIRECT16_N128 = MatmulConfig(256, 128, 64, 4, 2, 2, 16, 1, 8, 0, 0, 1)
 ALL_DIRECT = [DIRECT, DIRECT_N128, DIRECT16, DIRECT16_N128]
 DIRECT_IDS = ["256x256", "256x128", "256x256_mi16", "256x128_mi16"]
+# fp32 operands: 32-deep K tiles (the same 128-byte rows), 16x16x4 MFMAs
+F32_DIRECT = [MatmulConfig(128, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1), MatmulConfig(256, 128, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1),
+              MatmulConfig(128, 256, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1), MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 1)]
+F32_IDS = ["f32_128x128", "f32_256x128", "f32_128x256", "f32_64x64"]
 
 
-def _source(cfg, M=256, N=256, K=64, epi="plain"):
+def _source(cfg, M=256, N=256, K=64, epi="plain", dt=DType.bf16):
     fns = {"plain": (lambda x, w: tj.linear(x, w), [(M, K), (N, K)]),
            "residual": (lambda x, w, r: tj.linear(x, w) + r, [(M, K), (N, K), (M, N)]),
            "bias_gelu": (lambda x, w, b: tj.gelu(tj.linear(x, w, b)), [(M, K), (N, K), (N,)])}
     fn, shapes = fns[epi]
-    p = C.lower(tj.trace(fn, [TensorType(s, DType.bf16) for s in shapes]), "hip")
+    p = C.lower(tj.trace(fn, [TensorType(s, dt) for s in shapes]), "hip")
     return hb.generate(p, {0: cfg})
 
 
@@ -54,12 +58,16 @@ def _c_eval(expr: str, env: dict) -> int:
     return int(eval(py, {}, dict(env))) & 0xFFFFFFFF
 
 
-@pytest.mark.parametrize("cfg", ALL_DIRECT, ids=DIRECT_IDS)
+@pytest.mark.parametrize("cfg", ALL_DIRECT + F32_DIRECT, ids=DIRECT_IDS + F32_IDS)
 def test_dma_placement_and_fragment_reads_agree(cfg):
-    K = 64
-    src, launches = _source(cfg, N=cfg.TN, K=K)
+    """(fp32: the same 128-byte rows hold 32 k; a lane's 16-byte chunk holds 4 consecutive k,
+    element j of which feeds the group's j-th 16x16x4 MFMA, so the (row, chunk) checks are
+    the bf16 16x16x32 kernel's.)"""
+    f32 = cfg.TK == 32
+    esz, K = (4, 32) if f32 else (2, 64)
+    src, launches = _source(cfg, M=cfg.TM, N=cfg.TN, K=K, dt=DType.f32 if f32 else DType.bf16)
     nw, WM, WN, MI = cfg.num_warps, cfg.WM, cfg.WN, cfg.MI
-    kc = 2 if MI == 32 else 4                     # 16-byte chunks of K per MFMA
+    kc = 2 if MI == 32 else 4                     # 16-byte chunks of K per sub-step
     fofs = {int(i): e for i, e in re.findall(r"  fofs\[(\d+)\] = (.*);\n", src)}
     assert sorted(fofs) == list(range(4))
     for op, rows, wdim, rowdim in (("A", cfg.TM, WM, cfg.TM // WM), ("B", cfg.TN, WN, cfg.TN // WN)):
@@ -73,20 +81,24 @@ def test_dma_placement_and_fragment_reads_agree(cfg):
                 env = {"m0": 0, "n0": 0, "wv": wv, "lane": lane, "drow": lane >> 3}
                 for lds_expr, i in dst:
                     off = _c_eval(vo[i], env)                # global byte offset of this lane's 16 bytes
-                    g_row, g_col = divmod(off // 2, K)
-                    assert g_col % 8 == 0
+                    g_row, g_col = divmod(off // esz, K)
+                    assert g_col % (16 // esz) == 0
                     slot = (_c_eval(lds_expr, env) + lane * 16) // 16
                     assert slot not in slots, (op, wv, lane, i)
-                    slots[slot] = (g_row, g_col // 8)
-        assert sorted(slots) == list(range(rows * K * 2 // 16)), op      # every 16-byte slot filled once
+                    slots[slot] = (g_row, g_col // (16 // esz))
+        assert sorted(slots) == list(range(rows * K * esz // 16)), op      # every 16-byte slot filled once
         # fragment reads: lane l of wave (wm, wn), tile t, sub-step ks wants row base + MI t + l % MI,
         # 16-byte chunk kc ks + l / MI (8 bf16 of k per lane)
         fsw = re.search(r"const unsigned int fsw = (.*);", src).group(1)
         base = re.search(rf"const unsigned int {'arow' if op == 'A' else 'brow'} = (.*);", src).group(1)
-        reads = re.findall(rf"f{'a' if op == 'A' else 'b'}(?:\[\d\])?\[(\d)\] = \*\(const tj_bf16x8\*\)\({op}s0 \+ "
+        vt = "tj_f32x4" if f32 else "tj_bf16x8"
+        reads = re.findall(rf"f{'a' if op == 'A' else 'b'}(?:\[\d\])?\[(\d)\] = \*\(const {vt}\*\)\({op}s0 \+ "
                            rf"{'arow' if op == 'A' else 'brow'} \+ fofs\[(\d)\] \+ (\d+)u\);", src)
         # every (tile, sub-step) pair is read, each with its own offset register
         assert len(set(reads)) == (rowdim // MI) * (64 // (8 * kc)), (op, sorted(set(reads)))
+        if f32:
+            # every fp32 MFMA takes element j of a fragment pair read with the same chunk offsets
+            assert re.search(r"mfma_f32_16x16x4f32\(fa\[\d+\]\[3\], fb\[\d\]\[\d+\]\[3\]", src)
 
         def lane_env(lane, w):
             env = {"fr": lane & (MI - 1), "fh": lane // MI, "wm": w, "wn": w}
