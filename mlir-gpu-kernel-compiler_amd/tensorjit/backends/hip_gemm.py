@@ -127,11 +127,12 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
     if cfg.INTERLEAVE and (cfg.PINGPONG or (cfg.TK // ki) % 2):
         return False
     if cfg.DIRECT:
-        # direct-to-LDS tiles: 16-bit operands, 128-byte K rows (TK 64), 32x32x16 or
-        # 16x16x32 MFMAs with wave tiles whose row bases are multiples of 32 (the LDS
-        # swizzle's period), 8-row DMA blocks per wave and no other schedule
-        # (fp32: tiles up to 128x256 -- at 256x256 each wave's 4 passes of 64 MFMAs per
-        # sub-step need ~500 VGPRs, spill in the persistent form and take ~80 s to compile)
+        # direct-to-LDS tiles: 128-byte K rows -- 16-bit operands with TK 64 and 32x32x16
+        # or 16x16x32 MFMAs, or fp32 with TK 32 and 16x16x4 MFMAs -- wave tiles whose row
+        # bases are multiples of 32 (the LDS swizzle's period), 8-row DMA blocks per wave
+        # and no other schedule.  fp32 tiles stop at 128x256: at 256x256 each wave's 4
+        # passes of 64 MFMAs per sub-step need ~500 VGPRs, spill in the persistent form
+        # and take ~80 s to compile.
         ok = (((dt in (DType.bf16, DType.f16) and cfg.TK == 64 and cfg.MI in (16, 32))
                or (dt == DType.f32 and cfg.TK == 32 and cfg.MI == 16 and cfg.TM * cfg.TN <= 128 * 256))
               and not cfg.PINGPONG
@@ -148,7 +149,7 @@ def config_ok(cfg: MatmulConfig, dt: DType, mm: Node | None = None) -> bool:
             ok = (tb and K % cfg.TK == 0 and a.dtype == b.dtype == dt
                   and (M + cfg.TM) * K * dt.itemsize < 2**31 and (N + cfg.TN) * K * dt.itemsize < 2**31)
         if ok and cfg.PERSIST:
-            # persistent tile loop: 16x16x32 MFMAs, 4 waves, a multiple of 8 workgroups
+            # persistent tile loop: 16x16 MFMAs, 4 waves, a multiple of 8 workgroups
             # (XCD order), an epilogue staging array of its own beside the two stages,
             # wave columns a power of two (a staged output row splits evenly over the 64
             # lanes), whole tiles (no edges), an even number of at least 4 K tiles, and a
