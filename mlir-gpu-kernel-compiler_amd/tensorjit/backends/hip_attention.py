@@ -358,6 +358,54 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         pack4 = ("(unsigned long)(tj_f2h({0}) | (tj_f2h({1}) << 16)) | "
                  "((unsigned long)(tj_f2h({2}) | (tj_f2h({3}) << 16)) << 32)")
 
+    # head dim 128, ping-pong: K and V blocks go straight from memory into LDS (DMA)
+    dma = (pingpong and D == 128 and Dv == 128 and NS == 1
+           and os.environ.get("TENSORJIT_HIP_ATTENTION_DMA", "1") != "0"
+           and Sk * kst * 2 < 2**31 and Sk * vst * 2 < 2**31)
+    if dma:
+        NST = 4
+        lds_decl = [f"  __shared__ __attribute__((aligned(1024))) char {a}{s}[{BKV * 256}];"
+                    for a in ("Ks", "Vs") for s in range(NST)]
+    else:
+        lds_decl = [f"  __shared__ __attribute__((aligned(16))) {T} Ks[{NST}][{BKV}][{DP}];",
+                    f"  __shared__ __attribute__((aligned(16))) {T} Vs[{NST}][{BKV}][{VP}];"]
+
+    def dma_setup_lines() -> list[str]:
+        """Wave w (group gq = w / 4) moves rows gq*32 + (w % 4)*8 + q*4 .. +3 (q = 0, 1) of
+        every K and V block: one ``buffer_load_dwordx4 ... lds`` writes 1 KiB of LDS, four
+        256-byte rows, lane l at byte 16 l.  Rows are not padded; lane l fetches 16-byte
+        chunk (l % 16) ^ f(row) of its row, so position p of a stored row holds chunk
+        p ^ f(row), f = (row >> 1) & 15 for K and ((row >> 1) & 3) << 2 for V.  The offsets
+        (block included) go in the lane's voffset, which the descriptor's range checks:
+        rows past the last key read zeros.  Fragment addresses: K row ``col`` of tile t,
+        chunk 2c + g, sits at (2c + g) ^ f(col) = (g ^ f(col)) ^ 2c; a Vᵀ read's row
+        vr (+ 16 ch, + 8) and chunk 4u + vcl sit at ((4u) ^ f(vr)) + vcl."""
+        return ["  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave), gq = wv / 4u;",
+                f"  const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, {Sk * kst * 2}, 0x00020000);",
+                f"  const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, {Sk * vst * 2}, 0x00020000);",
+                "  unsigned int voK[2], voV[2], dmo[2];",
+                "#pragma unroll",
+                "  for (int q = 0; q < 2; ++q) {",
+                "    dmo[q] = (gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u) * 256u;",
+                "    const unsigned int r = gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u + lane / 16u;",
+                f"    voK[q] = (r * {kst}u + ((lane % 16u) ^ ((r >> 1) & 15u)) * 8u) * 2u;",
+                f"    voV[q] = (r * {vst}u + ((lane % 16u) ^ (((r >> 1) & 3u) << 2)) * 8u) * 2u;",
+                "  }",
+                "  const unsigned int kx = col * 256u + ((g ^ ((col >> 1) & 15u)) << 4);",
+                "  const unsigned int vr = g * 4u + (lane % 16u) / 4u, vsw = ((vr >> 1) & 3u) << 2;",
+                "  const unsigned int vcl = ((lane / 16u) % 2u) * 2u + (lane % 4u) / 2u;",
+                "  unsigned int va[4];",
+                "#pragma unroll",
+                "  for (int u = 0; u < 4; ++u)",
+                "    va[u] = vr * 256u + (lane % 2u) * 8u + ((((unsigned int)u * 4u) ^ vsw) + vcl) * 16u;"]
+
+    def dma_lines(which: str, blk: str, stage: int) -> list[str]:
+        """This wave's two DMA loads of key block ``blk`` (K or V) into ``stage``."""
+        rs, vo, st = ("rsK", "voK", kst) if which == "k" else ("rsV", "voV", vst)
+        arr = "Ks" if which == "k" else "Vs"
+        return [f"__builtin_amdgcn_raw_ptr_buffer_load_lds({rs}, (__attribute__((address_space(3))) void*)"
+                f"({arr}{stage} + dmo[{q}]), 16, {vo}[{q}] + ({blk}) * {BKV * st * 2}u, 0, 0, 0);" for q in range(2)]
+
     # two waves per SIMD: one wave's softmax arithmetic runs under the other's MFMAs;
     # the compiler then keeps everything in 256 VGPRs
     occ = 2
@@ -366,8 +414,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     L = [f'extern "C" __global__ void __launch_bounds__({THREADS}) __attribute__((amdgpu_waves_per_eu({occ}, {occ}))) {fname}(',
          f"    const {T}* __restrict__ in0_p, const {T}* __restrict__ in1_p, const {T}* __restrict__ in2_p,",
          f"    {T}* __restrict__ out0_p{', float* __restrict__ ws_p' if NS > 1 else ''}) {{",
-         f"  __shared__ __attribute__((aligned(16))) {T} Ks[{NST}][{BKV}][{DP}];",
-         f"  __shared__ __attribute__((aligned(16))) {T} Vs[{NST}][{BKV}][{VP}];",
+         *lds_decl,
          "  const unsigned int tid = threadIdx.x, lane = tid % 64u, wave = tid / 64u;",
          "  const unsigned int g = lane / 32u, col = lane % 32u;",
          *_split_tile_lines(nq, batch, NS, KBL, idx_t),
@@ -390,9 +437,12 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
          f"    for (int u = 0; u < {Dv // 32}; ++u) o[q][u] = (tj_f32x16)(0.0f);",
          "    m_run[q] = -__builtin_inff();",
          "    l_run[q] = 0.0f;",
-         "  }",
-         f"  tj_u32x4 rk[{KC}], rv[{VC}];"]
-    if pingpong:
+         "  }"]
+    if dma:
+        L += dma_setup_lines()
+    else:
+        L.append(f"  tj_u32x4 rk[{KC}], rv[{VC}];")
+    if pingpong and not dma:
         L.append("  const unsigned int gq = wave / 4u, gtid = tid % 256u;")
 
     def k_load(blk: str) -> list[str]:
@@ -447,6 +497,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 f"  for (int t = 0; t < {BKV // 32}; ++t) {dst}[q][t] = (tj_f32x16)(0.0f);",
                 "#pragma unroll", f"for (int c = 0; c < {D // 16}; ++c) {{", "#pragma unroll",
                 f"  for (int t = 0; t < {BKV // 32}; ++t) {{",
+                f"    const {opvec} kf = *(const {opvec}*)(Ks{stage} + t * {32 * 256}u + (kx ^ (c * 32u)));" if dma else
                 f"    const {opvec} kf = *(const {opvec}*)&Ks[{stage}][t * 32 + col][c * 16 + g * 8u];",
                 "#pragma unroll",
                 f"    for (int q = 0; q < {QT}; ++q) {dst}[q][t] = {mfma}(kf, qf[q][c], {dst}[q][t], 0, 0, 0);",
@@ -514,6 +565,16 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         """O^T += V^T P^T.  The V^T fragment of chunk ch holds keys ch*16 + g*4 + 0..3 then
         ch*16 + 8 + g*4 + 0..3 (the score accumulator's order) for d = u*32 + lane % 32,
         gathered by two transposing reads of V's natural rows."""
+        if dma:
+            rd = "__builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)"
+            return ["#pragma unroll", f"for (int ch = 0; ch < {BKV // 16}; ++ch) {{",
+                    "#pragma unroll", f"  for (int u = 0; u < {Dv // 32}; ++u) {{",
+                    f"    tj_i16x4 v0 = {rd}(Vs{stage} + ch * 4096u + va[u]));",
+                    f"    tj_i16x4 v1 = {rd}(Vs{stage} + ch * 4096u + 2048u + va[u]));",
+                    f"    const {opvec} vv = __builtin_bit_cast({opvec}, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));",
+                    "#pragma unroll",
+                    f"    for (int q = 0; q < {QT}; ++q) o[q][u] = {mfma}(vv, pf[q][ch], o[q][u], 0, 0, 0);",
+                    "  }", "}"]
         return ["#pragma unroll", f"for (int ch = 0; ch < {BKV // 16}; ++ch) {{",
                 "  const unsigned int vrow = ch * 16 + g * 4u + (lane % 16u) / 4u;",
                 "#pragma unroll", f"  for (int u = 0; u < {Dv // 32}; ++u) {{",
@@ -625,6 +686,77 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         out.append("  if (gq == 0u) __syncthreads();")
         return out
 
+    def phase_end(vm: int | None) -> list[str]:
+        """End of a ping-pong phase in the DMA schedule: this wave's fragment reads are done
+        and, with ``vm``, all but its ``vm`` youngest DMA loads have landed; then the
+        workgroup barrier.  A plain ``s_barrier``: __syncthreads' workgroup fence would
+        wait for every DMA load in flight."""
+        imm = 0xC07F if vm is None else (vm & 15) | ((vm >> 4) << 14) | 0x70
+        return ["__builtin_amdgcn_sched_barrier(0);", f"__builtin_amdgcn_s_waitcnt({hex(imm)});",
+                "__builtin_amdgcn_s_barrier();", "__builtin_amdgcn_sched_barrier(0);"]
+
+    def n_dma(x: int) -> int:
+        """DMA loads a wave issues in phase B of block x: V(x+3) and K(x+4), two each."""
+        return 2 * (x + 3 < KB) + 2 * (x + 4 < KB)
+
+    def dma_block(j: str, jc: int, s: int, vm: int) -> list[str]:
+        """Block ``jc`` (-1: a loop block, never the last) in stage s = j % 4 for one wave group.
+        Phase A: softmax of S(j) with the MFMAs of S(j+1) (K(j+1), stage (s+1)%4); at its
+        end the DMA loads of phase B(j-2) have landed (``vm``: those of B(j-1) may not).
+        Phase B: V(j+3) into stage (s+3)%4 and K(j+4) into stage s are issued, then
+        O += P(j) V(j).  With group 1 one phase behind group 0 (group 0 runs A(j) in phase
+        2j, B(j) in 2j+1), the stage V(j+3) overwrites was last read in phase 2j (V(j-1)) and
+        the one of K(j+4) in 2j-1 (K(j)), before either group issues into it (2j+1, 2j+2);
+        loads of B(j) land by A(j+2) (phases 2j+4 and 2j+5), before the first read of
+        K(j+4) (2j+6) and of V(j+3) (2j+7)."""
+        par = (jc if jc >= 0 else s) % 2
+        sc, sn = ("sA", "sB") if par == 0 else ("sB", "sA")
+        has_next = jc < 0 or jc + 1 < KB
+        out = block_max(sc, jc)
+        if has_next:
+            out += scores(sn, (s + 1) % 4)
+        out += probs(sc)
+        out += phase_end(vm)
+        if jc < 0 or jc + 3 < KB:
+            out += dma_lines("v", f"{j} + 3u", (s + 3) % 4)
+        if jc < 0 or jc + 4 < KB:
+            out += dma_lines("k", f"{j} + 4u", s)
+        out += pv(s)
+        out += phase_end(None)
+        return out
+
+    def dma_body() -> list[str]:
+        """Ping-pong over 4 K and 4 V stages filled by DMA.  Prologue (all waves): K(0),
+        K(1), V(0), then the loads phases B(-2) and B(-1) would have issued (V(1), K(2);
+        V(2), K(3)); a barrier once K(0), K(1) and V(0) have landed; S(0); group 1 waits one
+        extra barrier.  Blocks 0 .. 4n-1 (each followed by at least four more) run in a loop
+        unrolled by four, so every stage is a compile-time array; the rest are peeled."""
+        out = []
+        first = dma_lines("k", "0u", 0) + (dma_lines("k", "1u", 1) if KB > 1 else []) + dma_lines("v", "0u", 0)
+        for x in (-2, -1):
+            if x + 3 < KB:
+                out_v = dma_lines("v", f"{x + 3}u", (x + 3) % 4)
+                first += out_v
+            if x + 4 < KB:
+                first += dma_lines("k", f"{x + 4}u", (x + 4) % 4)
+        out += ["  " + x for x in first]
+        out += ["  " + x for x in phase_end(n_dma(-2) + n_dma(-1))]
+        out += ["  " + x for x in scores("sA", 0)]
+        out += ["  if (gq == 1u) {"] + ["    " + x for x in phase_end(None)] + ["  }"]
+        nquad = max(0, (KB - 4) // 4)
+        if nquad:
+            out.append(f"  for (unsigned int jj = 0; jj < {4 * nquad}u; jj += 4u) {{")
+            for i in range(4):
+                out += ["    {"] + [f"      const unsigned int j{i} = jj + {i}u;"]
+                out += ["      " + x for x in dma_block(f"j{i}", -1, i, 4)] + ["    }"]
+            out.append("  }")
+        for j in range(4 * nquad, KB):
+            out.append(f"  {{  // block {j}")
+            out += ["    " + x for x in dma_block(f"{j}u", j, j % 4, n_dma(j - 1))]
+            out.append("  }")
+        out += ["  if (gq == 0u) {"] + ["    " + x for x in phase_end(None)] + ["  }"]
+        return out
+
     def epilogue_lines() -> list[str]:
         # O = O^T / l: lane holds 4 consecutive dv per (u, r/4) for its query
         return ["#pragma unroll", f"  for (int q = 0; q < {QT}; ++q) {{",
@@ -672,13 +804,13 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 "}"]
 
     L += [f"  tj_f32x16 sA[{QT}][{BKV // 32}], sB[{QT}][{BKV // 32}];", f"  {opvec} pf[{QT}][{BKV // 16}];"]
-    L += pingpong_body() if pingpong else double_buffer_body()
+    L += dma_body() if dma else pingpong_body() if pingpong else double_buffer_body()
     L += epilogue_lines() if NS == 1 else partial_epilogue_lines()
-    lds = NST * BKV * (DP + VP) * dt.itemsize
+    lds = NST * BKV * 256 * 2 if dma else NST * BKV * (DP + VP) * dt.itemsize
     flops = 2.0 * batch * Sq * Sk * (D + Dv)
     meta = {"family": "attention", "dtype": dt.value, "batch": batch, "Sq": Sq, "Sk": Sk, "D": D, "Dv": Dv,
             "scale": scale, "lds_bytes": lds, "flops": flops, "splits": NS,
-            "schedule": "pingpong" if pingpong else "double-buffer"}
+            "schedule": "pingpong-dma" if dma else "pingpong" if pingpong else "double-buffer"}
     main = Launch(fname, (nq * batch * NS, 1, 1), (THREADS, 1, 1), 0, meta)
     if NS == 1:
         return "\n".join(L), main

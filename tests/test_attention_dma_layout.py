@@ -1,0 +1,351 @@
+"""The flash-attention kernel's DMA schedule (head dim 128, 8 waves), checked on the CPU
+from its generated source.
+
+K and V blocks move from memory into LDS with ``buffer_load_dwordx4 ... lds``: one
+instruction writes lane ``l``'s 16 bytes at byte ``16 l`` of a 1 KiB block, so the
+swizzle lives in which global chunk each lane fetches.  These tests evaluate the
+generated expressions for every wave and lane and check that (a) the DMA of one block
+fills each 16-byte LDS slot of a stage exactly once, with the 64 rows x 16 chunks of
+the block, (b) each score-fragment read returns K row ``t*32 + lane % 32``, chunk
+``2c + lane / 32`` (the 32x32x16 MFMA's operand), (c) each transposing V read returns
+the 8 bytes the padded-row kernel reads (row ``ch*16 + g*4 + (lane % 16)/4`` (+8),
+columns ``u*32 + ((lane/16) % 2)*16 + (lane % 4)*4`` .. +3), (d) the reads are
+conflict-free under the LDS model of the GEMM layout test (16-byte reads served 32
+lanes a pass over 512 bytes of banks; 8-byte reads 64 lanes a pass), and (e) the
+ping-pong schedule itself -- DMA issues, wait counts and barriers of both wave groups,
+expanded from the source -- never reads a stage before both groups' halves of the
+expected block have landed and been published, and never overwrites one that a group
+may still read.
+"""
+import re
+
+import pytest
+
+import tensorjit as tj
+import tensorjit.compiler as C
+from tensorjit.backends import hip_backend as hb
+from tensorjit.backends.hip_attention import fuse_attention
+from tensorjit.ir import DType, TensorType
+
+BKV = 64
+
+
+@pytest.fixture(autouse=True)
+def _eight_waves(monkeypatch):
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_WAVES", "8")
+    monkeypatch.delenv("TENSORJIT_HIP_ATTENTION_DMA", raising=False)
+
+
+def _source(Sk=2048, Sq=1024, layout="bhsd", H=2):
+    fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * 0.088), v)  # noqa: E731
+    if layout == "bshd":
+        tq = lambda t: tj.transpose(t, 1, 2)  # noqa: E731
+        fn2 = lambda q, k, v: fn(tq(q), tq(k), tq(v))  # noqa: E731
+        shapes = [(1, Sq, H, 128), (1, Sk, H, 128), (1, Sk, H, 128)]
+    else:
+        fn2 = fn
+        shapes = [(1, H, Sq, 128), (1, H, Sk, 128), (1, H, Sk, 128)]
+    p = fuse_attention(C.lower(tj.trace(fn2, [TensorType(s, DType.bf16) for s in shapes]), "hip"))
+    src, launches = hb.generate(p)
+    (launch,) = launches if isinstance(launches, list) else [launches]
+    assert launch.meta["family"] == "attention" and launch.meta["schedule"] == "pingpong-dma", launch.meta
+    return src, launch
+
+
+def _c_eval(expr: str, env: dict) -> int:
+    py = re.sub(r"(\d+)u\b", r"\1", expr).replace("(unsigned int)", "").replace("/", "//")
+    return int(eval(py, {}, dict(env))) & 0xFFFFFFFF
+
+
+def _expr(src: str, pattern: str) -> str:
+    m = re.search(pattern, src)
+    assert m, pattern
+    return m.group(1)
+
+
+def _lane_env(lane: int, wave: int) -> dict:
+    return {"lane": lane, "wave": wave, "wv": wave, "gq": wave // 4, "g": lane // 32, "col": lane % 32}
+
+
+def _setup(src: str):
+    """The per-lane set-up expressions, as generated."""
+    e = {
+        "dmo": _expr(src, r"    dmo\[q\] = (.*);\n"),
+        "r": _expr(src, r"    const unsigned int r = (.*);\n"),
+        "voK": _expr(src, r"    voK\[q\] = (.*);\n"),
+        "voV": _expr(src, r"    voV\[q\] = (.*);\n"),
+        "kx": _expr(src, r"  const unsigned int kx = (.*);\n"),
+        "vr": _expr(src, r"  const unsigned int vr = (.*?), vsw"),
+        "vsw": _expr(src, r", vsw = (.*);\n"),
+        "vcl": _expr(src, r"  const unsigned int vcl = (.*);\n"),
+        "va": _expr(src, r"    va\[u\] = (.*);\n"),
+        "kread": _expr(src, r"kf = \*\(const tj_bf16x8\*\)\(Ks\d \+ (.*)\);\n"),
+        "v0": _expr(src, r"tj_i16x4 v0 = .*?\(Vs\d \+ (.*)\)\);\n"),
+        "v1": _expr(src, r"tj_i16x4 v1 = .*?\(Vs\d \+ (.*)\)\);\n"),
+        "kstep": _expr(src, r"voK\[\d\] \+ \(.*?\) \* (\d+)u"),
+        "vstep": _expr(src, r"voV\[\d\] \+ \(.*?\) \* (\d+)u"),
+    }
+    return e
+
+
+def _dma_map(e: dict, which: str, kst: int):
+    """LDS slot (16-byte index in a stage) -> (row, chunk) of the block, from both groups'
+    DMA loads of one block (block 0: offsets relative to the block's first row)."""
+    slots = {}
+    for wave in range(8):
+        for q in range(2):
+            base = _c_eval(e["dmo"], dict(_lane_env(0, wave), q=q))
+            assert base % 1024 == 0 and 0 <= base < BKV * 256
+            for lane in range(64):
+                env = dict(_lane_env(lane, wave), q=q)
+                env["r"] = _c_eval(e["r"], env)
+                off = _c_eval(e["voK" if which == "k" else "voV"], env)
+                row, byte = divmod(off, kst * 2)
+                assert byte % 16 == 0 and byte < 256
+                slot = (base + 16 * lane) // 16
+                assert slot not in slots, (which, wave, q, lane)
+                slots[slot] = (row, byte // 16)
+    assert sorted(slots) == list(range(BKV * 16))
+    assert sorted(slots.values()) == [(r, c) for r in range(BKV) for c in range(16)]
+    return slots
+
+
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+def test_dma_placement_and_fragment_reads_agree(layout):
+    src, _ = _source(layout=layout)
+    kst = 128 * (2 if layout == "bshd" else 1)
+    e = _setup(src)
+    assert int(e["kstep"]) == BKV * kst * 2 and int(e["vstep"]) == BKV * kst * 2
+    kmap, vmap = _dma_map(e, "k", kst), _dma_map(e, "v", kst)
+    for lane in range(64):
+        env = _lane_env(lane, 0)
+        env["kx"] = _c_eval(e["kx"], env)
+        env["vr"] = _c_eval(e["vr"], env)
+        env["vsw"] = _c_eval(e["vsw"], env)
+        env["vcl"] = _c_eval(e["vcl"], env)
+        g, col = lane // 32, lane % 32
+        for t in range(2):
+            for c in range(8):
+                a = _c_eval(e["kread"], dict(env, t=t, c=c))
+                assert a % 16 == 0
+                assert kmap[a // 16] == (t * 32 + col, 2 * c + g), (lane, t, c)
+        for u in range(4):
+            env["va"] = [0] * 4
+            va_u = _c_eval(e["va"], dict(env, u=u))
+            env["va"][u] = va_u
+            for ch in range(4):
+                for second, key in ((0, "v0"), (1, "v1")):
+                    a = _c_eval(e[key].replace("va[u]", "va_u"), dict(env, ch=ch, u=u, va_u=va_u))
+                    assert a % 8 == 0
+                    row, chunk = vmap[a // 16]
+                    vrow = ch * 16 + g * 4 + (lane % 16) // 4 + 8 * second
+                    vcol = u * 32 + ((lane // 16) % 2) * 16 + (lane % 4) * 4
+                    assert (row, chunk * 8 + ((a % 16) // 8) * 4) == (vrow, vcol), (lane, ch, u, second)
+
+
+def test_fragment_reads_are_bank_conflict_free():
+    src, _ = _source()
+    e = _setup(src)
+    envs = []
+    for lane in range(64):
+        env = _lane_env(lane, 0)
+        for name in ("kx", "vr", "vsw", "vcl"):
+            env[name] = _c_eval(e[name], env)
+        envs.append(env)
+    for t in range(2):
+        for c in range(8):
+            a = [_c_eval(e["kread"], dict(env, t=t, c=c)) for env in envs]
+            for h in (0, 1):   # 16-byte reads: 32 lanes a pass over 32 groups of 16 bytes
+                assert len({(x // 16) % 32 for x in a[32 * h:32 * h + 32]}) == 32, (t, c, h)
+    for u in range(4):
+        for ch in range(4):
+            for key in ("v0", "v1"):
+                a = []
+                for env in envs:
+                    va_u = _c_eval(e["va"], dict(env, u=u))
+                    a.append(_c_eval(e[key].replace("va[u]", "va_u"), dict(env, ch=ch, u=u, va_u=va_u)))
+                assert len({(x // 8) % 64 for x in a}) == 64, (u, ch, key)   # 8-byte reads: one pass
+
+
+# ---------------------------------------------------------------------------
+# the schedule, expanded from the source and run for both wave groups
+# ---------------------------------------------------------------------------
+
+DMA_RE = re.compile(r"raw_ptr_buffer_load_lds\(rs([KV]), .*?\(([KV])s(\d) \+ dmo\[(\d)\]\), 16, vo[KV]\[\d\] \+ \((.*?)\) \* \d+u")
+WAIT_RE = re.compile(r"__builtin_amdgcn_s_waitcnt\((0x[0-9a-f]+)\)")
+LOOP_RE = re.compile(r"for \(unsigned int jj = 0; jj < (\d+)u; jj \+= 4u\) \{")
+
+
+def _body_lines(src: str) -> list[str]:
+    start = src.index("wv = __builtin_amdgcn_readfirstlane")
+    end = src.index("const float l_tot", start)
+    return [x.strip() for x in src[start:end].splitlines()]
+
+
+def _expand(lines: list[str]) -> list[tuple]:
+    """Flatten the body into (kind, payload, group-or-None, block-context) events."""
+    out = []
+    i, cur_j, only = 0, None, None
+    while i < len(lines):
+        ln = lines[i]
+        m = LOOP_RE.match(ln)
+        if m:
+            depth, k = 1, i + 1
+            while depth:
+                depth += lines[k].count("{") - lines[k].count("}")
+                k += 1
+            body = lines[i + 1:k - 1]
+            for jj in range(0, int(m.group(1)), 4):
+                out += _expand_block(body, {"jj": jj}, only)
+            i = k
+            continue
+        out += _expand_block([ln], {}, only, cur_j)
+        mb = re.match(r"\{  // block (\d+)", ln)
+        if mb:
+            cur_j = int(mb.group(1))
+            out.append(("ctx", cur_j, None, None))
+        mg = re.match(r"if \(gq == (\d)u\) \{", ln)
+        if mg:
+            only = int(mg.group(1))
+        elif ln == "}" and only is not None:
+            only = None
+        i += 1
+    return out
+
+
+def _expand_block(lines, env, only, cur_j=None):
+    out = []
+    for ln in lines:
+        mj = re.match(r"const unsigned int (j\d) = jj \+ (\d)u;", ln)
+        if mj:
+            env = dict(env, **{mj.group(1): env["jj"] + int(mj.group(2))})
+            out.append(("ctx", env[mj.group(1)], None, None))
+            continue
+        m = DMA_RE.search(ln)
+        if m:
+            assert m.group(1) == m.group(2)
+            blk = _c_eval(m.group(5), env)
+            out.append(("dma", (m.group(1), int(m.group(3)), int(m.group(4)), blk), only, None))
+            continue
+        m = WAIT_RE.search(ln)
+        if m:
+            imm = int(m.group(1), 16)
+            out.append(("wait", ((imm & 15) | (((imm >> 14) & 3) << 4), (imm >> 8) & 15), only, None))
+            continue
+        if "__builtin_amdgcn_s_barrier()" in ln:
+            out.append(("barrier", None, only, None))
+            continue
+        assert "__syncthreads" not in ln
+        mk = re.search(r"\(Ks(\d) \+ t \*", ln)
+        if mk:
+            out.append(("read", ("K", int(mk.group(1))), only, None))
+        mv = re.search(r"\(Vs(\d) \+ ch \*", ln)
+        if mv:
+            out.append(("read", ("V", int(mv.group(1))), only, None))
+    return out
+
+
+def _run_group(events, gq: int):
+    """One group's trace: DMA loads (op, stage, block, issue interval, visible-from
+    interval) and reads (op, stage, expected block, interval)."""
+    interval, cur_j = 0, None
+    dmas, reads = [], []
+    for kind, pay, only, _ in events:
+        if only is not None and only != gq:
+            continue
+        if kind == "ctx":
+            cur_j = pay
+        elif kind == "dma":
+            op, st, q, blk = pay
+            if q == 0:
+                dmas.append({"op": op, "stage": st, "block": blk, "issued": interval, "visible": None, "n": 0})
+            dmas[-1]["n"] += 1
+        elif kind == "wait":
+            vm, lgkm = pay
+            # vmcnt counts this wave's instructions (two per block half); they land in order
+            insts = [d for d in dmas for _ in range(d["n"])]
+            for d_i, d in enumerate(dmas):
+                last = sum(x["n"] for x in dmas[:d_i + 1])
+                if d["visible"] is None and len(insts) - last >= vm:
+                    d["visible"] = interval + 1
+        elif kind == "barrier":
+            interval += 1
+        elif kind == "read":
+            op, st = pay
+            want = (0 if cur_j is None else cur_j + 1) if op == "K" else cur_j
+            reads.append({"op": op, "stage": st, "block": want, "at": interval})
+    return dmas, reads, interval
+
+
+@pytest.mark.parametrize("Sk", [64, 128, 192, 256, 320, 448, 512, 576, 640, 704, 960, 1024, 1100, 2048, 2000])
+def test_schedule_reads_only_published_blocks(Sk):
+    src, _ = _source(Sk=Sk)
+    lines = _body_lines(src)
+    # every barrier is preceded by a wait that includes lgkmcnt(0): a group's fragment
+    # reads are done before the barrier after which the other group may overwrite them
+    for i, ln in enumerate(lines):
+        if "__builtin_amdgcn_s_barrier()" in ln:
+            prev = [x for x in lines[:i] if "s_waitcnt" in x][-1]
+            assert (int(WAIT_RE.search(prev).group(1), 16) >> 8) & 15 == 0
+    events = _expand(lines)
+    KB = -(-Sk // BKV)
+    traces = [_run_group(events, gq) for gq in (0, 1)]
+    assert traces[0][2] == traces[1][2], "both groups pass the same number of barriers"
+    for gq in (0, 1):
+        dmas = traces[gq][0]
+        assert all(d["visible"] is not None for d in dmas), "every DMA load is waited for"
+        assert all(d["n"] == 2 for d in dmas)
+        for op in ("K", "V"):
+            assert sorted(d["block"] for d in dmas if d["op"] == op) == list(range(KB))
+            assert all(d["stage"] == d["block"] % 4 for d in dmas if d["op"] == op)
+    nread = 0
+    for gq in (0, 1):
+        for r in traces[gq][1]:
+            if r["op"] == "K" and r["block"] >= KB:
+                raise AssertionError(f"S({r['block']}) read past the last block")
+            for h in (0, 1):
+                cands = [d for d in traces[h][0] if d["op"] == r["op"] and d["stage"] == r["stage"]]
+                before = [d for d in cands if d["issued"] < r["at"]]
+                assert before, (gq, r)
+                src_d = before[-1]
+                assert src_d["block"] == r["block"], (gq, h, r, src_d)
+                assert src_d["visible"] <= r["at"], (gq, h, r, src_d)
+                assert not [d for d in cands if d["issued"] == r["at"]], ("overwritten while read", gq, h, r)
+            nread += 1
+    # group 0 reads K of blocks 0..KB-1 and V of blocks 0..KB-1, as group 1 does
+    for gq in (0, 1):
+        got = sorted({(r["op"], r["block"]) for r in traces[gq][1]})
+        assert got == sorted([("K", b) for b in range(KB)] + [("V", b) for b in range(KB)])
+    assert nread
+
+
+def test_planted_schedule_mistake_is_caught():
+    """A wait that lets one more DMA load stay in flight at the end of a block's first
+    phase publishes a block before it has landed: the simulation must flag it."""
+    src, _ = _source(Sk=1024)
+    lines = _body_lines(src)
+    i = next(i for i, ln in enumerate(lines) if "s_waitcnt(0x74)" in ln)
+    lines[i] = lines[i].replace("0x74", "0x76")
+    events = _expand(lines)
+    traces = [_run_group(events, gq) for gq in (0, 1)]
+    bad = False
+    for gq in (0, 1):
+        for r in traces[gq][1]:
+            for h in (0, 1):
+                cands = [d for d in traces[h][0] if d["op"] == r["op"] and d["stage"] == r["stage"]]
+                before = [d for d in cands if d["issued"] < r["at"]]
+                if not before or before[-1]["block"] != r["block"] or before[-1]["visible"] is None \
+                        or before[-1]["visible"] > r["at"]:
+                    bad = True
+    assert bad
+
+
+def test_dma_schedule_only_for_head_dim_128(monkeypatch):
+    fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * 0.125), v)  # noqa: E731
+    p = fuse_attention(C.lower(tj.trace(fn, [TensorType((1, 2, 1024, 64), DType.bf16)] * 3), "hip"))
+    _, launches = hb.generate(p)
+    assert launches[0].meta["schedule"] == "pingpong"
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_DMA", "0")
+    p = fuse_attention(C.lower(tj.trace(fn, [TensorType((1, 2, 1024, 128), DType.bf16)] * 3), "hip"))
+    _, launches = hb.generate(p)
+    assert launches[0].meta["schedule"] == "pingpong"
