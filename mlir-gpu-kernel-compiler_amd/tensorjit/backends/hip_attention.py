@@ -40,6 +40,15 @@ from .hip_prelude import CTYPE
 BQ_PER_WAVE = 32
 BKV = 64
 MAX_HEAD_DIM = 128
+# DMA schedule (head dim 128): how many fragment reads the score MFMAs (K) and the PV
+# MFMAs (Vᵀ) keep in flight ahead of themselves, pinned by sched_group_barrier (0: the
+# compiler's own order).  Same box, interleaved, bit-identical outputs, [4,32,2048,128],
+# (KS, PV): compiler's order 260.4 us, (2, 2) 248.9, (2, 3) 248.7, (3, 3) 249.3, (3, 4) 250.5,
+# (2, 4) 250.8, (2, 6) 252.2, (1, 4) 256.5; another box: compiler's order 262.6, (0, 4)
+# 256.4, (4, 0) 252.9, (4, 4) 250.5; [1,32,8192,128] 929.4 -> 878.9 at (2, 2)
+KS_AHEAD = 2
+PV_AHEAD = 2
+SG_MFMA, SG_DS_READ = 0x008, 0x100
 
 
 # ---------------------------------------------------------------------------
@@ -493,6 +502,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
 
     def scores(dst: str, stage: int) -> list[str]:
         """S^T = K Q^T over D in 16-wide chunks: tile t covers keys t*32 .. t*32+31."""
+        if dma and KS_AHEAD:
+            return scores_pipelined(dst, stage, KS_AHEAD)
         return ["#pragma unroll", f"for (int q = 0; q < {QT}; ++q)", "#pragma unroll",
                 f"  for (int t = 0; t < {BKV // 32}; ++t) {dst}[q][t] = (tj_f32x16)(0.0f);",
                 "#pragma unroll", f"for (int c = 0; c < {D // 16}; ++c) {{", "#pragma unroll",
@@ -565,6 +576,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         """O^T += V^T P^T.  The V^T fragment of chunk ch holds keys ch*16 + g*4 + 0..3 then
         ch*16 + 8 + g*4 + 0..3 (the score accumulator's order) for d = u*32 + lane % 32,
         gathered by two transposing reads of V's natural rows."""
+        if dma and PV_AHEAD:
+            return pv_pipelined(stage, PV_AHEAD)
         if dma:
             rd = "__builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)"
             return ["#pragma unroll", f"for (int ch = 0; ch < {BKV // 16}; ++ch) {{",
@@ -685,6 +698,55 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
             out.append("  }")
         out.append("  if (gq == 0u) __syncthreads();")
         return out
+
+    def scores_pipelined(dst: str, stage: int, ahead: int) -> list[str]:
+        """The score MFMAs with the K fragment read of MFMA p + ``ahead`` issued after MFMA p
+        (fragments in (c, t) order), pinned by ``sched_group_barrier``."""
+        assert QT == 1
+        n = (D // 16) * (BKV // 32)
+
+        def read(p: int) -> str:
+            c, t = divmod(p, BKV // 32)
+            return f"const {opvec} kt{p} = *(const {opvec}*)(Ks{stage} + {t * 32 * 256}u + (kx ^ {c * 32}u));"
+
+        out = [f"{dst}[0][{t}] = (tj_f32x16)(0.0f);" for t in range(BKV // 32)]
+        out.append("{")
+        sg = [f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, {min(ahead, n)}, 0);"]
+        out += [read(p) for p in range(min(ahead, n))]
+        for p in range(n):
+            c, t = divmod(p, BKV // 32)
+            out.append(f"{dst}[0][{t}] = {mfma}(kt{p}, qf[0][{c}], {dst}[0][{t}], 0, 0, 0);")
+            sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_MFMA}, 1, 0);")
+            if p + ahead < n:
+                out.append(read(p + ahead))
+                sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, 1, 0);")
+        return out + sg + ["}"]
+
+    def pv_pipelined(stage: int, ahead: int) -> list[str]:
+        """The PV phase with the transposing reads of fragment p + ``ahead`` issued after the
+        MFMA of fragment p (fragments in (ch, u) order), pinned by ``sched_group_barrier``;
+        the score accumulator that PV follows is dead by then, so its registers hold them."""
+        assert QT == 1
+        rd = "__builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)"
+        n = (BKV // 16) * (Dv // 32)
+
+        def reads(p: int) -> list[str]:
+            ch, u = divmod(p, Dv // 32)
+            return [f"const tj_i16x4 vt{p}a = {rd}(Vs{stage} + {ch * 4096}u + va[{u}]));",
+                    f"const tj_i16x4 vt{p}b = {rd}(Vs{stage} + {ch * 4096 + 2048}u + va[{u}]));"]
+
+        out, sg = ["{"], [f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, {2 * min(ahead, n)}, 0);"]
+        for p in range(min(ahead, n)):
+            out += reads(p)
+        for p in range(n):
+            ch, u = divmod(p, Dv // 32)
+            out.append(f"o[0][{u}] = {mfma}(__builtin_bit_cast({opvec}, __builtin_shufflevector(vt{p}a, vt{p}b, "
+                       f"0, 1, 2, 3, 4, 5, 6, 7)), pf[0][{ch}], o[0][{u}], 0, 0, 0);")
+            sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_MFMA}, 1, 0);")
+            if p + ahead < n:
+                out += reads(p + ahead)
+                sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, 2, 0);")
+        return out + sg + ["}"]
 
     def phase_end(vm: int | None) -> list[str]:
         """End of a ping-pong phase in the DMA schedule: this wave's fragment reads are done

@@ -79,13 +79,37 @@ def _setup(src: str):
         "vsw": _expr(src, r", vsw = (.*);\n"),
         "vcl": _expr(src, r"  const unsigned int vcl = (.*);\n"),
         "va": _expr(src, r"    va\[u\] = (.*);\n"),
-        "kread": _expr(src, r"kf = \*\(const tj_bf16x8\*\)\(Ks\d \+ (.*)\);\n"),
-        "v0": _expr(src, r"tj_i16x4 v0 = .*?\(Vs\d \+ (.*)\)\);\n"),
-        "v1": _expr(src, r"tj_i16x4 v1 = .*?\(Vs\d \+ (.*)\)\);\n"),
         "kstep": _expr(src, r"voK\[\d\] \+ \(.*?\) \* (\d+)u"),
         "vstep": _expr(src, r"voV\[\d\] \+ \(.*?\) \* (\d+)u"),
     }
     return e
+
+
+KREAD_RE = re.compile(r"const tj_bf16x8 kt(\d+) = \*\(const tj_bf16x8\*\)\(Ks(\d) \+ (.*?)\);")
+VREAD_RE = re.compile(r"const tj_i16x4 vt(\d+)([ab]) = .*?\(Vs(\d) \+ (.*?)\)\);")
+KMMA_RE = re.compile(r"(s[AB])\[0\]\[(\d)\] = __builtin_amdgcn_mfma_f32_32x32x16_bf16\(kt(\d+), qf\[0\]\[(\d)\], (s[AB])\[0\]\[(\d)\]")
+VMMA_RE = re.compile(r"o\[0\]\[(\d)\] = __builtin_amdgcn_mfma_f32_32x32x16_bf16\(.*?shufflevector\(vt(\d+)a, vt(\d+)b, "
+                     r"0, 1, 2, 3, 4, 5, 6, 7\)\), pf\[0\]\[(\d)\], o\[0\]\[(\d)\]")
+
+
+def _block_reads(src: str):
+    """One block's score and PV sections as generated: K fragment p's address expression
+    and the MFMA that takes it (accumulator tile t, Q chunk c); Vᵀ fragment p's two
+    address expressions and its MFMA (output tile u, probability chunk ch)."""
+    blk = src.split("// block")[1]
+    kreads = {int(p): e for p, _, e in KREAD_RE.findall(blk)}
+    vreads = {}
+    for p, h, _, e in VREAD_RE.findall(blk):
+        vreads.setdefault(int(p), {})[h] = e
+    kmma = {}
+    for dst, t, p, c, src_acc, t2 in KMMA_RE.findall(blk):
+        assert dst == src_acc and t == t2
+        kmma[int(p)] = (int(t), int(c))
+    vmma = {}
+    for u, pa, pb, ch, u2 in VMMA_RE.findall(blk):
+        assert pa == pb and u == u2
+        vmma[int(pa)] = (int(u), int(ch))
+    return kreads, kmma, vreads, vmma
 
 
 def _dma_map(e: dict, which: str, kst: int):
@@ -117,30 +141,32 @@ def test_dma_placement_and_fragment_reads_agree(layout):
     e = _setup(src)
     assert int(e["kstep"]) == BKV * kst * 2 and int(e["vstep"]) == BKV * kst * 2
     kmap, vmap = _dma_map(e, "k", kst), _dma_map(e, "v", kst)
+    kreads, kmma, vreads, vmma = _block_reads(src)
+    # every score MFMA takes one K fragment read, every (tile, chunk) once; likewise PV
+    assert sorted(kreads) == sorted(kmma) == list(range(16))
+    assert sorted(kmma.values()) == [(t, c) for t in range(2) for c in range(8)]
+    assert sorted(vreads) == sorted(vmma) == list(range(16))
+    assert sorted(vmma.values()) == [(u, ch) for u in range(4) for ch in range(4)]
     for lane in range(64):
         env = _lane_env(lane, 0)
-        env["kx"] = _c_eval(e["kx"], env)
-        env["vr"] = _c_eval(e["vr"], env)
-        env["vsw"] = _c_eval(e["vsw"], env)
-        env["vcl"] = _c_eval(e["vcl"], env)
+        for name in ("kx", "vr", "vsw", "vcl"):
+            env[name] = _c_eval(e[name], env)
+        env["va"] = [_c_eval(e["va"], dict(env, u=u)) for u in range(4)]
         g, col = lane // 32, lane % 32
-        for t in range(2):
-            for c in range(8):
-                a = _c_eval(e["kread"], dict(env, t=t, c=c))
-                assert a % 16 == 0
-                assert kmap[a // 16] == (t * 32 + col, 2 * c + g), (lane, t, c)
-        for u in range(4):
-            env["va"] = [0] * 4
-            va_u = _c_eval(e["va"], dict(env, u=u))
-            env["va"][u] = va_u
-            for ch in range(4):
-                for second, key in ((0, "v0"), (1, "v1")):
-                    a = _c_eval(e[key].replace("va[u]", "va_u"), dict(env, ch=ch, u=u, va_u=va_u))
-                    assert a % 8 == 0
-                    row, chunk = vmap[a // 16]
-                    vrow = ch * 16 + g * 4 + (lane % 16) // 4 + 8 * second
-                    vcol = u * 32 + ((lane // 16) % 2) * 16 + (lane % 4) * 4
-                    assert (row, chunk * 8 + ((a % 16) // 8) * 4) == (vrow, vcol), (lane, ch, u, second)
+        for p, expr in kreads.items():
+            t, c = kmma[p]
+            a = _c_eval(expr, env)
+            assert a % 16 == 0
+            assert kmap[a // 16] == (t * 32 + col, 2 * c + g), (lane, p, t, c)
+        for p, pair in vreads.items():
+            u, ch = vmma[p]
+            for second, h in ((0, "a"), (1, "b")):
+                a = _c_eval(pair[h], env)
+                assert a % 8 == 0
+                row, chunk = vmap[a // 16]
+                vrow = ch * 16 + g * 4 + (lane % 16) // 4 + 8 * second
+                vcol = u * 32 + ((lane // 16) % 2) * 16 + (lane % 4) * 4
+                assert (row, chunk * 8 + ((a % 16) // 8) * 4) == (vrow, vcol), (lane, p, u, ch, second)
 
 
 def test_fragment_reads_are_bank_conflict_free():
@@ -151,20 +177,17 @@ def test_fragment_reads_are_bank_conflict_free():
         env = _lane_env(lane, 0)
         for name in ("kx", "vr", "vsw", "vcl"):
             env[name] = _c_eval(e[name], env)
+        env["va"] = [_c_eval(e["va"], dict(env, u=u)) for u in range(4)]
         envs.append(env)
-    for t in range(2):
-        for c in range(8):
-            a = [_c_eval(e["kread"], dict(env, t=t, c=c)) for env in envs]
-            for h in (0, 1):   # 16-byte reads: 32 lanes a pass over 32 groups of 16 bytes
-                assert len({(x // 16) % 32 for x in a[32 * h:32 * h + 32]}) == 32, (t, c, h)
-    for u in range(4):
-        for ch in range(4):
-            for key in ("v0", "v1"):
-                a = []
-                for env in envs:
-                    va_u = _c_eval(e["va"], dict(env, u=u))
-                    a.append(_c_eval(e[key].replace("va[u]", "va_u"), dict(env, ch=ch, u=u, va_u=va_u)))
-                assert len({(x // 8) % 64 for x in a}) == 64, (u, ch, key)   # 8-byte reads: one pass
+    kreads, _, vreads, _ = _block_reads(src)
+    for p, expr in kreads.items():
+        a = [_c_eval(expr, env) for env in envs]
+        for h in (0, 1):   # 16-byte reads: 32 lanes a pass over 32 groups of 16 bytes
+            assert len({(x // 16) % 32 for x in a[32 * h:32 * h + 32]}) == 32, (p, h)
+    for p, pair in vreads.items():
+        for h, expr in pair.items():
+            a = [_c_eval(expr, env) for env in envs]
+            assert len({(x // 8) % 64 for x in a}) == 64, (p, h)   # 8-byte reads: one pass
 
 
 # ---------------------------------------------------------------------------
@@ -236,12 +259,12 @@ def _expand_block(lines, env, only, cur_j=None):
             out.append(("barrier", None, only, None))
             continue
         assert "__syncthreads" not in ln
-        mk = re.search(r"\(Ks(\d) \+ t \*", ln)
+        mk = KREAD_RE.search(ln)
         if mk:
-            out.append(("read", ("K", int(mk.group(1))), only, None))
-        mv = re.search(r"\(Vs(\d) \+ ch \*", ln)
+            out.append(("read", ("K", int(mk.group(2))), only, None))
+        mv = VREAD_RE.search(ln)
         if mv:
-            out.append(("read", ("V", int(mv.group(1))), only, None))
+            out.append(("read", ("V", int(mv.group(3))), only, None))
     return out
 
 

@@ -2,6 +2,8 @@
 (matmul -> softmax -> matmul) and elementwise kernels moved into a GEMM's epilogue --
 which planned programs are rewritten, what the rewritten program looks like, and that
 the generated flash-attention kernel compiles for gfx950 with hipRTC."""
+import re
+
 import pytest
 
 import tensorjit as tj
@@ -259,7 +261,8 @@ def test_flash_kernel_compiles_for_gfx950(shapes, dtype, forced, tj_env, monkeyp
         kb = -(-shapes[1][-2] // 64)
         tag = f"// block {kb - 1}" if l.meta["schedule"] == "pingpong-dma" else f"const unsigned int jj = {kb - 1}u;"
         last = src.split(tag)[1].split("if (gq == 0u)")[0]
-        assert "(kf, qf[q][c]" not in last and "(kf, qf[q][c]" in src
+        score_mfma = re.compile(r"\((kf|kt\d+), qf\[")
+        assert not score_mfma.search(last) and score_mfma.search(src)
     code = hb.compile_source(src, "gfx950")
     assert len(code) > 1000
 
