@@ -48,6 +48,13 @@ MAX_HEAD_DIM = 128
 # 256.4, (4, 0) 252.9, (4, 4) 250.5; [1,32,8192,128] 929.4 -> 878.9 at (2, 2)
 KS_AHEAD = 2
 PV_AHEAD = 2
+# the same for the register-staged schedules (4 waves, and 8 waves below head dim 128); K
+# reads ahead only from head dim 128.  Same box, bit-identical, (KS, PV): [1,16,2048,128]
+# (4 waves, 128 workgroups) compiler's order 50.8 us, (2, 2) 46.1, (2, 0) 45.8; head dim 64
+# [4,32,2048,64] 159.7 -> 157.4 at (0, 2), 8 waves 161.5 -> 159.3; 16 queries x 4096 keys
+# [8,32,*,64] 47.9 -> 47.5 at (0, 2) but 55.1 at (2, 2)
+KS_AHEAD_STAGED = 2
+PV_AHEAD_STAGED = 2
 SG_MFMA, SG_DS_READ = 0x008, 0x100
 
 
@@ -384,11 +391,20 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         every K and V block: one ``buffer_load_dwordx4 ... lds`` writes 1 KiB of LDS, four
         256-byte rows, lane l at byte 16 l.  Rows are not padded; lane l fetches 16-byte
         chunk (l % 16) ^ f(row) of its row, so position p of a stored row holds chunk
-        p ^ f(row), f = (row >> 1) & 15 for K and ((row >> 1) & 3) << 2 for V.  The offsets
-        (block included) go in the lane's voffset, which the descriptor's range checks:
-        rows past the last key read zeros.  Fragment addresses: K row ``col`` of tile t,
-        chunk 2c + g, sits at (2c + g) ^ f(col) = (g ^ f(col)) ^ 2c; a Vᵀ read's row
-        vr (+ 16 ch, + 8) and chunk 4u + vcl sit at ((4u) ^ f(vr)) + vcl."""
+        p ^ f(row), f = (row & 15) ^ ((row >> 4) & 1) for K and ((row ^ (row >> 2)) & 3) << 2
+        for V.  The offsets (block included) go in the lane's voffset, which the descriptor's
+        range checks: rows past the last key read zeros.  Fragment addresses: K row ``col``
+        of tile t, chunk 2c + g, sits at (2c + g) ^ f(col) = (g ^ f(col)) ^ 2c; 16 rows in a
+        row hold a chunk at 16 distinct positions and 32 rows of one parity too, so a
+        fragment read meets no bank twice whether the LDS serves it 8, 16 or 32 lanes at a
+        time (the padded layout's property; f = (row >> 1) & 15 held only for 32).  A transposing
+        Vᵀ read takes rows 16 ch + 8 s + vr (vr = 4g + (lane % 16) / 4) and chunk 4u + vcl:
+        f = ((vr % 4) ^ (2s + g)) << 2, so chunk 4u + vcl sits at ((4u) ^ vsw) + vcl for
+        the first read (s = 0) and at that of tile u ^ 2 for the second.  The transposing
+        reads are served a half-wave (32 lanes of 8 bytes) at a time over 256 bytes of
+        banks: a swizzle that keeps the 4 rows of a half-wave apart only within 512 bytes,
+        f = ((row >> 1) & 3) << 2, measured 3.4e7 bank-conflict cycles per launch at
+        [4,32,2048,128] against 0 for the padded rows."""
         return ["  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave), gq = wv / 4u;",
                 f"  const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, {Sk * kst * 2}, 0x00020000);",
                 f"  const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, {Sk * vst * 2}, 0x00020000);",
@@ -397,11 +413,11 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 "  for (int q = 0; q < 2; ++q) {",
                 "    dmo[q] = (gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u) * 256u;",
                 "    const unsigned int r = gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u + lane / 16u;",
-                f"    voK[q] = (r * {kst}u + ((lane % 16u) ^ ((r >> 1) & 15u)) * 8u) * 2u;",
-                f"    voV[q] = (r * {vst}u + ((lane % 16u) ^ (((r >> 1) & 3u) << 2)) * 8u) * 2u;",
+                f"    voK[q] = (r * {kst}u + ((lane % 16u) ^ (r & 15u) ^ ((r >> 4) & 1u)) * 8u) * 2u;",
+                f"    voV[q] = (r * {vst}u + ((lane % 16u) ^ (((r ^ (r >> 2)) & 3u) << 2)) * 8u) * 2u;",
                 "  }",
-                "  const unsigned int kx = col * 256u + ((g ^ ((col >> 1) & 15u)) << 4);",
-                "  const unsigned int vr = g * 4u + (lane % 16u) / 4u, vsw = ((vr >> 1) & 3u) << 2;",
+                "  const unsigned int kx = col * 256u + ((g ^ (col & 15u) ^ ((col >> 4) & 1u)) << 4);",
+                "  const unsigned int vr = g * 4u + (lane % 16u) / 4u, vsw = (((lane % 16u) / 4u) ^ g) << 2;",
                 "  const unsigned int vcl = ((lane / 16u) % 2u) * 2u + (lane % 4u) / 2u;",
                 "  unsigned int va[4];",
                 "#pragma unroll",
@@ -451,6 +467,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         L += dma_setup_lines()
     else:
         L.append(f"  tj_u32x4 rk[{KC}], rv[{VC}];")
+        if PV_AHEAD_STAGED:
+            L.append("  const unsigned int vrow0 = g * 4u + (lane % 16u) / 4u, vcol0 = ((lane / 16u) % 2u) * 16u + (lane % 4u) * 4u;")
     if pingpong and not dma:
         L.append("  const unsigned int gq = wave / 4u, gtid = tid % 256u;")
 
@@ -502,8 +520,9 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
 
     def scores(dst: str, stage: int) -> list[str]:
         """S^T = K Q^T over D in 16-wide chunks: tile t covers keys t*32 .. t*32+31."""
-        if dma and KS_AHEAD:
-            return scores_pipelined(dst, stage, KS_AHEAD)
+        ks_ahead = KS_AHEAD if dma else KS_AHEAD_STAGED if D >= 128 else 0
+        if ks_ahead:
+            return scores_pipelined(dst, stage, ks_ahead)
         return ["#pragma unroll", f"for (int q = 0; q < {QT}; ++q)", "#pragma unroll",
                 f"  for (int t = 0; t < {BKV // 32}; ++t) {dst}[q][t] = (tj_f32x16)(0.0f);",
                 "#pragma unroll", f"for (int c = 0; c < {D // 16}; ++c) {{", "#pragma unroll",
@@ -576,14 +595,14 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         """O^T += V^T P^T.  The V^T fragment of chunk ch holds keys ch*16 + g*4 + 0..3 then
         ch*16 + 8 + g*4 + 0..3 (the score accumulator's order) for d = u*32 + lane % 32,
         gathered by two transposing reads of V's natural rows."""
-        if dma and PV_AHEAD:
-            return pv_pipelined(stage, PV_AHEAD)
+        if (PV_AHEAD if dma else PV_AHEAD_STAGED):
+            return pv_pipelined(stage, PV_AHEAD if dma else PV_AHEAD_STAGED)
         if dma:
             rd = "__builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)"
             return ["#pragma unroll", f"for (int ch = 0; ch < {BKV // 16}; ++ch) {{",
                     "#pragma unroll", f"  for (int u = 0; u < {Dv // 32}; ++u) {{",
                     f"    tj_i16x4 v0 = {rd}(Vs{stage} + ch * 4096u + va[u]));",
-                    f"    tj_i16x4 v1 = {rd}(Vs{stage} + ch * 4096u + 2048u + va[u]));",
+                    f"    tj_i16x4 v1 = {rd}(Vs{stage} + ch * 4096u + 2048u + va[u ^ 2]));",
                     f"    const {opvec} vv = __builtin_bit_cast({opvec}, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));",
                     "#pragma unroll",
                     f"    for (int q = 0; q < {QT}; ++q) o[q][u] = {mfma}(vv, pf[q][ch], o[q][u], 0, 0, 0);",
@@ -707,7 +726,9 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
 
         def read(p: int) -> str:
             c, t = divmod(p, BKV // 32)
-            return f"const {opvec} kt{p} = *(const {opvec}*)(Ks{stage} + {t * 32 * 256}u + (kx ^ {c * 32}u));"
+            if dma:
+                return f"const {opvec} kt{p} = *(const {opvec}*)(Ks{stage} + {t * 32 * 256}u + (kx ^ {c * 32}u));"
+            return f"const {opvec} kt{p} = *(const {opvec}*)&Ks[{stage}][{t * 32}u + col][{c * 16}u + g * 8u];"
 
         out = [f"{dst}[0][{t}] = (tj_f32x16)(0.0f);" for t in range(BKV // 32)]
         out.append("{")
@@ -732,8 +753,11 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
 
         def reads(p: int) -> list[str]:
             ch, u = divmod(p, Dv // 32)
-            return [f"const tj_i16x4 vt{p}a = {rd}(Vs{stage} + {ch * 4096}u + va[{u}]));",
-                    f"const tj_i16x4 vt{p}b = {rd}(Vs{stage} + {ch * 4096 + 2048}u + va[{u}]));"]
+            if dma:
+                return [f"const tj_i16x4 vt{p}a = {rd}(Vs{stage} + {ch * 4096}u + va[{u}]));",
+                        f"const tj_i16x4 vt{p}b = {rd}(Vs{stage} + {ch * 4096 + 2048}u + va[{u ^ 2}]));"]
+            return [f"const tj_i16x4 vt{p}{h} = {rd}&Vs[{stage}][{ch * 16 + 8 * i}u + vrow0][{u * 32}u + vcol0]);"
+                    for i, h in enumerate("ab")]
 
         out, sg = ["{"], [f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, {2 * min(ahead, n)}, 0);"]
         for p in range(min(ahead, n)):

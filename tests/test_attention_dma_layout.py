@@ -10,8 +10,12 @@ the block, (b) each score-fragment read returns K row ``t*32 + lane % 32``, chun
 ``2c + lane / 32`` (the 32x32x16 MFMA's operand), (c) each transposing V read returns
 the 8 bytes the padded-row kernel reads (row ``ch*16 + g*4 + (lane % 16)/4`` (+8),
 columns ``u*32 + ((lane/16) % 2)*16 + (lane % 4)*4`` .. +3), (d) the reads are
-conflict-free under the LDS model of the GEMM layout test (16-byte reads served 32
-lanes a pass over 512 bytes of banks; 8-byte reads 64 lanes a pass), and (e) the
+conflict-free under the LDS model of the GEMM layout test for 16-byte reads (32 lanes a
+pass over 512 bytes of banks) and with 16 or 8 lanes a pass over 256 or 128 bytes (the
+padded rows' property) and, for the transposing 8-byte reads, with each half-wave
+over 256 bytes (a V swizzle that was conflict-free only over 512 bytes measured 3.4e7
+conflict cycles per [4,32,2048,128] launch, the padded rows 0) and the whole wave over
+512 bytes, and (e) the
 ping-pong schedule itself -- DMA issues, wait counts and barriers of both wave groups,
 expanded from the source -- never reads a stage before both groups' halves of the
 expected block have landed and been published, and never overwrites one that a group
@@ -182,12 +186,20 @@ def test_fragment_reads_are_bank_conflict_free():
     kreads, _, vreads, _ = _block_reads(src)
     for p, expr in kreads.items():
         a = [_c_eval(expr, env) for env in envs]
-        for h in (0, 1):   # 16-byte reads: 32 lanes a pass over 32 groups of 16 bytes
-            assert len({(x // 16) % 32 for x in a[32 * h:32 * h + 32]}) == 32, (p, h)
+        # 16-byte reads: 32 lanes a pass over 512 bytes of banks, and the padded layout's
+        # stronger property, 16 lanes over 256 bytes and 8 over 128 (a swizzle without it
+        # measured 1.7e7 conflict cycles per [4,32,2048,128] launch, the padded rows 0)
+        for lanes, groups in ((32, 32), (16, 16), (8, 8)):
+            for h in range(64 // lanes):
+                assert len({(x // 16) % groups for x in a[lanes * h:lanes * (h + 1)]}) == lanes, (p, lanes, h)
     for p, pair in vreads.items():
         for h, expr in pair.items():
             a = [_c_eval(expr, env) for env in envs]
-            assert len({(x // 8) % 64 for x in a}) == 64, (p, h)   # 8-byte reads: one pass
+            # transposing 8-byte reads: each half-wave over 256 bytes of banks (the model the
+            # measured conflict counts fit), and the whole wave over 512 bytes
+            for half in (0, 1):
+                assert len({(x // 8) % 32 for x in a[32 * half:32 * half + 32]}) == 32, (p, h, half)
+            assert len({(x // 8) % 64 for x in a}) == 64, (p, h)
 
 
 # ---------------------------------------------------------------------------

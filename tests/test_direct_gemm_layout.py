@@ -15,8 +15,13 @@ zero for the 32x32 layout, one extra pass per read for a 16x16 layout with k-gro
 0 and 1 in chunks c and c+1 (rows r and r ^ 8 collide), zero once they sit in c and
 c+2, and zero for the flash-attention kernel's 272-byte row pitch (32 consecutive
 rows on 32 distinct groups).  Groupings of 16 consecutive lanes, or of 8 + 8 lanes,
-contradict at least one of these readings.  The wait-count immediate is pinned against the assembler's own
-decoding of a compiled kernel."""
+contradict at least one of these readings as the only condition.  The 32-lane condition
+is necessary, not sufficient: the flash kernel's unpadded 256-byte K rows with a swizzle
+that met it but put rows 2k and 2k + 1 of each 16 consecutive lanes on one bank group
+measured 1.7e7 conflict cycles per launch, and 0 once each 16 lanes also spread over 256
+bytes (its own test checks both).  The GEMM layouts here meet that too: with 128-byte
+rows, the rows of one parity among 16 consecutive lanes sit at distinct chunks.  The
+wait-count immediate is pinned against the assembler's own decoding of a compiled kernel."""
 import re
 import shutil
 import subprocess
