@@ -660,6 +660,31 @@ def test_fused_attention_negative_scale(shapes, monkeypatch):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Sk", [40, 64, 100, 128, 192, 256, 300, 448, 520, 1000])
+def test_dma_flash_kernel_equals_the_register_staged_one(Sk, dt, monkeypatch):
+    """Head dim 128 on the ping-pong schedule, 1-16 key blocks, ragged and not: the kernel
+    whose K and V blocks go into LDS by DMA (4 swizzled stages, a peeled tail of up to 7
+    blocks) gives the register-staged kernel's output bit for bit (the same arithmetic in
+    the same order; keys past the end read zeros instead of the last key, and their
+    probabilities are 0 either way), and is within the flash bound of the fp32 oracle."""
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_WAVES", "8")
+    torch.manual_seed(Sk)
+    shapes = [(1, 2, 512, 128), (1, 2, Sk, 128), (1, 2, Sk, 128)]
+    q, k, v = [torch.randn(sh, device=DEV).to(dt) for sh in shapes]
+    print(f"DMA attention Sk={Sk} {dt}", flush=True)
+    f = tj.jit(ATTN)
+    out = f(q, k, v)
+    assert f.compiled(q, k, v).launches[0].meta["schedule"] == "pingpong-dma"
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_DMA", "0")
+    f0 = tj.jit(ATTN)
+    out0 = f0(q, k, v)
+    assert f0.compiled(q, k, v).launches[0].meta["schedule"] == "pingpong"
+    assert torch.equal(out, out0)
+    (ref,) = oracle.run(ATTN, *[t.float().cpu() for t in (q, k, v)])
+    close_lowp(out, ref, tol=2e-2)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shapes,scale,splits", [
     ([(2, 2, 1000, 128)] * 3, 0.088, None),                                   # ragged last block, 8 splits
     ([(1, 1, 4096, 128)] * 3, 0.088, None),                                   # one head, 32 splits
