@@ -686,7 +686,11 @@ def profile_set(torch, dev, steps, which="all") -> None:
     trace of the layer in its own context.  ``c1``: ``steps`` calls of config 1's MLP
     block with direct launches, then ``steps`` with hipGraph replay, back to back (the
     trace's dispatch timestamps show each mode's gaps between kernels).  Each program's
-    source digest is logged, so a counter summary names the kernel source it measured."""
+    source digest is logged, so a counter summary names the kernel source it measured.
+    ``clock``: ``steps`` launches each of config 5's attention and config 4's bf16 GEMM,
+    then the register-only MFMA streams of ``mfma_sustained``; with ``GRBM_COUNT`` (GPU
+    clocks per XCD) over each dispatch's own timestamps it gives the clock each kernel
+    ran at."""
     import tensorjit as tj
 
     def run(fn, fargs):
@@ -695,6 +699,21 @@ def profile_set(torch, dev, steps, which="all") -> None:
             jf(*fargs)
         cp = jf.compiled(*fargs)
         log("profile_source " + json.dumps({"launches": [l.name for l in cp.launches], "sha16": source_sha16(cp)}))
+
+    if which == "clock":
+        gen = torch.Generator(device=dev).manual_seed(0)
+        qkv = [torch.randn(4, 32, 2048, 128, device=dev, generator=gen).bfloat16() for _ in range(3)]
+        run(_fn_attn, qkv)
+        del qkv
+        xg = torch.randn(8192, 8192, device=dev, generator=gen).bfloat16()
+        wg = (0.02 * torch.randn(8192, 8192, device=dev, generator=gen)).bfloat16()
+        bg = (0.02 * torch.randn(8192, device=dev, generator=gen)).bfloat16()
+        run(_fn_gemm, [xg, wg, bg])
+        del xg, wg, bg
+        log(f"mfma streams: {mfma_sustained(torch)}")
+        torch.cuda.synchronize()
+        log(f"profile set clock done ({steps} launches per kernel)")
+        return
 
     if which == "c5":
         os.environ["TENSORJIT_HIP_GRAPH"] = "0"
@@ -761,9 +780,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--quick", action="store_true", help="skip the GEMM / MLP secondaries")
-    ap.add_argument("--profile-set", nargs="?", const="all", choices=["all", "c5", "c1"], default=None,
+    ap.add_argument("--profile-set", nargs="?", const="all", choices=["all", "c5", "c1", "clock"], default=None,
                     help="only launch the kernels used for rocprofv3 runs (no JSON line): 'all' (default) "
-                         "the counter set, 'c5' config 5's whole layer, 'c1' config 1 direct then replayed")
+                         "the counter set, 'c5' config 5's whole layer, 'c1' config 1 direct then replayed, "
+                         "'clock' the MFMA kernels and the register-only MFMA streams (for GRBM_COUNT)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one MI355X); "
