@@ -20,7 +20,11 @@ B operand of ``Oᵀ += Vᵀ·Pᵀ`` without an LDS round trip.  V stays in its n
 ``[key][d]`` layout in LDS; the ``Vᵀ`` operand is gathered with gfx950's
 transposing LDS read ``ds_read_b64_tr_b16`` (within each 16 lanes, lane ``i``
 receives element ``i % 4`` of the 8-byte rows loaded by lanes ``4e + i / 4``,
-e = 0..3), two per fragment, in the key order of the score accumulator.
+e = 0..3), two per fragment, in the key order of the score accumulator.  At head dim
+128 with 8 waves (K/V moved into LDS by DMA) the same data flow runs on 16x16x32
+MFMAs: a wave's 32 queries are two 16-query column tiles, a query's keys of a block
+sit on four lanes (l % 16 + 16 g), and each K or Vᵀ fragment feeds one MFMA of each
+tile.
 
 Grids short of one workgroup per CU (few heads, long keys) split the key range: each
 workgroup runs the same loop over an equal share of the key blocks and stores its
@@ -56,6 +60,40 @@ PV_AHEAD = 2
 KS_AHEAD_STAGED = 2
 PV_AHEAD_STAGED = 2
 SG_MFMA, SG_DS_READ = 0x008, 0x100
+
+# The DMA schedule runs on 16x16x32 MFMAs (TENSORJIT_HIP_ATTENTION_MI16=0 keeps 32x32x16):
+# each wave's 32 queries are two 16-query column tiles, and every K and Vᵀ fragment feeds
+# one MFMA of each, so the LDS reads per FLOP stay those of the 32x32x16 form.  The card is
+# power-limited, and a 16x16x32 stream on random data holds a higher clock (2197 against
+# 1810 MHz for 32x32x16, one box).  Same box, interleaved, best of three, accuracy against
+# fp32 unchanged (relative norm error 2.342e-3 for both): [4,32,2048,128] 247.6 -> 238.0 us,
+# [1,32,2000,128] 65.0 -> 63.2, [1,32,8192,128] 893.6 -> 861.7.  Fragment reads in flight
+# (KS, PV), bit-identical: (2, 2) 238.0 / 860.9 us ([4,32,2048,128] / [1,32,8192,128]),
+# (1, 1) 262.6 / 944.8, (2, 1) 249.0 / 894.1, (2, 3) 237.8 / 859.8, (3, 3) 236.9 / 855.9,
+# (3, 2) 236.6 / 854.1, (4, 4) 236.4 / 853.1 (254 VGPRs).
+KS_AHEAD16 = 3
+PV_AHEAD16 = 2
+QUAD_HELPERS = r"""#ifndef TJ_QUAD_LANES
+#define TJ_QUAD_LANES
+// lanes l, l ^ 16, l ^ 32, l ^ 48 combined: v_permlane16_swap exchanges the odd and even
+// 16-lane rows, v_permlane32_swap the halves; each step combines a pair in either order,
+// so the four lanes end with the same bits
+__device__ __forceinline__ float tj_quad_max(float x) {
+  const unsigned int u = __builtin_bit_cast(unsigned int, x);
+  const auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return tj_pair_max(fmaxf(__builtin_bit_cast(float, (unsigned int)s[0]), __builtin_bit_cast(float, (unsigned int)s[1])));
+}
+__device__ __forceinline__ float tj_quad_sum(float x) {
+  const unsigned int u = __builtin_bit_cast(unsigned int, x);
+  const auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return tj_pair_sum(__builtin_bit_cast(float, (unsigned int)s[0]) + __builtin_bit_cast(float, (unsigned int)s[1]));
+}
+#endif
+"""
+
+
+def mi16_enabled() -> bool:
+    return os.environ.get("TENSORJIT_HIP_ATTENTION_MI16", "1") != "0"
 
 
 # ---------------------------------------------------------------------------
@@ -378,6 +416,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     dma = (pingpong and D == 128 and Dv == 128 and NS == 1
            and os.environ.get("TENSORJIT_HIP_ATTENTION_DMA", "1") != "0"
            and Sk * kst * 2 < 2**31 and Sk * vst * 2 < 2**31)
+    mi16 = dma and mi16_enabled()
+    mfma16 = "__builtin_amdgcn_mfma_f32_16x16x32_bf16" if dt == DType.bf16 else "__builtin_amdgcn_mfma_f32_16x16x32_f16"
     if dma:
         NST = 4
         lds_decl = [f"  __shared__ __attribute__((aligned(1024))) char {a}{s}[{BKV * 256}];"
@@ -404,7 +444,35 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         reads are served a half-wave (32 lanes of 8 bytes) at a time over 256 bytes of
         banks: a swizzle that keeps the 4 rows of a half-wave apart only within 512 bytes,
         f = ((row >> 1) & 3) << 2, measured 3.4e7 bank-conflict cycles per launch at
-        [4,32,2048,128] against 0 for the padded rows."""
+        [4,32,2048,128] against 0 for the padded rows.
+
+        With 16x16x32 MFMAs (``mi16``) the K layout is kept: a fragment read takes K rows
+        16t + lane % 16, chunk 4c + lane / 16, at (4c + g16) ^ r16 ^ (t & 1), and 16 rows
+        of one parity again hold 16 distinct positions per chunk pair.  A transposing Vᵀ
+        read takes rows 32 ch + 16 s + 4 g16 + (lane % 16) / 4 and columns 16 u + 4 (lane % 4)
+        .. +3, i.e. 8 rows x 2 chunks per half-wave and 16 rows per wave, so V is stored
+        with f = h(row) << 1, h = (row & 7) ^ ((row >> 3) & 1): position 2 (u ^ h) + j for
+        chunk 2u + j, distinct over the 8 rows of a half-wave and over the 8 rows of each
+        parity in the wave (the 512-byte model)."""
+        if mi16:
+            vsw = "((((r & 7u) ^ ((r >> 3) & 1u))) << 1)"
+            return ["  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave), gq = wv / 4u;",
+                    f"  const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, {Sk * kst * 2}, 0x00020000);",
+                    f"  const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, {Sk * vst * 2}, 0x00020000);",
+                    "  unsigned int voK[2], voV[2], dmo[2];",
+                    "#pragma unroll",
+                    "  for (int q = 0; q < 2; ++q) {",
+                    "    dmo[q] = (gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u) * 256u;",
+                    "    const unsigned int r = gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u + lane / 16u;",
+                    f"    voK[q] = (r * {kst}u + ((lane % 16u) ^ (r & 15u) ^ ((r >> 4) & 1u)) * 8u) * 2u;",
+                    f"    voV[q] = (r * {vst}u + ((lane % 16u) ^ {vsw}) * 8u) * 2u;",
+                    "  }",
+                    "  const unsigned int kx16 = r16 * 256u + ((g16 ^ r16) << 4);",
+                    "  const unsigned int vr16 = g16 * 4u + (lane % 16u) / 4u, vh16 = (vr16 & 7u) ^ ((vr16 >> 3) & 1u);",
+                    f"  unsigned int va16[{Dv // 16}];",
+                    "#pragma unroll",
+                    f"  for (int u = 0; u < {Dv // 16}; ++u)",
+                    "    va16[u] = vr16 * 256u + (((((unsigned int)u ^ vh16) << 1) | ((lane % 4u) >> 1)) << 4) + (lane % 2u) * 8u;"]
         return ["  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave), gq = wv / 4u;",
                 f"  const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, {Sk * kst * 2}, 0x00020000);",
                 f"  const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, {Sk * vst * 2}, 0x00020000);",
@@ -446,7 +514,27 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
          f"  const {T}* __restrict__ Qb = in0_p + ({qoff});",
          f"  const {T}* __restrict__ Kb = in1_p + ({koff});",
          f"  const {T}* __restrict__ Vb = in2_p + ({voff});",
-         f"  {T}* __restrict__ Ob = out0_p + ({ooff});",
+         f"  {T}* __restrict__ Ob = out0_p + ({ooff});"]
+    if mi16:
+        # 16x16x32: query tile h of this wave is rows qrow0 + h*16 (lane column lane % 16);
+        # Q as the B operand of S^T = K Q^T: chunk c holds Q[row][c*32 + g16*8 .. +8]
+        L += ["  const unsigned int r16 = lane % 16u, g16 = lane / 16u;",
+              f"  const unsigned int qrow0 = qt * {BQ}u + wave * 32u + r16;",
+              f"  {opvec} qf[2][{D // 32}];",
+              f"  tj_f32x4 o[2][{Dv // 16}];",
+              "  float m_run[2], l_run[2];",
+              "#pragma unroll",
+              "  for (int h = 0; h < 2; ++h) {",
+              f"    const unsigned int qc = qrow0 + h * 16u < {Sq}u ? qrow0 + h * 16u : {Sq - 1}u;",
+              "#pragma unroll",
+              f"    for (int c = 0; c < {D // 32}; ++c) qf[h][c] = *(const {opvec}*)&Qb[qc * {qst}u + c * 32 + g16 * 8u];",
+              "#pragma unroll",
+              f"    for (int u = 0; u < {Dv // 16}; ++u) o[h][u] = (tj_f32x4)(0.0f);",
+              "    m_run[h] = -__builtin_inff();",
+              "    l_run[h] = 0.0f;",
+              "  }"]
+    else:
+        L += [
          # query tile q of this wave: rows qrow0 + q*32 .. +31, one per lane column
          f"  const unsigned int qrow0 = qt * {BQ}u + wave * {32 * QT}u + col;",
          # Q as the B operand of S^T = K Q^T: chunk c holds Q[row][c*16 + g*8 .. +8]
@@ -520,6 +608,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
 
     def scores(dst: str, stage: int) -> list[str]:
         """S^T = K Q^T over D in 16-wide chunks: tile t covers keys t*32 .. t*32+31."""
+        if mi16:
+            return scores16(dst, stage, KS_AHEAD16)
         ks_ahead = KS_AHEAD if dma else KS_AHEAD_STAGED if D >= 128 else 0
         if ks_ahead:
             return scores_pipelined(dst, stage, ks_ahead)
@@ -546,6 +636,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         ("fminf", "__builtin_inff()", "__builtin_inff()")
 
     def block_max(sc: str, j: int | None) -> list[str]:
+        if mi16:
+            return block_max16(sc, j)
         mask = None
         if ragged and j == KBL - 1:
             mask = f"{j * BKV}" if NS == 1 else f"(int)kb0 * {BKV} + {j * BKV}"
@@ -577,6 +669,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     def probs(sc: str) -> list[str]:
         """exp2 of the block's scores, the running sums, and the P^T operands (chunk 2t+h)."""
         cvt = ("tj_f2bf2({0}, {1})" if dt == DType.bf16 else "tj_f2h({0}) | (tj_f2h({1}) << 16)")
+        if mi16:
+            return probs16(sc, cvt)
         return ["#pragma unroll", f"for (int q = 0; q < {QT}; ++q) {{",
                 "  float rs = 0.0f;", "#pragma unroll", f"  for (int t = 0; t < {BKV // 32}; ++t)",
                 "#pragma unroll", "    for (int h = 0; h < 2; ++h) {",
@@ -595,6 +689,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         """O^T += V^T P^T.  The V^T fragment of chunk ch holds keys ch*16 + g*4 + 0..3 then
         ch*16 + 8 + g*4 + 0..3 (the score accumulator's order) for d = u*32 + lane % 32,
         gathered by two transposing reads of V's natural rows."""
+        if mi16:
+            return pv16(stage, PV_AHEAD16)
         if (PV_AHEAD if dma else PV_AHEAD_STAGED):
             return pv_pipelined(stage, PV_AHEAD if dma else PV_AHEAD_STAGED)
         if dma:
@@ -772,6 +868,125 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, 2, 0);")
         return out + sg + ["}"]
 
+    # --- 16x16x32 forms (DMA schedule): S[h][t] is the 16 x 16 score tile of keys 16t ..
+    # 16t+15 and queries 16h .. 16h+15 of the wave; lane l holds keys 16t + 4 (l / 16) + i
+    # (i = 0..3) of query column l % 16, so a query's 64 keys of a block sit on lanes
+    # l % 16 + 16 g, g = 0..3, 16 per lane.  P^T chunk ch (keys 32ch .. 32ch+31) is the lane's
+    # own S[h][2ch] and S[h][2ch+1]: MFMA k index 8g + m stands for key 32ch + 16(m / 4) + 4g
+    # + m % 4, and the Vᵀ fragment is read in that key order.
+
+    def scores16(dst: str, stage: int, ahead: int) -> list[str]:
+        """S^T = K Q^T with 16x16x32 MFMAs: the K fragment of (d chunk c, key tile t) feeds
+        both query tiles; the read of fragment p + ``ahead`` is issued after fragment p's
+        two MFMAs (fragments in (c, t) order), pinned by ``sched_group_barrier``."""
+        nt = BKV // 16
+        n = (D // 32) * nt
+
+        def read(p: int) -> str:
+            c, t = divmod(p, nt)
+            return f"const {opvec} kt{p} = *(const {opvec}*)(Ks{stage} + {t * 4096}u + (kx16 ^ {((4 * c) ^ (t & 1)) << 4}u));"
+
+        out = [f"{dst}[{h}][{t}] = (tj_f32x4)(0.0f);" for h in range(2) for t in range(nt)]
+        out.append("{")
+        sg = [f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, {min(ahead, n)}, 0);"]
+        out += [read(p) for p in range(min(ahead, n))]
+        for p in range(n):
+            c, t = divmod(p, nt)
+            out += [f"{dst}[{h}][{t}] = {mfma16}(kt{p}, qf[{h}][{c}], {dst}[{h}][{t}], 0, 0, 0);" for h in range(2)]
+            sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_MFMA}, 2, 0);")
+            if p + ahead < n:
+                out.append(read(p + ahead))
+                sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, 1, 0);")
+        return out + sg + ["}"]
+
+    def block_max16(sc: str, j: int | None) -> list[str]:
+        """The lane's own block extremes (16 keys per query), lazy rescale as in the 32x32
+        form; a rescale combines the four lanes of a query (``tj_quad_max``)."""
+        mask = f"{j * BKV}" if ragged and j == KBL - 1 else None
+        out_l = ["float mb[2];", "bool grow = false;", "#pragma unroll", "for (int h = 0; h < 2; ++h) {",
+                 f"  float mx = {ext_init};", "#pragma unroll", f"  for (int t = 0; t < {BKV // 16}; ++t)",
+                 "#pragma unroll", "    for (int i = 0; i < 4; ++i) {"]
+        if mask is not None:
+            out_l.append(f"      if ({mask} + t * 16 + (int)g16 * 4 + i >= {Sk}) {sc}[h][t][i] = {masked};")
+        out_l += [f"      mx = {ext}(mx, {sc}[h][t][i]);", "    }",
+                  f"  mb[h] = mx * {cs!r}f;",
+                  "  grow = grow || mb[h] > m_run[h] + 8.0f;",
+                  "}",
+                  "if (__builtin_amdgcn_ballot_w64(grow)) {",
+                  "#pragma unroll",
+                  "  for (int h = 0; h < 2; ++h) {",
+                  "    const float m_new = fmaxf(m_run[h], tj_quad_max(mb[h]));",
+                  "    const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);",
+                  "    l_run[h] *= alpha;",
+                  "#pragma unroll",
+                  f"    for (int u = 0; u < {Dv // 16}; ++u) o[h][u] *= alpha;",
+                  "    m_run[h] = m_new;",
+                  "  }",
+                  "}"]
+        return out_l
+
+    def probs16(sc: str, cvt: str) -> list[str]:
+        """exp2 of the block's scores, the running sums, and P^T chunk ch of each query
+        tile from the lane's own S[h][2ch] (k 0..3 of its group) and S[h][2ch+1] (k 4..7)."""
+        return ["#pragma unroll", "for (int h = 0; h < 2; ++h) {",
+                "  float rs = 0.0f;", "#pragma unroll", f"  for (int ch = 0; ch < {BKV // 32}; ++ch) {{",
+                "    tj_u32x4 pw;", "#pragma unroll", "    for (int s = 0; s < 2; ++s)",
+                "#pragma unroll", "      for (int w = 0; w < 2; ++w) {",
+                f"        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[h][2 * ch + s][2 * w], {cs!r}f, -m_run[h]));",
+                f"        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[h][2 * ch + s][2 * w + 1], {cs!r}f, -m_run[h]));",
+                "        rs += e0 + e1;",
+                "        pw[2 * s + w] = " + cvt.format("e0", "e1") + ";",
+                "      }",
+                f"    pf[h][ch] = __builtin_bit_cast({opvec}, pw);",
+                "  }",
+                "  l_run[h] += rs;",
+                "}"]
+
+    def pv16(stage: int, ahead: int) -> list[str]:
+        """O^T += V^T P^T with 16x16x32 MFMAs: the Vᵀ fragment of (key chunk ch, dv tile u)
+        holds dv 16u + lane % 16 and keys 32ch + 4 g16 + 0..3 (first read) then 32ch + 16 +
+        4 g16 + 0..3 (second), and feeds both query tiles; reads of fragment p + ``ahead``
+        after fragment p's MFMAs, fragments in (ch, u) order."""
+        rd = "__builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)"
+        nu = Dv // 16
+        n = (BKV // 32) * nu
+
+        def reads(p: int) -> list[str]:
+            ch, u = divmod(p, nu)
+            return [f"const tj_i16x4 vt{p}a = {rd}(Vs{stage} + {ch * 8192}u + va16[{u}]));",
+                    f"const tj_i16x4 vt{p}b = {rd}(Vs{stage} + {ch * 8192 + 4096}u + va16[{u}]));"]
+
+        out, sg = ["{"], [f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, {2 * min(ahead, n)}, 0);"]
+        for p in range(min(ahead, n)):
+            out += reads(p)
+        for p in range(n):
+            ch, u = divmod(p, nu)
+            out.append(f"const {opvec} vv{p} = __builtin_bit_cast({opvec}, __builtin_shufflevector(vt{p}a, vt{p}b, "
+                       "0, 1, 2, 3, 4, 5, 6, 7));")
+            out += [f"o[{h}][{u}] = {mfma16}(vv{p}, pf[{h}][{ch}], o[{h}][{u}], 0, 0, 0);" for h in range(2)]
+            sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_MFMA}, 2, 0);")
+            if p + ahead < n:
+                out += reads(p + ahead)
+                sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, 2, 0);")
+        return out + sg + ["}"]
+
+    def epilogue16_lines() -> list[str]:
+        # O = O^T / l: lane holds dv 16u + 4 g16 + 0..3 of query 16h + lane % 16
+        return ["#pragma unroll", "  for (int h = 0; h < 2; ++h) {",
+                "    const unsigned int qrow = qrow0 + h * 16u;",
+                "    const float l_tot = tj_quad_sum(l_run[h]);",
+                f"    if (qrow < {Sq}u) {{",
+                "      const float inv = 1.0f / l_tot;",
+                "#pragma unroll",
+                f"      for (int u = 0; u < {Dv // 16}; ++u) {{",
+                "        const unsigned int dv = u * 16 + g16 * 4u;",
+                "        *(unsigned long*)&Ob[qrow * " + f"{ost}u + dv] = "
+                + pack4.format("o[h][u][0] * inv", "o[h][u][1] * inv", "o[h][u][2] * inv", "o[h][u][3] * inv") + ";",
+                "      }",
+                "    }",
+                "  }",
+                "}"]
+
     def phase_end(vm: int | None) -> list[str]:
         """End of a ping-pong phase in the DMA schedule: this wave's fragment reads are done
         and, with ``vm``, all but its ``vm`` youngest DMA loads have landed; then the
@@ -889,17 +1104,21 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 "  }",
                 "}"]
 
-    L += [f"  tj_f32x16 sA[{QT}][{BKV // 32}], sB[{QT}][{BKV // 32}];", f"  {opvec} pf[{QT}][{BKV // 16}];"]
+    if mi16:
+        L += [f"  tj_f32x4 sA[2][{BKV // 16}], sB[2][{BKV // 16}];", f"  {opvec} pf[2][{BKV // 32}];"]
+    else:
+        L += [f"  tj_f32x16 sA[{QT}][{BKV // 32}], sB[{QT}][{BKV // 32}];", f"  {opvec} pf[{QT}][{BKV // 16}];"]
     L += dma_body() if dma else pingpong_body() if pingpong else double_buffer_body()
-    L += epilogue_lines() if NS == 1 else partial_epilogue_lines()
+    L += epilogue16_lines() if mi16 else epilogue_lines() if NS == 1 else partial_epilogue_lines()
     lds = NST * BKV * 256 * 2 if dma else NST * BKV * (DP + VP) * dt.itemsize
     flops = 2.0 * batch * Sq * Sk * (D + Dv)
     meta = {"family": "attention", "dtype": dt.value, "batch": batch, "Sq": Sq, "Sk": Sk, "D": D, "Dv": Dv,
             "scale": scale, "lds_bytes": lds, "flops": flops, "splits": NS,
-            "schedule": "pingpong-dma" if dma else "pingpong" if pingpong else "double-buffer"}
+            "schedule": "pingpong-dma" if dma else "pingpong" if pingpong else "double-buffer",
+            "mfma": "16x16x32" if mi16 else "32x32x16"}
     main = Launch(fname, (nq * batch * NS, 1, 1), (THREADS, 1, 1), 0, meta)
     if NS == 1:
-        return "\n".join(L), main
+        return (QUAD_HELPERS if mi16 else "") + "\n".join(L), main
     meta["workspace"] = (ml_base + NS * batch * Sq * 2) * 4
     meta["ws_arg"] = True
     # combine: one lane per 8 consecutive outputs of a row; weights 2^(m_s - max m) over

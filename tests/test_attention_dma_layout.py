@@ -21,6 +21,7 @@ expanded from the source -- never reads a stage before both groups' halves of th
 expected block have landed and been published, and never overwrites one that a group
 may still read.
 """
+import os
 import re
 
 import pytest
@@ -40,7 +41,20 @@ def _eight_waves(monkeypatch):
     monkeypatch.delenv("TENSORJIT_HIP_ATTENTION_DMA", raising=False)
 
 
-def _source(Sk=2048, Sq=1024, layout="bhsd", H=2):
+def _source(Sk=2048, Sq=1024, layout="bhsd", H=2, mi16=False):
+    """The generated source and launch; ``mi16``: the 16x16x32 form of the schedule."""
+    old = os.environ.get("TENSORJIT_HIP_ATTENTION_MI16")
+    os.environ["TENSORJIT_HIP_ATTENTION_MI16"] = "1" if mi16 else "0"
+    try:
+        return _source_env(Sk, Sq, layout, H, mi16)
+    finally:
+        if old is None:
+            os.environ.pop("TENSORJIT_HIP_ATTENTION_MI16")
+        else:
+            os.environ["TENSORJIT_HIP_ATTENTION_MI16"] = old
+
+
+def _source_env(Sk, Sq, layout, H, mi16):
     fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * 0.088), v)  # noqa: E731
     if layout == "bshd":
         tq = lambda t: tj.transpose(t, 1, 2)  # noqa: E731
@@ -53,6 +67,7 @@ def _source(Sk=2048, Sq=1024, layout="bhsd", H=2):
     src, launches = hb.generate(p)
     (launch,) = launches if isinstance(launches, list) else [launches]
     assert launch.meta["family"] == "attention" and launch.meta["schedule"] == "pingpong-dma", launch.meta
+    assert launch.meta["mfma"] == ("16x16x32" if mi16 else "32x32x16"), launch.meta
     return src, launch
 
 
@@ -312,9 +327,10 @@ def _run_group(events, gq: int):
     return dmas, reads, interval
 
 
+@pytest.mark.parametrize("mi16", [False, True])
 @pytest.mark.parametrize("Sk", [64, 128, 192, 256, 320, 448, 512, 576, 640, 704, 960, 1024, 1100, 2048, 2000])
-def test_schedule_reads_only_published_blocks(Sk):
-    src, _ = _source(Sk=Sk)
+def test_schedule_reads_only_published_blocks(Sk, mi16):
+    src, _ = _source(Sk=Sk, mi16=mi16)
     lines = _body_lines(src)
     # every barrier is preceded by a wait that includes lgkmcnt(0): a group's fragment
     # reads are done before the barrier after which the other group may overwrite them
@@ -384,3 +400,129 @@ def test_dma_schedule_only_for_head_dim_128(monkeypatch):
     p = fuse_attention(C.lower(tj.trace(fn, [TensorType((1, 2, 1024, 128), DType.bf16)] * 3), "hip"))
     _, launches = hb.generate(p)
     assert launches[0].meta["schedule"] == "pingpong"
+
+
+# ---------------------------------------------------------------------------
+# the 16x16x32 form: same DMA schedule, K layout kept, V stored with its own swizzle
+# ---------------------------------------------------------------------------
+
+KMMA16_RE = re.compile(r"(s[AB])\[(\d)\]\[(\d)\] = __builtin_amdgcn_mfma_f32_16x16x32_bf16\(kt(\d+), qf\[(\d)\]\[(\d)\], "
+                       r"(s[AB])\[(\d)\]\[(\d)\]")
+VVEC16_RE = re.compile(r"const tj_bf16x8 vv(\d+) = .*?shufflevector\(vt(\d+)a, vt(\d+)b, 0, 1, 2, 3, 4, 5, 6, 7\)\);")
+VMMA16_RE = re.compile(r"o\[(\d)\]\[(\d)\] = __builtin_amdgcn_mfma_f32_16x16x32_bf16\(vv(\d+), pf\[(\d)\]\[(\d)\], "
+                       r"o\[(\d)\]\[(\d)\]")
+
+
+def _setup16(src: str) -> dict:
+    return {
+        "dmo": _expr(src, r"    dmo\[q\] = (.*);\n"),
+        "r": _expr(src, r"    const unsigned int r = (.*);\n"),
+        "voK": _expr(src, r"    voK\[q\] = (.*);\n"),
+        "voV": _expr(src, r"    voV\[q\] = (.*);\n"),
+        "kx16": _expr(src, r"  const unsigned int kx16 = (.*);\n"),
+        "vr16": _expr(src, r"  const unsigned int vr16 = (.*?), vh16"),
+        "vh16": _expr(src, r", vh16 = (.*);\n"),
+        "va16": _expr(src, r"    va16\[u\] = (.*);\n"),
+    }
+
+
+def _lane_env16(lane: int, e: dict) -> dict:
+    env = dict(_lane_env(lane, 0), r16=lane % 16, g16=lane // 16)
+    for name in ("kx16", "vr16", "vh16"):
+        env[name] = _c_eval(e[name], env)
+    env["va16"] = [_c_eval(e["va16"], dict(env, u=u)) for u in range(8)]
+    return env
+
+
+def _block_reads16(src: str):
+    """K fragment p -> (key tile t, d chunk c), each feeding the MFMAs of both query tiles
+    h = 0, 1 into S[h][t]; Vᵀ fragment p -> (dv tile u, key chunk ch), each feeding
+    O[h][u] of both query tiles with P chunk pf[h][ch]."""
+    blk = src.split("// block")[1]
+    kreads = {int(p): e for p, _, e in KREAD_RE.findall(blk)}
+    vreads = {}
+    for p, h, _, e in VREAD_RE.findall(blk):
+        vreads.setdefault(int(p), {})[h] = e
+    kmma = {}
+    for dst, h, t, p, hq, c, dst2, h2, t2 in KMMA16_RE.findall(blk):
+        assert dst == dst2 and h == hq == h2 and t == t2
+        kmma.setdefault(int(p), set()).add((int(h), int(t), int(c)))
+    vvec = {int(v): int(a) for v, a, b in VVEC16_RE.findall(blk) if a == b}
+    vmma = {}
+    for h, u, v, hp, ch, h2, u2 in VMMA16_RE.findall(blk):
+        assert h == hp == h2 and u == u2
+        vmma.setdefault(vvec[int(v)], set()).add((int(h), int(u), int(ch)))
+    return kreads, kmma, vreads, vmma
+
+
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+def test_dma16_placement_and_fragment_reads_agree(layout):
+    """The 16x16x32 form reads, per lane, the K row and chunk of its MFMA A operand (key
+    16t + lane % 16, d 32c + 8 (lane / 16) .. +7) and, per transposing read, the 8 bytes
+    whose 16-lane transpose gives lane i of group g the keys 32ch + 16s + 4g + 0..3 of
+    dv 16u + i -- the k order of the lane's own probabilities S[h][2ch + s][0..3]."""
+    src, _ = _source(layout=layout, mi16=True)
+    kst = 128 * (2 if layout == "bshd" else 1)
+    e = _setup16(src)
+    kmap, vmap = _dma_map(e, "k", kst), _dma_map(e, "v", kst)
+    kreads, kmma, vreads, vmma = _block_reads16(src)
+    assert sorted(kreads) == sorted(kmma) == list(range(16))
+    assert all(len({(t, c) for _, t, c in v}) == 1 and {h for h, _, _ in v} == {0, 1} for v in kmma.values())
+    assert sorted({(t, c) for v in kmma.values() for _, t, c in v}) == [(t, c) for t in range(4) for c in range(4)]
+    assert sorted(vreads) == sorted(vmma) == list(range(16))
+    assert all(len({(u, ch) for _, u, ch in v}) == 1 and {h for h, _, _ in v} == {0, 1} for v in vmma.values())
+    assert sorted({(u, ch) for v in vmma.values() for _, u, ch in v}) == [(u, ch) for u in range(8) for ch in range(2)]
+    for lane in range(64):
+        env = _lane_env16(lane, e)
+        g16, r16 = lane // 16, lane % 16
+        for p, expr in kreads.items():
+            (_, t, c), = {(0, t, c) for _, t, c in kmma[p]}
+            a = _c_eval(expr, env)
+            assert a % 16 == 0 and a < BKV * 256
+            assert kmap[a // 16] == (16 * t + r16, 4 * c + g16), (lane, p, t, c)
+        for p, pair in vreads.items():
+            (_, u, ch), = {(0, u, ch) for _, u, ch in vmma[p]}
+            for s, h in ((0, "a"), (1, "b")):
+                a = _c_eval(pair[h], env)
+                assert a % 8 == 0 and a + 8 <= BKV * 256
+                row, chunk = vmap[a // 16]
+                want = (32 * ch + 16 * s + 4 * g16 + (lane % 16) // 4, 16 * u + (lane % 4) * 4)
+                assert (row, chunk * 8 + ((a % 16) // 8) * 4) == want, (lane, p, u, ch, s)
+
+
+def test_dma16_fragment_reads_are_bank_conflict_free():
+    src, _ = _source(mi16=True)
+    e = _setup16(src)
+    envs = [_lane_env16(lane, e) for lane in range(64)]
+    kreads, _, vreads, _ = _block_reads16(src)
+    for p, expr in kreads.items():
+        a = [_c_eval(expr, env) for env in envs]
+        for lanes, groups in ((32, 32), (16, 16), (8, 8)):
+            for h in range(64 // lanes):
+                assert len({(x // 16) % groups for x in a[lanes * h:lanes * (h + 1)]}) == lanes, (p, lanes, h)
+    for p, pair in vreads.items():
+        for h, expr in pair.items():
+            a = [_c_eval(expr, env) for env in envs]
+            for half in (0, 1):
+                assert len({(x // 8) % 32 for x in a[32 * half:32 * half + 32]}) == 32, (p, h, half)
+            assert len({(x // 8) % 64 for x in a}) == 64, (p, h)
+
+
+def test_dma16_planted_v_swizzle_mistake_is_caught():
+    """The padded-row-era V swizzle of the 32x32x16 form, planted into the 16x16x32 form's
+    DMA, leaves the reads pointing at other rows: the placement check must fail."""
+    src, _ = _source(mi16=True)
+    e = _setup16(src)
+    e["voV"] = e["voV"].replace("((((r & 7u) ^ ((r >> 3) & 1u))) << 1)", "(((r ^ (r >> 2)) & 3u) << 2)")
+    vmap = _dma_map(e, "v", 128)
+    _, _, vreads, vmma = _block_reads16(src)
+    bad = 0
+    for lane in range(64):
+        env = _lane_env16(lane, e)
+        for p, pair in vreads.items():
+            (_, u, ch), = {(0, u, ch) for _, u, ch in vmma[p]}
+            a = _c_eval(pair["a"], env)
+            row, chunk = vmap[a // 16]
+            bad += (row, chunk * 8 + ((a % 16) // 8) * 4) != (32 * ch + 4 * (lane // 16) + (lane % 16) // 4,
+                                                               16 * u + (lane % 4) * 4)
+    assert bad

@@ -666,8 +666,10 @@ def test_dma_flash_kernel_equals_the_register_staged_one(Sk, dt, monkeypatch):
     whose K and V blocks go into LDS by DMA (4 swizzled stages, a peeled tail of up to 7
     blocks) gives the register-staged kernel's output bit for bit (the same arithmetic in
     the same order; keys past the end read zeros instead of the last key, and their
-    probabilities are 0 either way), and is within the flash bound of the fp32 oracle."""
+    probabilities are 0 either way), and is within the flash bound of the fp32 oracle.
+    Both on 32x32x16 MFMAs (the DMA kernel's 16x16x32 form is checked below)."""
     monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_WAVES", "8")
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_MI16", "0")
     torch.manual_seed(Sk)
     shapes = [(1, 2, 512, 128), (1, 2, Sk, 128), (1, 2, Sk, 128)]
     q, k, v = [torch.randn(sh, device=DEV).to(dt) for sh in shapes]
@@ -682,6 +684,41 @@ def test_dma_flash_kernel_equals_the_register_staged_one(Sk, dt, monkeypatch):
     assert torch.equal(out, out0)
     (ref,) = oracle.run(ATTN, *[t.float().cpu() for t in (q, k, v)])
     close_lowp(out, ref, tol=2e-2)
+
+
+@pytest.mark.parametrize("scale", [0.088, -0.2])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Sk", [40, 64, 100, 192, 300, 520, 1000, 2048])
+def test_dma_flash_kernel_on_16x16x32_mfmas(Sk, dt, scale, monkeypatch):
+    """The DMA kernel's default 16x16x32 form (two 16-query tiles per wave, a query's keys
+    on four lanes, combined over lanes l ^ 16 and l ^ 32 when the reference moves), 1-32
+    key blocks, ragged and not, positive and negative scale: within the flash bound of the
+    fp32 oracle, and close to the 32x32x16 form: one 16-bit rounding step of the output
+    plus 2^-9 of its RMS (the two forms sum in other orders, and since a lane's keys
+    differ between them, the lazy rescale may move the running reference at other
+    blocks, so the probabilities round differently)."""
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_WAVES", "8")
+    torch.manual_seed(1000 + Sk)
+    shapes = [(1, 2, 512, 128), (1, 2, Sk, 128), (1, 2, Sk, 128)]
+    q, k, v = [torch.randn(sh, device=DEV).to(dt) for sh in shapes]
+    fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * scale), v)  # noqa: E731
+    print(f"DMA attention 16x16x32 Sk={Sk} {dt} scale={scale}", flush=True)
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_MI16", "1")
+    f = tj.jit(fn)
+    out = f(q, k, v)
+    meta = f.compiled(q, k, v).launches[0].meta
+    assert meta["schedule"] == "pingpong-dma" and meta["mfma"] == "16x16x32", meta
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_MI16", "0")
+    f32 = tj.jit(fn)
+    out32 = f32(q, k, v)
+    assert f32.compiled(q, k, v).launches[0].meta["mfma"] == "32x32x16"
+    (ref,) = oracle.run(fn, *[t.float().cpu() for t in (q, k, v)])
+    close_lowp(out, ref, tol=2e-2)
+    step = 2.0 ** -7 if dt == torch.bfloat16 else 2.0 ** -10
+    o32 = out32.float()
+    d = (out.float() - o32).abs()
+    bound = step * o32.abs() + 2.0 ** -9 * float(o32.pow(2).mean().sqrt())
+    assert bool((d <= bound).all()), float((d - bound).max())
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
