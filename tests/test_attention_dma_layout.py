@@ -526,3 +526,18 @@ def test_dma16_planted_v_swizzle_mistake_is_caught():
             bad += (row, chunk * 8 + ((a % 16) // 8) * 4) != (32 * ch + 4 * (lane // 16) + (lane % 16) // 4,
                                                                16 * u + (lane % 4) * 4)
     assert bad
+
+
+def test_two_16x16x32_attention_kernels_compile_in_one_module(monkeypatch):
+    """The quad-lane helpers the 16x16x32 form adds are guarded, so a program with two
+    such attention kernels is one valid hipRTC module."""
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_MI16", "1")
+
+    def two(q, k, v):
+        a = tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * 0.088), v)
+        return tj.matmul(tj.softmax(tj.matmul(a, tj.transpose(k, -1, -2)) * 0.088), v)
+
+    p = fuse_attention(C.lower(tj.trace(two, [TensorType((1, 2, 1024, 128), DType.bf16)] * 3), "hip"))
+    src, launches = hb.generate(p)
+    assert [ln.meta["mfma"] for ln in launches] == ["16x16x32", "16x16x32"]
+    assert hb.compile_source(src, "gfx950")
