@@ -837,18 +837,38 @@ def _block_reduce_lines(acc: str, is_max: bool, nwaves: int, slot: int) -> list[
 # viewed as [A, Rd, B] with the reduced axis Rd in the middle: the 64 lanes of a wave own
 # 64 consecutive 16-byte vectors along B, so each row of Rd is a coalesced 1 KiB load per
 # wave; the workgroup's 4 waves take interleaved rows of its slice of Rd and combine their
-# partials through LDS.  Rd is split over S workgroups to reach about 4 x CU_COUNT
-# workgroups (each walking at least COL_MIN_ROWS rows, at most COL_MAX_SPLITS splits);
-# with S > 1 the partials go to the workspace as [S][A*B] and a combine launch adds them
-# in a fixed order and runs the reduction's finish and epilogue: one lane per output, the
-# S partials of 64 outputs spread over up to 16 waves and combined through LDS.
+# partials through LDS.  Rd is split over S workgroups to reach a workgroup count set by
+# the bytes the reduction streams (``col_workgroups_per_cu``; each workgroup walks at least
+# COL_MIN_ROWS rows, at most COL_MAX_SPLITS splits); with S > 1 the partials go to the
+# workspace as [S][A*B] and a combine launch adds them in a fixed order and runs the
+# reduction's finish and epilogue: one lane per output, the S partials of 64 outputs
+# spread over up to 16 waves and combined through LDS.
 COL_WAVES = 4
 COL_MIN_ROWS = 16
 COL_MAX_SPLITS = 512
 
 
-def col_layout(A: int, Rd: int, B: int, vec: int) -> tuple[int, int, int]:
-    """(column blocks per A-slice nb, rows per workgroup RS, splits S) of a column reduction."""
+def col_workgroups_per_cu(streamed_bytes: int) -> int:
+    """Workgroups per CU for a column reduction streaming ``streamed_bytes``.  Measured on
+    MI355X (one box, back-to-back launches, main + combine launch in us at 1 / 2 / 4
+    workgroups per CU): 512 MiB fp32 [32768, 4096] 85.7 / 79.6 / 85.2; 256 MiB fp32
+    [16384, 4096] 39.7 / 42.4 / 46.4, [65536, 1024] 38.5 / 39.9 / 40.8, [32768, 2048]
+    38.6 / 41.1 / 45.9, bf16 [16384, 8192] 40.1 / 42.4 / 47.0, [65536, 2048] 39.5 / 39.7 /
+    40.8; 192 MiB fp32 [12288, 4096] 34.8 / 34.2 / 33.2, [24576, 2048] 40.9 / 31.5 / 32.9;
+    128 MiB bf16 [16384, 4096] 36.3 / 35.1 / 24.9; 64 MiB fp32 [8192, 2048] 20.5 / 14.0 /
+    14.6 (13.5 at 8).  So one per CU for about the MALL's size, two above, four below
+    (inputs that fit the 256 MB MALL stay partly in it between launches and want more
+    loads in flight); the boundaries sit between the measured sizes."""
+    if streamed_bytes >= 448 * 2**20:
+        return 2
+    if streamed_bytes >= 224 * 2**20:
+        return 1
+    return 4
+
+
+def col_layout(A: int, Rd: int, B: int, vec: int, streamed_bytes: int = 0) -> tuple[int, int, int]:
+    """(column blocks per A-slice nb, rows per workgroup RS, splits S) of a column reduction
+    whose inputs stream ``streamed_bytes``."""
     L = -(-B // vec)
     nb = -(-L // 64)
     base = A * nb
@@ -856,7 +876,8 @@ def col_layout(A: int, Rd: int, B: int, vec: int) -> tuple[int, int, int]:
     if forced and forced.isdigit():
         S = max(1, min(int(forced), Rd))
     else:
-        S = max(1, min(-(-4 * CU_COUNT // base), Rd // COL_MIN_ROWS, COL_MAX_SPLITS))
+        wgs = col_workgroups_per_cu(streamed_bytes) * CU_COUNT
+        S = max(1, min(-(-wgs // base), Rd // COL_MIN_ROWS, COL_MAX_SPLITS))
     RS = -(-Rd // S)
     return nb, RS, -(-Rd // RS)
 
@@ -872,7 +893,12 @@ def gen_colreduce(g: KernelGen) -> tuple[str, Launch | list[Launch]]:
     Sx = tuple(X.shape)
     dt = _kernel_dtype(k)
     vec = _vec_for(Sx[-1], A * Rd * B, dt)
-    nb, RS, S = col_layout(A, Rd, B, vec)
+    # inputs read per element of X: the folded elementwise kernel's inputs, or X itself
+    xin = [n for n in k.inputs if n is X or any(n in m.inputs for m in xnodes)]
+    xstr = {id(n): broadcast_strides(n.shape, Sx) for n in xin}
+    streamed = sum(math.prod(n.shape) * n.dtype.itemsize for n in xin if _streamed(Sx, xstr[id(n)]))
+    nt = _nt_loads(streamed)
+    nb, RS, S = col_layout(A, Rd, B, vec, streamed)
     L = -(-B // vec)
     AB = A * B
     idx_t = _index_type(A * Rd * B)
@@ -880,11 +906,6 @@ def gen_colreduce(g: KernelGen) -> tuple[str, Launch | list[Launch]]:
     init = "(-__builtin_inff())" if is_max else "0.0f"
     escaping = {id(o): j for j, o in enumerate(k.outputs)}
     nm = lambda n: g.names[id(n)]  # noqa: E731
-
-    # inputs read per element of X: the folded elementwise kernel's inputs, or X itself
-    xin = [n for n in k.inputs if n is X or any(n in m.inputs for m in xnodes)]
-    xstr = {id(n): broadcast_strides(n.shape, Sx) for n in xin}
-    nt = _nt_loads(sum(math.prod(n.shape) * n.dtype.itemsize for n in xin if _streamed(Sx, xstr[id(n)])))
 
     def fold(acc: str, v: str) -> str:
         return f"{acc} = fmaxf({acc}, {v});" if is_max else f"{acc} += {v};"

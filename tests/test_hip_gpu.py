@@ -353,6 +353,30 @@ def test_column_reductions_vs_oracle(case):
         assert torch.equal(f(xi).double(), xi.double().sum(axis))
 
 
+@pytest.mark.parametrize("shape,dt,splits", [((16384, 4096), torch.float32, 16), ((32768, 4096), torch.float32, 32),
+                                             ((16384, 4096), torch.bfloat16, 128)])
+def test_column_reductions_at_benchmark_sizes(shape, dt, splits):
+    """The split count follows the streamed bytes (one workgroup per CU at 256 MiB, two at
+    512 MiB, four at 128 MiB): each layout against the oracle, and small-integer sums bit
+    for bit against the exact sum."""
+    torch.manual_seed(0)
+    print(f"column reduction {shape} {dt}", flush=True)
+    fn = lambda x: tj.sum(x, axis=0)  # noqa: E731
+    x = torch.randn(shape, device=DEV).to(dt)
+    f = tj.jit(fn)
+    out = f(x)
+    launches = f.compiled(x).launches
+    assert launches[0].meta["family"] == "colreduce" and launches[0].meta["splits"] == splits, launches[0].meta
+    (ref,) = oracle.run(fn, x.float().cpu())
+    if dt == torch.float32:
+        close_f32(out, ref, scale=1e-5 * math.sqrt(shape[0] / 64))
+    else:
+        close_lowp(out, ref)
+    if dt == torch.float32:
+        xi = torch.randint(-3, 4, shape, device=DEV).float()
+        assert torch.equal(f(xi).double(), xi.double().sum(0))
+
+
 def test_column_reduction_matches_the_reference_plan(monkeypatch):
     """The same max and mean with the fold switched off (transpose kernel + row
     reduction): the max bit for bit, the mean to rounding."""
