@@ -496,7 +496,10 @@ def row_shape(N: int, vec: int, streaming_ok: bool, reductions: int = 1, whole_r
 # workgroup per row -> split: [1, 2^26] 4330 -> 39.5 us (6.8 TB/s; torch 47.5),
 # [8, 2^23] 524 -> 39.7, [64, 2^20] 78.9 -> 42.5, [1, 2^20] 29.4 -> 4.2, [8, 2^18]
 # 8.7 -> 4.5; the combine launch costs 2.0 us, so 256 KiB rows lose ([1, 2^16]
-# 3.2 -> 4.4) and [200, 2^16] gains nothing (10.9 -> 10.6).  TENSORJIT_HIP_ROW_SPLIT=0 / 1
+# 3.2 -> 4.4) and [200, 2^16] gains nothing (10.9 -> 10.6).  One workgroup per CU in all:
+# against 2 / 4 / 8 per CU (same box, main + combine launch, us) [1, 2^26] 38.8 against
+# 39.7 / 39.7 / 39.7, [64, 2^20] 39.1 against 39.3 / 41.1 / 40.2, [1, 2^27] 75.5 against
+# 77.0 / 76.4 / 77.3, [1, 2^25] 21.2 against 21.4 / 21.3 / 21.5.  TENSORJIT_HIP_ROW_SPLIT=0 / 1
 # forces the split off / on.
 SPLIT_THREADS = 256
 SPLIT_CHUNKS = 8
@@ -513,12 +516,12 @@ class RowSplit:
 def row_split(nrows: int, N: int, vec: int, itemsize: int) -> RowSplit | None:
     """Split of a single-stage reduction over ``nrows`` rows of ``N`` elements, or None
     when one workgroup per row already fills the chip or a row is short.  About
-    4 x CU_COUNT workgroups in all; segments shrink, down to one chunk per lane, until
+    CU_COUNT workgroups in all; segments shrink, down to one chunk per lane, until
     the row count times the segments per row reaches that."""
     forced = os.environ.get("TENSORJIT_HIP_ROW_SPLIT")
     if forced == "0" or (forced != "1" and (nrows >= CU_COUNT or N * itemsize < SPLIT_MIN_ROW_BYTES)):
         return None
-    target = 4 * CU_COUNT
+    target = CU_COUNT
     per_row = -(-N // (SPLIT_THREADS * vec))
     nch = max(1, min(SPLIT_CHUNKS, per_row * nrows // target))
     segs = -(-per_row // nch)

@@ -448,7 +448,7 @@ def test_row_split_rule_and_index_math(monkeypatch):
 
     assert hk.row_split(CU_COUNT, 1 << 20, 4, 4) is None          # one workgroup per row fills the chip
     assert hk.row_split(8, 32768, 4, 4) is None                  # 128 KiB rows: one workgroup each
-    assert hk.row_split(1, 1 << 26, 4, 4) == hk.RowSplit(8, 8192, 1024)
+    assert hk.row_split(1, 1 << 26, 4, 4) == hk.RowSplit(8, 8192, CU_COUNT)
     assert hk.row_split(1, 65536, 4, 4) is None                  # 256 KiB: the combine launch costs more
     assert hk.row_split(1, 131072, 4, 4) == hk.RowSplit(1, 128, 128)   # short enough for one chunk a segment
     monkeypatch.setenv("TENSORJIT_HIP_ROW_SPLIT", "0")

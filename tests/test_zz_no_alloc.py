@@ -115,7 +115,7 @@ def test_static_arena_run_of_split_row_reductions():
     f = tj.jit(lambda t: (tj.sum(t * t, axis=-1), tj.max(t, axis=-1)))
     gen = torch.Generator(device=DEV).manual_seed(4)
     sizes = []
-    for shape in [(4, 1 << 20), (2, 200000)]:
+    for shape in [(4, 1 << 20), (1, 140000)]:
         x = torch.randn(shape, device=DEV, generator=gen)
         cp = f.compiled(x)
         assert [l.meta["family"] for l in cp.launches] == ["row", "row_combine"] * 2
