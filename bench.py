@@ -679,7 +679,8 @@ def mfma_sustained(torch) -> dict:
 def profile_set(torch, dev, steps, which="all") -> None:
     """Kernels for rocprofv3 runs.  ``all``: the headline kernel, a plain copy-like
     calibration kernel of known traffic (y = x + 0.5, fp32 [16384,4096]: 256 MiB
-    read + 256 MiB written), the row configs, the config-4 bf16 GEMM, its decode
+    read + 256 MiB written), the row configs, the column reduction of fp32 [16384,4096]
+    and the split sum of the same 2^26 values, the config-4 bf16 GEMM, its decode
     shape and its fp32 variant, config 5's bf16 softmax rows and fused attention,
     ``steps`` launches each.
     ``c5``: ``steps`` calls of config 5's whole layer (direct launches), for a kernel
@@ -747,6 +748,10 @@ def profile_set(torch, dev, steps, which="all") -> None:
     s = torch.randn(65536, 2048, device=dev, generator=gen) * 3
     run(_fn_softmax, [s])
     del s
+    xc = torch.randn(16384, 4096, device=dev, generator=gen)
+    run(_fn_sum_axis0, [xc])
+    run(_fn_sum_all, [xc.reshape(-1)])
+    del xc
     xg = torch.randn(8192, 8192, device=dev, generator=gen).bfloat16()
     wg = (0.02 * torch.randn(8192, 8192, device=dev, generator=gen)).bfloat16()
     bg = (0.02 * torch.randn(8192, device=dev, generator=gen)).bfloat16()
