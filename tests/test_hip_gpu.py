@@ -632,8 +632,8 @@ def _mha(x, wq, wk, wv, heads):
     return o.transpose(1, 2).reshape(B, S, Dm)
 
 
-@pytest.mark.parametrize("B,S,Dm,heads,waves", [(2, 200, 128, 2, "4"), (1, 600, 256, 4, "8")],
-                         ids=["4_waves", "pingpong"])
+@pytest.mark.parametrize("B,S,Dm,heads,waves", [(2, 200, 128, 2, "4"), (1, 600, 256, 4, "8"), (1, 600, 512, 4, "8")],
+                         ids=["4_waves", "pingpong", "pingpong_dma_16x16x32"])
 def test_fused_attention_reads_and_writes_head_interleaved_layout(B, S, Dm, heads, waves, monkeypatch):
     """Multi-head attention with the head transposes folded into the flash kernel's
     strided loads and stores (no copy kernels), against the fp32 oracle."""
