@@ -84,7 +84,7 @@ class JitFunction:
 
     def _key(self, args: Sequence[torch.Tensor]) -> tuple:
         dev = args[0].device
-        return (tuple((a.shape, a.dtype) for a in args), dev, pick_backend(dev.type, self.backend))
+        return (tuple([(a.shape, a.dtype) for a in args]), dev, pick_backend(dev.type, self.backend))
 
     def trace(self, *args: torch.Tensor) -> Graph:
         return trace(self.fn, [tensor_type_of(a) for a in args], name=getattr(self.fn, "__name__", "main"))
@@ -94,6 +94,10 @@ class JitFunction:
 
     def compiled(self, *args: torch.Tensor):
         key = self._key(args)
+        cp = self.cache.get(key)        # the common case, without the compile lock
+        if cp is not None:
+            self.stats.hits += 1
+            return cp
         with self._lock:
             cp = self.cache.get(key)
             if cp is not None:
@@ -108,8 +112,11 @@ class JitFunction:
             return cp
 
     def __call__(self, *args: torch.Tensor):
-        if not args or not all(isinstance(a, torch.Tensor) for a in args):
+        if not args:
             raise TypeError("jit functions take torch.Tensor positional arguments only")
+        for a in args:
+            if not isinstance(a, torch.Tensor):
+                raise TypeError("jit functions take torch.Tensor positional arguments only")
         outs = self.compiled(*args)(*args)
         return outs[0] if len(outs) == 1 else tuple(outs)
 

@@ -182,12 +182,25 @@ class NativeHipProgram:
     def run(self, ins: Sequence[int], outs: Sequence[int], stream: int) -> None:
         check(self._lib.tj_hip_program_run(self.handle, *self._tables(ins, outs), stream), "tj_hip_program_run")
 
+    def _tensor_tables(self, ins, outs):
+        """The pointer tables filled straight from tensors (the per-call path)."""
+        if len(ins) != self.n_in or len(outs) != self.n_out:
+            raise HipError(f"expected {self.n_in} input and {self.n_out} output tensors, got {len(ins)} and {len(outs)}")
+        ia, oa = self._in_arr, self._out_arr
+        for i, t in enumerate(ins):
+            ia[i] = t.data_ptr()
+        for j, t in enumerate(outs):
+            oa[j] = t.data_ptr()
+        return ia, oa
+
     def run_tensors(self, ins, outs, stream: int) -> None:
         """``run`` on tensors (their data pointers), the executor's per-call path."""
-        self.run([t.data_ptr() for t in ins], [t.data_ptr() for t in outs], stream)
+        if self._lib.tj_hip_program_run(self.handle, *self._tensor_tables(ins, outs), stream):
+            check(1, "tj_hip_program_run")
 
     def replay_tensors(self, ins, outs, stream: int) -> None:
-        self.replay([t.data_ptr() for t in ins], [t.data_ptr() for t in outs], stream)
+        if self._lib.tj_hip_program_replay(self.handle, *self._tensor_tables(ins, outs), stream):
+            check(1, "tj_hip_program_replay")
 
     def run_static(self, ins: Sequence[int], outs: Sequence[int], stream: int) -> None:
         """``run`` with the intermediates in the library's static per-GPU arena (allocates

@@ -5,13 +5,17 @@ Contract (the reference's ``BufferPool.take_output``,
 reused by a later call only when the caller holds nothing that can still see
 its memory -- no tensor, no view, no storage handle.
 
-Mechanism (this module's own): the pool owns each buffer as a bare
-``UntypedStorage`` and never keeps a tensor of it.  Every call gets a *new*
-tensor built on a free storage with ``Tensor.set_``.  Any tensor or view the
-caller still holds keeps a reference on the storage's C++ object, so a storage
-is free exactly when the pool's handle is its only user: use count 1 on the C++
-side and no Python reference to the handle beyond the pool's own (a caller may
-hold ``out.untyped_storage()``, which is the very same Python object).
+Mechanism (this module's own): the pool owns each buffer as a base tensor of the
+buffer's layout and its ``UntypedStorage`` handle, and never hands out the base
+itself.  Every call gets a *new* tensor on the storage, ``base.detach()`` (its own
+TensorImpl sharing the storage: 0.7 us against 2.4 for an empty tensor re-pointed
+with ``Tensor.set_``).  Any tensor or view the caller still holds -- and anything
+that keeps one alive on the C++ side, such as autograd's saved tensors -- keeps a
+reference on the storage's C++ object, and a caller may hold
+``out.untyped_storage()``, which is the very same Python object as the pool's
+handle.  So a buffer is free exactly when the storage's C++ use count and the
+handle's Python reference count are back at the values measured when the pool
+created it.
 
 On the GPU the point is pointer stability: a program called in a loop whose
 results are dropped each time gets the same output addresses every call,
@@ -27,22 +31,24 @@ _use_count = torch._C._storage_Use_Count
 
 
 class _Buffer:
-    """One pooled storage and the layout it is handed out with."""
+    """One pooled storage, with the base tensor its outputs are detached from."""
 
-    __slots__ = ("storage", "dtype", "device", "shape", "stride")
+    __slots__ = ("base", "storage", "idle_uses", "idle_refs")
 
     def __init__(self, shape: tuple[int, ...], dtype: torch.dtype, device):
-        t = torch.empty(shape, dtype=dtype, device=device)
-        self.storage = t.untyped_storage()
-        self.dtype, self.device, self.shape, self.stride = dtype, t.device, tuple(shape), t.stride()
+        self.base = torch.empty(shape, dtype=dtype, device=device)
+        self.storage = self.base.untyped_storage()
+        # the counts with nothing handed out: the base and the handle on the C++ side;
+        # this attribute, getrefcount's argument and whatever torch itself keeps for a
+        # storage with several C++ owners on the Python side
+        self.idle_uses = _use_count(self.storage._cdata)
+        self.idle_refs = sys.getrefcount(self.storage)
 
     def unused(self) -> bool:
-        # sys.getrefcount sees this attribute and its own argument: 2 means nobody
-        # outside the pool holds the storage handle
-        return _use_count(self.storage._cdata) == 1 and sys.getrefcount(self.storage) == 2
+        return _use_count(self.storage._cdata) == self.idle_uses and sys.getrefcount(self.storage) == self.idle_refs
 
     def tensor(self) -> torch.Tensor:
-        return torch.empty(0, dtype=self.dtype, device=self.device).set_(self.storage, 0, self.shape, self.stride)
+        return self.base.detach()
 
 
 class BufferPool:
@@ -61,7 +67,9 @@ class BufferPool:
         if type(shape) is not tuple:
             shape = tuple(int(d) for d in shape)
         key = (shape, dtype, device)
-        held = self._held.setdefault(key, [])
+        held = self._held.get(key)
+        if held is None:
+            held = self._held[key] = []
         for buf in held:
             if buf.unused():
                 return buf.tensor()

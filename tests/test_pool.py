@@ -34,6 +34,8 @@ def test_anything_the_caller_still_holds_blocks_reuse():
         "detach": lambda t: t.detach(),
         "storage": lambda t: t.untyped_storage(),
         "numpy": lambda t: t.numpy(),
+        # autograd saves the output's TensorImpl (not its Python object) for the backward
+        "autograd": lambda t: t * torch.ones(1, requires_grad=True),
     }
     for name, make in holders.items():
         keep = make(out)
