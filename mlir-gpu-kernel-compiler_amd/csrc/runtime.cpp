@@ -144,8 +144,19 @@ struct Program {
 
   int launch_one(KernelRec& k, hipStream_t stream) {
     const tj_launch& l = k.launch;
+    if (k.values.empty()) {
+      TJ_HIP(hipModuleLaunchKernel(k.fn, l.grid[0], l.grid[1], l.grid[2], l.block[0], l.block[1], l.block[2],
+                                   l.lds_bytes, stream, k.params.data(), nullptr));
+      return 0;
+    }
+    // every kernel argument is a pointer, so values[] already is the packed argument
+    // buffer: handed over whole, HIP copies it instead of walking the kernel's argument
+    // list per parameter
+    size_t bytes = k.values.size() * sizeof(void*);
+    void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, k.values.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &bytes,
+                     HIP_LAUNCH_PARAM_END};
     TJ_HIP(hipModuleLaunchKernel(k.fn, l.grid[0], l.grid[1], l.grid[2], l.block[0], l.block[1], l.block[2],
-                                 l.lds_bytes, stream, k.params.data(), nullptr));
+                                 l.lds_bytes, stream, nullptr, extra));
     return 0;
   }
 
