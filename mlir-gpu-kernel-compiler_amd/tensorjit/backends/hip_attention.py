@@ -454,36 +454,28 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         with f = h(row) << 1, h = (row & 7) ^ ((row >> 3) & 1): position 2 (u ^ h) + j for
         chunk 2u + j, distinct over the 8 rows of a half-wave and over the 8 rows of each
         parity in the wave (the 512-byte model)."""
+        # V's chunk swizzle follows the transposing reads of the MFMA form
+        vsw_row = "((((r & 7u) ^ ((r >> 3) & 1u))) << 1)" if mi16 else "(((r ^ (r >> 2)) & 3u) << 2)"
+        dma_lines_ = ["  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave), gq = wv / 4u;",
+                      f"  const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, {Sk * kst * 2}, 0x00020000);",
+                      f"  const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, {Sk * vst * 2}, 0x00020000);",
+                      "  unsigned int voK[2], voV[2], dmo[2];",
+                      "#pragma unroll",
+                      "  for (int q = 0; q < 2; ++q) {",
+                      "    dmo[q] = (gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u) * 256u;",
+                      "    const unsigned int r = gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u + lane / 16u;",
+                      f"    voK[q] = (r * {kst}u + ((lane % 16u) ^ (r & 15u) ^ ((r >> 4) & 1u)) * 8u) * 2u;",
+                      f"    voV[q] = (r * {vst}u + ((lane % 16u) ^ {vsw_row}) * 8u) * 2u;",
+                      "  }"]
         if mi16:
-            vsw = "((((r & 7u) ^ ((r >> 3) & 1u))) << 1)"
-            return ["  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave), gq = wv / 4u;",
-                    f"  const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, {Sk * kst * 2}, 0x00020000);",
-                    f"  const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, {Sk * vst * 2}, 0x00020000);",
-                    "  unsigned int voK[2], voV[2], dmo[2];",
-                    "#pragma unroll",
-                    "  for (int q = 0; q < 2; ++q) {",
-                    "    dmo[q] = (gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u) * 256u;",
-                    "    const unsigned int r = gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u + lane / 16u;",
-                    f"    voK[q] = (r * {kst}u + ((lane % 16u) ^ (r & 15u) ^ ((r >> 4) & 1u)) * 8u) * 2u;",
-                    f"    voV[q] = (r * {vst}u + ((lane % 16u) ^ {vsw}) * 8u) * 2u;",
-                    "  }",
-                    "  const unsigned int kx16 = r16 * 256u + ((g16 ^ r16) << 4);",
-                    "  const unsigned int vr16 = g16 * 4u + (lane % 16u) / 4u, vh16 = (vr16 & 7u) ^ ((vr16 >> 3) & 1u);",
-                    f"  unsigned int va16[{Dv // 16}];",
-                    "#pragma unroll",
-                    f"  for (int u = 0; u < {Dv // 16}; ++u)",
-                    "    va16[u] = vr16 * 256u + (((((unsigned int)u ^ vh16) << 1) | ((lane % 4u) >> 1)) << 4) + (lane % 2u) * 8u;"]
-        return ["  const unsigned int wv = __builtin_amdgcn_readfirstlane(wave), gq = wv / 4u;",
-                f"  const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, {Sk * kst * 2}, 0x00020000);",
-                f"  const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, {Sk * vst * 2}, 0x00020000);",
-                "  unsigned int voK[2], voV[2], dmo[2];",
+            return dma_lines_ + [
+                "  const unsigned int kx16 = r16 * 256u + ((g16 ^ r16) << 4);",
+                "  const unsigned int vr16 = g16 * 4u + (lane % 16u) / 4u, vh16 = (vr16 & 7u) ^ ((vr16 >> 3) & 1u);",
+                f"  unsigned int va16[{Dv // 16}];",
                 "#pragma unroll",
-                "  for (int q = 0; q < 2; ++q) {",
-                "    dmo[q] = (gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u) * 256u;",
-                "    const unsigned int r = gq * 32u + (wv % 4u) * 8u + (unsigned int)q * 4u + lane / 16u;",
-                f"    voK[q] = (r * {kst}u + ((lane % 16u) ^ (r & 15u) ^ ((r >> 4) & 1u)) * 8u) * 2u;",
-                f"    voV[q] = (r * {vst}u + ((lane % 16u) ^ (((r ^ (r >> 2)) & 3u) << 2)) * 8u) * 2u;",
-                "  }",
+                f"  for (int u = 0; u < {Dv // 16}; ++u)",
+                "    va16[u] = vr16 * 256u + (((((unsigned int)u ^ vh16) << 1) | ((lane % 4u) >> 1)) << 4) + (lane % 2u) * 8u;"]
+        return dma_lines_ + [
                 "  const unsigned int kx = col * 256u + ((g ^ (col & 15u) ^ ((col >> 4) & 1u)) << 4);",
                 "  const unsigned int vr = g * 4u + (lane % 16u) / 4u, vsw = (((lane % 16u) / 4u) ^ g) << 2;",
                 "  const unsigned int vcl = ((lane / 16u) % 2u) * 2u + (lane % 4u) / 2u;",
