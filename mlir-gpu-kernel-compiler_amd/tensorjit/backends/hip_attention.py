@@ -83,6 +83,14 @@ __device__ __forceinline__ float tj_quad_max(float x) {
   const auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
   return tj_pair_max(fmaxf(__builtin_bit_cast(float, (unsigned int)s[0]), __builtin_bit_cast(float, (unsigned int)s[1])));
 }
+typedef _Float16 tj_f16x2q __attribute__((ext_vector_type(2)));
+// sum of the two 16-bit probabilities of a packed pair, added to acc (v_dot2c with ones)
+__device__ __forceinline__ float tj_pair_acc_bf16(unsigned int p, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(tj_bf16x2, p), __builtin_bit_cast(tj_bf16x2, 0x3F803F80u), acc, false);
+}
+__device__ __forceinline__ float tj_pair_acc_f16(unsigned int p, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(tj_f16x2q, p), __builtin_bit_cast(tj_f16x2q, 0x3C003C00u), acc, false);
+}
 __device__ __forceinline__ float tj_quad_sum(float x) {
   const unsigned int u = __builtin_bit_cast(unsigned int, x);
   const auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
@@ -90,6 +98,15 @@ __device__ __forceinline__ float tj_quad_sum(float x) {
 }
 #endif
 """
+
+
+def balance_enabled() -> bool:
+    """16x16x32 DMA kernel: take each block's row sums from the 16-bit probabilities the
+    PV MFMAs use (v_dot2 with ones) and the next block's extremes in the PV phase, instead
+    of fp32 sums and extremes in the softmax phase.  Measured against fp32 reference
+    attention the outputs are closer (the normaliser matches the weights applied: max
+    error 2.8e-3 against 4.9e-3 of the largest output at [4,32,2048,128]); time equal."""
+    return os.environ.get("TENSORJIT_HIP_ATTENTION_BALANCE", "1") != "0"
 
 
 def mi16_enabled() -> bool:
@@ -417,6 +434,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
            and os.environ.get("TENSORJIT_HIP_ATTENTION_DMA", "1") != "0"
            and Sk * kst * 2 < 2**31 and Sk * vst * 2 < 2**31)
     mi16 = dma and mi16_enabled()
+    balanced = mi16 and balance_enabled()
     mfma16 = "__builtin_amdgcn_mfma_f32_16x16x32_bf16" if dt == DType.bf16 else "__builtin_amdgcn_mfma_f32_16x16x32_f16"
     if dma:
         NST = 4
@@ -515,6 +533,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
               f"  {opvec} qf[2][{D // 32}];",
               f"  tj_f32x4 o[2][{Dv // 16}];",
               "  float m_run[2], l_run[2];",
+              *(["  float mbn[2];"] if balanced else []),
               "#pragma unroll",
               "  for (int h = 0; h < 2; ++h) {",
               f"    const unsigned int qc = qrow0 + h * 16u < {Sq}u ? qrow0 + h * 16u : {Sq - 1}u;",
@@ -627,9 +646,9 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     ext, ext_init, masked = ("fmaxf", "-__builtin_inff()", "-__builtin_inff()") if cs > 0 else \
         ("fminf", "__builtin_inff()", "__builtin_inff()")
 
-    def block_max(sc: str, j: int | None) -> list[str]:
+    def block_max(sc: str, j: int | None, pre: bool = False) -> list[str]:
         if mi16:
-            return block_max16(sc, j)
+            return block_max16(sc, j, pre)
         mask = None
         if ragged and j == KBL - 1:
             mask = f"{j * BKV}" if NS == 1 else f"(int)kb0 * {BKV} + {j * BKV}"
@@ -662,7 +681,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         """exp2 of the block's scores, the running sums, and the P^T operands (chunk 2t+h)."""
         cvt = ("tj_f2bf2({0}, {1})" if dt == DType.bf16 else "tj_f2h({0}) | (tj_f2h({1}) << 16)")
         if mi16:
-            return probs16(sc, cvt)
+            return probs16(sc, cvt, not balanced)
         return ["#pragma unroll", f"for (int q = 0; q < {QT}; ++q) {{",
                 "  float rs = 0.0f;", "#pragma unroll", f"  for (int t = 0; t < {BKV // 32}; ++t)",
                 "#pragma unroll", "    for (int h = 0; h < 2; ++h) {",
@@ -677,12 +696,13 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 "  l_run[q] += rs;",
                 "}"]
 
-    def pv(stage: int) -> list[str]:
+    def pv(stage: int, extra: list[str] | None = None) -> list[str]:
         """O^T += V^T P^T.  The V^T fragment of chunk ch holds keys ch*16 + g*4 + 0..3 then
         ch*16 + 8 + g*4 + 0..3 (the score accumulator's order) for d = u*32 + lane % 32,
-        gathered by two transposing reads of V's natural rows."""
+        gathered by two transposing reads of V's natural rows.  ``extra``: independent
+        code of the 16x16x32 form scheduled among the MFMAs."""
         if mi16:
-            return pv16(stage, PV_AHEAD16)
+            return pv16(stage, PV_AHEAD16, extra or [])
         if (PV_AHEAD if dma else PV_AHEAD_STAGED):
             return pv_pipelined(stage, PV_AHEAD if dma else PV_AHEAD_STAGED)
         if dma:
@@ -891,54 +911,71 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
                 sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, 1, 0);")
         return out + sg + ["}"]
 
-    def block_max16(sc: str, j: int | None) -> list[str]:
-        """The lane's own block extremes (16 keys per query), lazy rescale as in the 32x32
-        form; a rescale combines the four lanes of a query (``tj_quad_max``)."""
+    def lane_max16(sc: str, j: int | None, dst: str) -> list[str]:
+        """The lane's own extremes of block ``j``'s scores (16 keys per query tile), scaled
+        into exp2's domain, into ``dst``; keys past Sk in a ragged last block are masked."""
         mask = f"{j * BKV}" if ragged and j == KBL - 1 else None
-        out_l = ["float mb[2];", "bool grow = false;", "#pragma unroll", "for (int h = 0; h < 2; ++h) {",
+        out_l = ["#pragma unroll", "for (int h = 0; h < 2; ++h) {",
                  f"  float mx = {ext_init};", "#pragma unroll", f"  for (int t = 0; t < {BKV // 16}; ++t)",
                  "#pragma unroll", "    for (int i = 0; i < 4; ++i) {"]
         if mask is not None:
             out_l.append(f"      if ({mask} + t * 16 + (int)g16 * 4 + i >= {Sk}) {sc}[h][t][i] = {masked};")
-        out_l += [f"      mx = {ext}(mx, {sc}[h][t][i]);", "    }",
-                  f"  mb[h] = mx * {cs!r}f;",
-                  "  grow = grow || mb[h] > m_run[h] + 8.0f;",
-                  "}",
-                  "if (__builtin_amdgcn_ballot_w64(grow)) {",
-                  "#pragma unroll",
-                  "  for (int h = 0; h < 2; ++h) {",
-                  "    const float m_new = fmaxf(m_run[h], tj_quad_max(mb[h]));",
-                  "    const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);",
-                  "    l_run[h] *= alpha;",
-                  "#pragma unroll",
-                  f"    for (int u = 0; u < {Dv // 16}; ++u) o[h][u] *= alpha;",
-                  "    m_run[h] = m_new;",
-                  "  }",
-                  "}"]
-        return out_l
+        return out_l + [f"      mx = {ext}(mx, {sc}[h][t][i]);", "    }", f"  {dst}[h] = mx * {cs!r}f;", "}"]
 
-    def probs16(sc: str, cvt: str) -> list[str]:
-        """exp2 of the block's scores, the running sums, and P^T chunk ch of each query
-        tile from the lane's own S[h][2ch] (k 0..3 of its group) and S[h][2ch+1] (k 4..7)."""
+    def block_max16(sc: str, j: int | None, pre: bool) -> list[str]:
+        """The lane's own block extremes (16 keys per query), lazy rescale as in the 32x32
+        form; a rescale combines the four lanes of a query (``tj_quad_max``).  With ``pre``
+        the extremes were taken in the previous phase (``mbn``)."""
+        out_l = ["float mb[2];", "bool grow = false;"]
+        out_l += ["mb[0] = mbn[0];", "mb[1] = mbn[1];"] if pre else lane_max16(sc, j, "mb")
+        return out_l + ["#pragma unroll", "for (int h = 0; h < 2; ++h)",
+                        "  grow = grow || mb[h] > m_run[h] + 8.0f;",
+                        "if (__builtin_amdgcn_ballot_w64(grow)) {",
+                        "#pragma unroll",
+                        "  for (int h = 0; h < 2; ++h) {",
+                        "    const float m_new = fmaxf(m_run[h], tj_quad_max(mb[h]));",
+                        "    const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);",
+                        "    l_run[h] *= alpha;",
+                        "#pragma unroll",
+                        f"    for (int u = 0; u < {Dv // 16}; ++u) o[h][u] *= alpha;",
+                        "    m_run[h] = m_new;",
+                        "  }",
+                        "}"]
+
+    def probs16(sc: str, cvt: str, with_sum: bool) -> list[str]:
+        """exp2 of the block's scores, the running sums (``with_sum``), and P^T chunk ch of
+        each query tile from the lane's own S[h][2ch] (k 0..3 of its group) and
+        S[h][2ch+1] (k 4..7)."""
         return ["#pragma unroll", "for (int h = 0; h < 2; ++h) {",
                 "  float rs = 0.0f;", "#pragma unroll", f"  for (int ch = 0; ch < {BKV // 32}; ++ch) {{",
                 "    tj_u32x4 pw;", "#pragma unroll", "    for (int s = 0; s < 2; ++s)",
                 "#pragma unroll", "      for (int w = 0; w < 2; ++w) {",
                 f"        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[h][2 * ch + s][2 * w], {cs!r}f, -m_run[h]));",
                 f"        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf({sc}[h][2 * ch + s][2 * w + 1], {cs!r}f, -m_run[h]));",
-                "        rs += e0 + e1;",
+                *(["        rs += e0 + e1;"] if with_sum else []),
                 "        pw[2 * s + w] = " + cvt.format("e0", "e1") + ";",
                 "      }",
                 f"    pf[h][ch] = __builtin_bit_cast({opvec}, pw);",
                 "  }",
-                "  l_run[h] += rs;",
+                *(["  l_run[h] += rs;"] if with_sum else []),
                 "}"]
 
-    def pv16(stage: int, ahead: int) -> list[str]:
+    def rowsum16() -> list[str]:
+        """The running sums from the 16-bit probabilities the PV MFMAs take (two per
+        v_dot2 with ones), so the sum and the weights of O are the same numbers."""
+        acc = "tj_pair_acc_bf16" if dt == DType.bf16 else "tj_pair_acc_f16"
+        return ["#pragma unroll", "for (int h = 0; h < 2; ++h) {", "  float rs = 0.0f;",
+                "#pragma unroll", f"  for (int ch = 0; ch < {BKV // 32}; ++ch) {{",
+                f"    const tj_u32x4 pw = __builtin_bit_cast(tj_u32x4, pf[h][ch]);",
+                "#pragma unroll", f"    for (int w = 0; w < 4; ++w) rs = {acc}(pw[w], rs);",
+                "  }", "  l_run[h] += rs;", "}"]
+
+    def pv16(stage: int, ahead: int, extra: list[str]) -> list[str]:
         """O^T += V^T P^T with 16x16x32 MFMAs: the Vᵀ fragment of (key chunk ch, dv tile u)
         holds dv 16u + lane % 16 and keys 32ch + 4 g16 + 0..3 (first read) then 32ch + 16 +
         4 g16 + 0..3 (second), and feeds both query tiles; reads of fragment p + ``ahead``
-        after fragment p's MFMAs, fragments in (ch, u) order."""
+        after fragment p's MFMAs, fragments in (ch, u) order.  ``extra`` (code independent
+        of the MFMAs) is placed before the scheduling groups, inside the same region."""
         rd = "__builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tj_i16x4*)"
         nu = Dv // 16
         n = (BKV // 32) * nu
@@ -960,7 +997,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
             if p + ahead < n:
                 out += reads(p + ahead)
                 sg.append(f"__builtin_amdgcn_sched_group_barrier({SG_DS_READ}, 2, 0);")
-        return out + sg + ["}"]
+        return out + extra + sg + ["}"]
 
     def epilogue16_lines() -> list[str]:
         # O = O^T / l: lane holds dv 16u + 4 g16 + 0..3 of query 16h + lane % 16
@@ -1005,7 +1042,7 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         par = (jc if jc >= 0 else s) % 2
         sc, sn = ("sA", "sB") if par == 0 else ("sB", "sA")
         has_next = jc < 0 or jc + 1 < KB
-        out = block_max(sc, jc)
+        out = block_max(sc, jc, balanced)
         if has_next:
             out += scores(sn, (s + 1) % 4)
         out += probs(sc)
@@ -1014,7 +1051,12 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
             out += dma_lines("v", f"{j} + 3u", (s + 3) % 4)
         if jc < 0 or jc + 4 < KB:
             out += dma_lines("k", f"{j} + 4u", s)
-        out += pv(s)
+        extra = []
+        if balanced:
+            # phase B carries part of the softmax: the sums of P(j) and the extremes of
+            # S(j+1), which phase A would otherwise add to its exp2 work
+            extra = rowsum16() + (lane_max16(sn, jc + 1 if jc >= 0 else None, "mbn") if has_next else [])
+        out += pv(s, extra)
         out += phase_end(None)
         return out
 
@@ -1035,6 +1077,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
         out += ["  " + x for x in first]
         out += ["  " + x for x in phase_end(n_dma(-2) + n_dma(-1))]
         out += ["  " + x for x in scores("sA", 0)]
+        if balanced:
+            out += ["  " + x for x in lane_max16("sA", 0, "mbn")]
         out += ["  if (gq == 1u) {"] + ["    " + x for x in phase_end(None)] + ["  }"]
         nquad = max(0, (KB - 4) // 4)
         if nquad:
@@ -1107,7 +1151,8 @@ def gen_attention(k: Kernel, idx: int) -> tuple[str, "Launch"]:  # noqa: F821
     meta = {"family": "attention", "dtype": dt.value, "batch": batch, "Sq": Sq, "Sk": Sk, "D": D, "Dv": Dv,
             "scale": scale, "lds_bytes": lds, "flops": flops, "splits": NS,
             "schedule": "pingpong-dma" if dma else "pingpong" if pingpong else "double-buffer",
-            "mfma": "16x16x32" if mi16 else "32x32x16"}
+            "mfma": "16x16x32" if mi16 else "32x32x16",
+            "row_sums": "16-bit" if balanced else "fp32"}
     main = Launch(fname, (nq * batch * NS, 1, 1), (THREADS, 1, 1), 0, meta)
     if NS == 1:
         return (QUAD_HELPERS if mi16 else "") + "\n".join(L), main

@@ -710,30 +710,34 @@ def test_dma_flash_kernel_equals_the_register_staged_one(Sk, dt, monkeypatch):
     close_lowp(out, ref, tol=2e-2)
 
 
+@pytest.mark.parametrize("balance", ["1", "0"])
 @pytest.mark.parametrize("scale", [0.088, -0.2])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("Sq,Sk", [(512, 40), (512, 64), (512, 100), (512, 192), (512, 300), (512, 520), (512, 1000),
                                    (512, 2048), (600, 333), (1000, 2000)])
-def test_dma_flash_kernel_on_16x16x32_mfmas(Sq, Sk, dt, scale, monkeypatch):
+def test_dma_flash_kernel_on_16x16x32_mfmas(Sq, Sk, dt, scale, balance, monkeypatch):
     """The DMA kernel's default 16x16x32 form (two 16-query tiles per wave, a query's keys
     on four lanes, combined over lanes l ^ 16 and l ^ 32 when the reference moves), 1-32
     key blocks, ragged and not, query counts short of the 256-row tile, positive and
-    negative scale: within the flash bound of the
+    negative scale, row sums from the 16-bit probabilities in the PV phase (default) or in
+    fp32 in the softmax phase: within the flash bound of the
     fp32 oracle, and close to the 32x32x16 form: one 16-bit rounding step of the output
     plus 2^-9 of its RMS (the two forms sum in other orders, and since a lane's keys
     differ between them, the lazy rescale may move the running reference at other
     blocks, so the probabilities round differently)."""
     monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_WAVES", "8")
+    monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_BALANCE", balance)
     torch.manual_seed(1000 + Sk)
     shapes = [(1, 2, Sq, 128), (1, 2, Sk, 128), (1, 2, Sk, 128)]
     q, k, v = [torch.randn(sh, device=DEV).to(dt) for sh in shapes]
     fn = lambda q, k, v: tj.matmul(tj.softmax(tj.matmul(q, tj.transpose(k, -1, -2)) * scale), v)  # noqa: E731
-    print(f"DMA attention 16x16x32 Sq={Sq} Sk={Sk} {dt} scale={scale}", flush=True)
+    print(f"DMA attention 16x16x32 Sq={Sq} Sk={Sk} {dt} scale={scale} balance={balance}", flush=True)
     monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_MI16", "1")
     f = tj.jit(fn)
     out = f(q, k, v)
     meta = f.compiled(q, k, v).launches[0].meta
     assert meta["schedule"] == "pingpong-dma" and meta["mfma"] == "16x16x32", meta
+    assert meta["row_sums"] == ("16-bit" if balance == "1" else "fp32"), meta
     monkeypatch.setenv("TENSORJIT_HIP_ATTENTION_MI16", "0")
     f32 = tj.jit(fn)
     out32 = f32(q, k, v)
