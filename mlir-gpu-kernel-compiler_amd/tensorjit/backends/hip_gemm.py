@@ -30,6 +30,7 @@ gfx950 design:
 from __future__ import annotations
 
 import math
+import os
 
 from ..ir import DType, Node
 from ..runtime.autotune import MatmulConfig
@@ -1578,11 +1579,61 @@ def persistent_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, M, N, B
     return pre_lines, L, stores, len(pre) == len(epi_inputs)
 
 
-def _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW, TNW,
-                   NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname):
+def ksplit_fused_enabled() -> bool:
+    return os.environ.get("TENSORJIT_HIP_KSPLIT_FUSED", "1") != "0"
+
+
+def _ksplit_sum_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, S, bi, i_expr, j_expr,
+                      ve, idx_t, coherent: bool = False) -> list[str]:
+    """out = epilogue(sum of the S partials) for the run of ``ve`` outputs at (i, j): the
+    partials added in split order, as ``gen_ksplit_sum`` and the fused last-workgroup sum
+    both do, so the two forms give the same bits.  ``coherent``: the partials are read
+    through the buffer descriptor ``rsW`` with sc1 (agent-coherent: past this XCD's L2,
+    which may hold no line of them yet but is not kept coherent with the other XCDs)."""
+    L = [f"    const {idx_t} i = {i_expr}, j = {j_expr};",
+         f"    float sm[{ve}];", "#pragma unroll", f"    for (int q = 0; q < {ve}; ++q) sm[q] = 0.0f;",
+         "#pragma unroll", f"    for (int s = 0; s < {S}; ++s) {{"]
+    if coherent:
+        L.append(f"      const unsigned int src = (unsigned int)((({bi} * {S}u + s) * {M}u + i) * {N}u + j) * 4u;")
+        ld4 = "__builtin_bit_cast(tj_f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsW, (int)(src + q4 * 16u), 0, 16))"
+        ld1 = "__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsW, (int)(src + q * 4u), 0, 16))"
+    else:
+        L.append(f"      const float* src = ws_p + (({bi} * {S}u + s) * {M}u + i) * {N}u + j;")
+        ld4, ld1 = "*(const tj_f32x4*)(src + q4 * 4)", "src[q]"
+    if ve % 4 == 0:
+        L += ["#pragma unroll", f"      for (int q4 = 0; q4 < {ve // 4}; ++q4) {{",
+              f"        const tj_f32x4 x = {ld4};",
+              "        sm[q4 * 4] += x[0]; sm[q4 * 4 + 1] += x[1]; sm[q4 * 4 + 2] += x[2]; sm[q4 * 4 + 3] += x[3];",
+              "      }"]
+    else:
+        L.append(f"      for (int q = 0; q < {ve}; ++q) sm[q] += {ld1};")
+    L.append("    }")
+    return L + _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, ve, "sm[q]")
+
+
+def _ksplit_ve(k, N) -> int:
+    out_dt = k.outputs[0].dtype
+    if any(o.dtype.itemsize != out_dt.itemsize for o in k.outputs):
+        return 1
+    return 16 // out_dt.itemsize if N % (16 // out_dt.itemsize) == 0 else 1
+
+
+def _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN, MI, TMW,
+                   TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname):
     """K split over workgroups: each workgroup stores its fp32 partial tile into the
-    workspace ``[batch][KSPLIT][M][N]``; a second launch sums the partials and applies
-    the fused epilogue (``gen_ksplit_sum``)."""
+    workspace ``[batch][KSPLIT][M][N]``.  Fused form (default): the last of a tile's S
+    workgroups to finish sums the tile's partials and applies the epilogue.  Each
+    workgroup writes its partial with agent-scope stores (sc1: through this XCD's L2),
+    waits for them (vmcnt 0), and bumps the tile's counter after a workgroup barrier; the
+    one that reads S - 1 reads the partials with sc1 loads, sums, and resets the counter
+    to 0 for the next call.  (Agent-scope fences instead write back and invalidate the
+    whole L2 of the XCD per workgroup: 112 µs instead of 26 for config 1's
+    down-projection.)  The counters
+    are a zero-initialised ``__device__`` array of the program's code object (zero when
+    it is loaded, zero again after every complete launch), so no memset is needed and a
+    captured graph replays as is; calls of one program that overlap on a GPU race on
+    them as they do on its arena.  Otherwise a second launch sums the partials and
+    applies the fused epilogue (``gen_ksplit_sum``)."""
     S = cfg.KSPLIT
     if MI == 32:
         row_of, col_of = "(r / 4) * 8 + (lane / 32u) * 4 + (r % 4)", "lane % 32u"
@@ -1596,12 +1647,46 @@ def _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M,
     conds = ([f"i < {M}u"] if guard_m else []) + ([f"j < {N}u"] if guard_n else [])
     if conds:
         L.append(f"    if ({' && '.join(conds)})")
-    L += [f"    ws_p[(({bi} * {S}u + ksp) * {M}u + i) * {N}u + j] = acc[x][y][r];", "  }", "}"]
     grid = (-(-N // BN), -(-M // BM), batch * S)
     ws_bytes = batch * S * M * N * 4
+    ve = _ksplit_ve(k, N)
+    fused = ksplit_fused_enabled() and BN % ve == 0 and ws_bytes < 2**31
+    dst = f"ws_p + (({bi} * {S}u + ksp) * {M}u + i) * {N}u + j"
+    # fused: agent-scope stores (sc1, written through to the coherent level) so the last
+    # workgroup, possibly on another XCD, reads them without an L2 write-back / invalidate
+    L += [f"    __hip_atomic_store({dst}, acc[x][y][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);" if fused else
+          f"    *({dst}) = acc[x][y][r];", "  }"]
     meta = {"family": "matmul", "config": cfg.as_dict(), "dtype": dt.value, "M": M, "N": N, "K": K, "batch": batch,
             "trans_b": tb, "lds_bytes": lds_bytes, "flops": 2.0 * M * N * K * batch, "workspace": ws_bytes,
             "ws_arg": True, "epilogue": "k-split partials"}
+    if fused:
+        ntm, ntn = -(-M // BM), -(-N // BN)
+        cnt = f"{fname}_cnt"
+        runs, rpr = BM * BN // ve, BN // ve
+        L += ["  __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0): this lane's partial stores are done",
+              "  __shared__ unsigned int tj_last_;",
+              "  __syncthreads();",
+              f"  const unsigned int ct_ = ({bi} * {ntm}u + m0 / {BM}u) * {ntn}u + n0 / {BN}u;",
+              f"  if (tid == 0u) tj_last_ = atomicAdd(&{cnt}[ct_], 1u) == {S - 1}u ? 1u : 0u;",
+              "  __syncthreads();",
+              "  if (tj_last_ == 0u) return;",
+              f"  const __amdgpu_buffer_rsrc_t rsW = __builtin_amdgcn_make_buffer_rsrc((void*)ws_p, (short)0, {ws_bytes}, 0x00020000);"]
+        if runs % THREADS == 0:
+            # a whole number of runs per lane, unrolled so every partial load is in flight at once
+            L += ["#pragma unroll", f"  for (unsigned int rr = 0; rr < {runs // THREADS}u; ++rr) {{",
+                  f"    const unsigned int run = tid + rr * {THREADS}u;"]
+        else:
+            L.append(f"  for (unsigned int run = tid; run < {runs}u; run += {THREADS}u) {{")
+        conds = ([f"m0 + run / {rpr}u < {M}u"] if guard_m else []) + ([f"n0 + (run % {rpr}u) * {ve}u < {N}u"] if guard_n else [])
+        if conds:
+            L.append(f"    if (!({' && '.join(conds)})) continue;")
+        L += _ksplit_sum_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, S, bi,
+                               f"m0 + run / {rpr}u", f"n0 + (run % {rpr}u) * {ve}u", ve, idx_t, coherent=True)
+        L += ["  }", f"  if (tid == 0u) {cnt}[ct_] = 0u;", "}"]
+        meta = dict(meta, epilogue="k-split, last workgroup sums", fused_sum=True)
+        decl = f"__device__ unsigned int {cnt}[{batch * ntm * ntn}];\n"
+        return decl + "\n".join(L), Launch(fname, grid, (THREADS, 1, 1), 0, meta)
+    L.append("}")
     partial = Launch(fname, grid, (THREADS, 1, 1), 0, meta)
     src2, sum_launch = gen_ksplit_sum(g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, S, fname)
     return "\n".join(L) + "\n\n" + src2, [partial, sum_launch]
@@ -1610,10 +1695,7 @@ def _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M,
 def gen_ksplit_sum(g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, S, fname) -> tuple[str, Launch]:
     """Second launch of a K-split GEMM: out = epilogue(sum over the S partials), one lane
     per run of ``ve`` outputs (16-byte output stores, 16-byte partial loads)."""
-    out_dt = k.outputs[0].dtype
-    ve = 16 // out_dt.itemsize if N % (16 // out_dt.itemsize) == 0 else 1
-    if any(o.dtype.itemsize != out_dt.itemsize for o in k.outputs):
-        ve = 1
+    ve = _ksplit_ve(k, N)
     batch = math.prod(batch_shape) if batch_shape else 1
     runs = batch * M * N // ve
     idx_t = "unsigned long" if batch * M * N >= 2**31 else "unsigned int"
@@ -1621,7 +1703,7 @@ def gen_ksplit_sum(g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N,
     L = [f'extern "C" __global__ __launch_bounds__(256) void {name}({g.params()}, const float* __restrict__ ws_p) {{',
          f"  const {idx_t} t = ({idx_t})blockIdx.x * 256u + threadIdx.x;",
          f"  if (t >= {runs}u) return;",
-         f"  const {idx_t} e = t * {ve}u, bi = e / {M * N}u, rem = e % {M * N}u, i = rem / {N}u, j = rem % {N}u;"]
+         f"  const {idx_t} e = t * {ve}u, bi = e / {M * N}u, rem = e % {M * N}u, i0 = rem / {N}u, j0 = rem % {N}u;"]
     bidx = []
     if batch_shape:
         rem = "bi"
@@ -1633,21 +1715,10 @@ def gen_ksplit_sum(g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N,
                 L.append(f"  const {idx_t} {v} = {rem} / {cst}u, br{d} = {rem} % {cst}u;")
                 rem = f"br{d}"
             bidx.append(v)
-    L.append(f"  float sm[{ve}];")
-    L.append("#pragma unroll")
-    L.append(f"  for (int q = 0; q < {ve}; ++q) sm[q] = 0.0f;")
-    L.append("#pragma unroll")
-    L.append(f"  for (int s = 0; s < {S}; ++s) {{")
-    L.append(f"    const float* src = ws_p + ((bi * {S}u + s) * {M}u + i) * {N}u + j;")
-    if ve % 4 == 0:
-        L += ["#pragma unroll", f"    for (int q4 = 0; q4 < {ve // 4}; ++q4) {{",
-              "      const tj_f32x4 x = *(const tj_f32x4*)(src + q4 * 4);",
-              "      sm[q4 * 4] += x[0]; sm[q4 * 4 + 1] += x[1]; sm[q4 * 4 + 2] += x[2]; sm[q4 * 4 + 3] += x[3];", "    }"]
-    else:
-        L.append(f"    for (int q = 0; q < {ve}; ++q) sm[q] += src[q];")
-    L.append("  }")
-    L += _run_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, ve, "sm[q]")
-    L.append("}")
+    L.append("  {")
+    L += _ksplit_sum_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, S, "bi", "i0", "j0",
+                           ve, idx_t)
+    L += ["  }", "}"]
     meta = {"family": "ksplit_sum", "splits": S, "ws_arg": True, "numel": batch * M * N}
     return "\n".join(L), Launch(name, (-(-runs // 256), 1, 1), (256, 1, 1), 0, meta)
 
@@ -1658,8 +1729,8 @@ def _finish_matmul(L, g, k, mm, epilogue, out_shape, bidx, batch_shape, M, N, K,
     # ---- epilogue on accumulators ------------------------------------------------------
     epi_inputs = epilogue_inputs(k, epilogue)
     if cfg.KSPLIT > 1:
-        return _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, batch_shape, M, N, K, BM, BN, WM, WN, MI,
-                              TMW, TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
+        return _ksplit_finish(L, g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, K, BM, BN, WM, WN,
+                              MI, TMW, TNW, NACC, THREADS, lds_bytes, guard_m, guard_n, idx_t, cfg, dt, tb, batch, fname)
     if cfg.DIRECT:
         staged = direct_staged_epilogue_lines(g, k, mm, epilogue, epi_inputs, out_shape, bidx, batch_shape, M, N, BM,
                                               BN, WM, WN, TMW, TNW, NACC, guard_m, guard_n, idx_t, cfg)

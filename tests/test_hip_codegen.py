@@ -323,10 +323,31 @@ def test_fp32_direct_to_lds_tiles():
     hb.compile_source(src, "gfx950")
 
 
-def test_k_split_gemm_has_a_partial_and_a_sum_launch():
-    """K split over workgroups: the partial-product launch owns a workspace of
-    batch x splits x M x N fp32 values (placed after the planned intermediates in the
-    arena) and both launches take it as their last argument."""
+def test_k_split_gemm_sums_in_its_last_workgroup():
+    """K split over workgroups, default form: one launch owning a workspace of
+    batch x splits x M x N fp32 partials; the last of a tile's workgroups (a counter per
+    output tile in a zero-initialised device array of the code object, reset by that
+    workgroup) sums them: partials written by agent-scope stores and waited for before the
+    counter moves, read back with sc1 (agent-coherent) buffer loads."""
+    fn = lambda x, w, b: tj.gelu(tj.linear(x, w, b))
+    p = C.lower(tj.trace(fn, [TensorType(s, DType.f32) for s in [(512, 3072), (768, 3072), (768,)]]), "hip")
+    cfg = MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 8)
+    src, launches = hb.generate(p, {0: cfg})
+    assert len(launches) == 1 and launches[0].grid == (12, 8, 8) and launches[0].meta["fused_sum"]
+    assert launches[0].meta["workspace"] == 8 * 512 * 768 * 4 and launches[0].meta["ws_arg"]
+    assert f"__device__ unsigned int {launches[0].name}_cnt[96];" in src
+    assert "__hip_atomic_store(ws_p + " in src and "__builtin_amdgcn_s_waitcnt(0x0F70);" in src
+    assert "== 7u ? 1u : 0u" in src and src.count("raw_buffer_load_b128(rsW") == 1 and "__threadfence" not in src
+    assert f"{launches[0].name}_cnt[ct_] = 0u;" in src
+    hb.compile_source(src, "gfx950")
+
+
+def test_k_split_gemm_has_a_partial_and_a_sum_launch(monkeypatch):
+    """K split over workgroups, two-launch form (``TENSORJIT_HIP_KSPLIT_FUSED=0``): the
+    partial-product launch owns a workspace of batch x splits x M x N fp32 values (placed
+    after the planned intermediates in the arena) and both launches take it as their last
+    argument."""
+    monkeypatch.setenv("TENSORJIT_HIP_KSPLIT_FUSED", "0")
     fn = lambda x, w, b: tj.gelu(tj.linear(x, w, b))
     p = C.lower(tj.trace(fn, [TensorType(s, DType.f32) for s in [(512, 3072), (768, 3072), (768,)]]), "hip")
     cfg = MatmulConfig(64, 64, 32, 4, 2, 2, 16, 1, 8, 0, 0, 0, 8)

@@ -1548,7 +1548,7 @@ def test_config4_fp32_full_size_on_its_packaged_tile_vs_oracle():
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_config1_mlp_full_size_vs_oracle(use_graph, monkeypatch):
     """Config 1, the README MLP block at [512, 768] -> 3072 fp32 on its packaged tiles (the
-    down-projection split 8 ways over K), against the oracle at the fp32 bound -- on every
+    down-projection split 4 ways over K), against the oracle at the fp32 bound -- on every
     call, in eager launches and in hipGraph replays."""
     monkeypatch.setenv("TENSORJIT_HIP_GRAPH", "1" if use_graph else "0")
     torch.manual_seed(0)
@@ -1565,7 +1565,7 @@ def test_config1_mlp_full_size_vs_oracle(use_graph, monkeypatch):
         close_f32(out, ref)
     cp = f.compiled(*args)
     assert cp.num_kernels == 3 and cp.stats["graph_replays"] == (3 if use_graph else 0)
-    assert cp.matmul_configs[2].KSPLIT == 8 and len(cp.launches) == 4
+    assert cp.matmul_configs[2].KSPLIT == 4 and len(cp.launches) == 3    # the last workgroup sums
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
@@ -1640,11 +1640,13 @@ def test_bf16_gemm_gelu_epilogue_is_within_its_bound_of_the_exact_gelu():
 
 
 @pytest.mark.parametrize("case", ["f32_residual", "f32_ragged_gelu", "bf16_batched", "skinny_bias_gelu"])
-def test_k_split_gemm_matches_reference(case):
+def test_k_split_gemm_matches_reference(case, monkeypatch):
     """K split over workgroups: fp32 partial tiles in the arena workspace, summed (in a
-    fixed order) by a second launch that applies the fused epilogue; compared with an
-    fp32 reference on three calls of one program (the workspace is reused without
-    clearing), bit-identical."""
+    fixed order) by the last workgroup of each tile (or, for the skinny kernel and with
+    ``TENSORJIT_HIP_KSPLIT_FUSED=0``, by a second launch) that applies the fused epilogue;
+    compared with an fp32 reference on three calls of one program (the workspace is reused
+    without clearing; the tile counters must be back at zero after each call), bit-identical
+    between the calls and between the two forms."""
     from tensorjit.runtime.autotune import MatmulConfig
 
     torch.manual_seed(0)
@@ -1672,6 +1674,8 @@ def test_k_split_gemm_matches_reference(case):
         cfgs = [(16, 64, 256, 8, 1, 1, 16, 8, 0, 0, 0, 0, 4), (16, 32, 256, 8, 1, 1, 16, 8, 0, 0, 0, 0, 2)]
     for vals in cfgs:
         cfg = MatmulConfig(*vals)
+        print(f"k-split {case} {vals}", flush=True)
+        monkeypatch.setenv("TENSORJIT_HIP_KSPLIT_FUSED", "1")
         outs = [o.float() for o in _run_with_config(fn, args, cfg, calls=3)]
         if tol == 1e-5:
             close_f32(outs[0], ref, what=f"{case} {vals}")
@@ -1679,6 +1683,9 @@ def test_k_split_gemm_matches_reference(case):
             close_lowp(outs[0], ref, tol=tol, what=f"{case} {vals}")
         for out in outs[1:]:
             assert torch.equal(out, outs[0]), (case, vals)      # fixed summation order
+        monkeypatch.setenv("TENSORJIT_HIP_KSPLIT_FUSED", "0")
+        two = _run_with_config(fn, args, cfg).float()
+        assert torch.equal(two, outs[0]), (case, vals)         # same order in both forms
 
 
 DIRECT_CFGS = [(256, 256, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1), (256, 128, 64, 4, 2, 2, 32, 1, 8, 0, 0, 1),

@@ -50,9 +50,9 @@ def _both(cp, args):
 
 def test_static_arena_run_matches_the_allocating_run():
     f = tj.jit(_mlp)
-    big = _inputs(512)             # arena: LayerNorm + gelu outputs + 8-way split-K partials
-    cp_big = f.compiled(*big)
-    assert 0 < cp_big.arena_bytes <= rt.STATIC_ARENA_BYTES and len(cp_big.launches) == 4
+    big = _inputs(512)             # arena: LayerNorm + gelu outputs + 4-way split-K partials
+    cp_big = f.compiled(*big)      # (summed by each tile's last workgroup: 3 launches)
+    assert 0 < cp_big.arena_bytes <= rt.STATIC_ARENA_BYTES and len(cp_big.launches) == 3
     small = _inputs(64, seed=1)
     cp_small = f.compiled(*small)
     assert 0 < cp_small.arena_bytes < cp_big.arena_bytes
