@@ -305,7 +305,7 @@ def timed_steps(torch, fn, args, steps, warmup, ramp_s=0.1):
 
 def kernel_ms(f, args, k=None, iters=20):
     """Device time of launch ``k``, or of all the program's launches (``k=None``: a
-    split-K GEMM is one kernel with two launches)."""
+    split-K decode GEMM is one kernel with two launches)."""
     cp = f.compiled(*args)
     ks = range(len(cp.launches)) if k is None else [k]
     return sum(cp.kernel_time_ms(i, *args, warmup=3, iters=iters) for i in ks)

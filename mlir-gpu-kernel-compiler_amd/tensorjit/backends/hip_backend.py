@@ -88,8 +88,9 @@ def reject_zero_size(nodes) -> None:
 
 def generate_kernel(k: Kernel, idx: int, cfg: MatmulConfig | None = None) -> tuple[str, Launch | list[Launch]]:
     """HIP source of one fused kernel and its launch(es).  A GEMM whose K is split
-    across workgroups (``KSPLIT``) has two: partial products into a workspace, then
-    the sum of the partials with the fused epilogue."""
+    across workgroups (``KSPLIT``) writes partial products into a workspace and sums
+    them, with the fused epilogue, in each output tile's last workgroup; the M <= 32
+    decode kernel (and ``TENSORJIT_HIP_KSPLIT_FUSED=0``) sums them in a second launch."""
     reject_zero_size(list(k.inputs) + list(k.nodes) + list(k.outputs))
     g = KernelGen.of(k, idx)
     if k.kind == "elementwise":
@@ -540,7 +541,7 @@ class HipProgram:
                                        [(l.grid, l.block, 0) for l in launches], launch_args(launches, args, ws),
                                        arena, len(ins), len(outs))
             ip, op = [t.data_ptr() for t in ins], [t.data_ptr() for t in outs]
-            # a split-K kernel is timed as the sum of its two launches
+            # a kernel of several launches (the decode split-K and its sum) is timed as their sum
             return lambda warmup, iters: sum(prog.kernel_time(i, ip, op, stream, warmup, iters)
                                              for i in range(len(launches)))
 
@@ -565,7 +566,7 @@ class HipProgram:
 
     @property
     def num_kernels(self) -> int:
-        """Fused kernels of the plan (a split-K GEMM is one kernel with two launches)."""
+        """Fused kernels of the plan (a split-K decode GEMM is one kernel with two launches)."""
         return len(self.program.kernels)
 
     @property

@@ -60,7 +60,7 @@ class MatmulConfig:
     PINGPONG: int = 0       # two wave groups alternate MFMA and memory phases: 1/2 = loads 2/3 K steps ahead, 3 = K-split tiles
     INTERLEAVE: int = 0     # 1: one wave per SIMD, memory instructions threaded between its MFMAs
     DIRECT: int = 0         # 1: one wave per SIMD, tiles loaded straight into LDS (buffer_load_dwordx4 ... lds)
-    KSPLIT: int = 1         # > 1: K split over that many workgroups, partials summed by a second launch
+    KSPLIT: int = 1         # > 1: K split over that many workgroups, partials summed by the last of them
     PERSIST: int = 0        # > 0 (DIRECT only): that many workgroups (one per CU) loop over the output tiles
 
     def as_dict(self) -> dict:
@@ -228,7 +228,8 @@ def _hip_cost(cfg: MatmulConfig, M: int, N: int, K: int, batch: int, elem: int) 
     t_out = M * N * batch * (4 * S if S > 1 else elem) / HBM_BYTES_PER_S / occ
     if cfg.PERSIST and tiles > CU_COUNT:
         t_out *= 0.5
-    # split K: the second launch reads the S fp32 partials, writes the output, and costs a launch
+    # split K: the S fp32 partials are read back and the output written after the last
+    # split finishes (in the tile's last workgroup, ~2.3 us of tail at config 1, or a second launch)
     t_sum = ((S * 4 + elem) * M * N * batch / HBM_BYTES_PER_S + 4e-6) if S > 1 else 0.0
     t = max(t_mfma, t_lds, t_l2, t_hbm) + t_out + t_sum
     return t * 1e6
