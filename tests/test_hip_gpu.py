@@ -1639,7 +1639,8 @@ def test_bf16_gemm_gelu_epilogue_is_within_its_bound_of_the_exact_gelu():
                                         float(exact.reshape(-1)[worst]))
 
 
-@pytest.mark.parametrize("case", ["f32_residual", "f32_ragged_gelu", "bf16_batched", "skinny_bias_gelu"])
+@pytest.mark.parametrize("case", ["f32_residual", "f32_ragged_gelu", "bf16_batched", "f16_ragged_bias_gelu",
+                                  "skinny_bias_gelu"])
 def test_k_split_gemm_matches_reference(case, monkeypatch):
     """K split over workgroups: fp32 partial tiles in the arena workspace, summed (in a
     fixed order) by the last workgroup of each tile (or, for the skinny kernel and with
@@ -1666,6 +1667,12 @@ def test_k_split_gemm_matches_reference(case, monkeypatch):
         fn, args = (lambda p, q: tj.matmul(p, tj.transpose(q, 1, 2))), [a, b]
         ref, tol = a.float() @ b.float().transpose(1, 2).contiguous(), 2e-2
         cfgs = [(64, 64, 64, 4, 2, 2, 16, 1, 8, 0, 0, 0, 4), (128, 128, 32, 4, 2, 2, 32, 1, 8, 0, 0, 0, 2)]
+    elif case == "f16_ragged_bias_gelu":
+        x, w = torch.randn(200, 2048, device=DEV).half(), (0.03 * torch.randn(328, 2048, device=DEV)).half()
+        b = torch.randn(328, device=DEV).half()
+        fn, args = (lambda a, bb, c: tj.gelu(tj.linear(a, bb, c))), [x, w, b]
+        ref, tol = torch.nn.functional.gelu(x.float() @ w.float().t() + b.float()), 2e-2
+        cfgs = [(64, 64, 64, 4, 2, 2, 16, 1, 8, 0, 0, 0, 4), (32, 64, 64, 4, 2, 2, 16, 1, 8, 0, 0, 0, 8)]
     else:
         x, w, b = torch.randn(16, 8192, device=DEV).bfloat16(), (0.02 * torch.randn(4096, 8192, device=DEV)).bfloat16(), \
             torch.randn(4096, device=DEV).bfloat16()
